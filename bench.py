@@ -1,0 +1,222 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X MoE hot path on synthetic Maple-shaped data.
+
+Default (the line the driver records): config 1, decode of 1 token through 24 stacked MoE layers
+(rmsnorm + router + top-8 + grouping + int8 quant + gate/up/SiLU + re-quant + down + combine per layer),
+expert codes resident in HBM. A "step" = one token through the 24 layers; value = tokens/s.
+The same line carries the 2048-token prefill layer with Zipf-skewed routing (config 2) under "prefill".
+
+roofline: the dominant kernel's algorithmic bytes (decode) or int8 ops (prefill) per launch divided by its
+average launch time, measured with HIP events on the library stream in a separate profiling pass.
+cpu_baseline: maple.c's own int8 AVX2 path (oracle/_ref, built from the reference sources) on the host.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [os.path.join(ROOT, "maple-runtime_amd"), os.path.join(ROOT, "oracle")]
+
+import numpy as np  # noqa: E402
+
+import maplemoe as M  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+NL = 24
+SEED = 20261201
+CODES_SCALES_PER_EXPERT = 2 * (262144 + 2048) + (262144 + 8192)   # gate+up, down: 798,720 B
+GU_BYTES_PER_EXPERT = 2 * (262144 + 2048)
+DN_BYTES_PER_EXPERT = 262144 + 8192
+OPS_GU_PER_PAIR = 2 * 1024 * 2048
+OPS_DN_PER_PAIR = 2 * 2048 * 512
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def prof_pass(fn, reps):
+    lib = M.lib()
+    lib.mmoe_prof_reset(); lib.mmoe_prof(1)
+    for _ in range(reps):
+        fn()
+    lib.mmoe_sync(); lib.mmoe_prof(0)
+    out = {}
+    import ctypes as C
+    for k, name in enumerate(M.KERNELS):
+        ms, n = C.c_double(0), C.c_long(0)
+        lib.mmoe_prof_get(k, C.byref(ms), C.byref(n))
+        if n.value:
+            out[name] = (ms.value, n.value)
+    return out
+
+
+def timed(fn, steps, warmup):
+    lib = M.lib()
+    for _ in range(warmup):
+        fn()
+    lib.mmoe_sync()
+    lib.mmoe_event_record(0)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    lib.mmoe_event_record(1)
+    lib.mmoe_sync()
+    t1 = time.perf_counter()
+    ev_ms = lib.mmoe_event_elapsed_ms()
+    return ev_ms / steps, (t1 - t0) * 1e3 / steps
+
+
+def cpu_baseline_decode(blocks, routers, seconds):
+    """maple.c's step() MoE block (oracle/_ref) for 24 layers per token, on the host cores."""
+    import pyoracle as O
+    if not O.ref_available():
+        return None
+    R = O.ref()
+    nt = min(os.cpu_count() or 1, 16)
+    nt = R.ref_set_threads(nt)
+    for L in range(NL):
+        R.ref_set_router(L, O._p(routers[L]))
+        for e in range(M.NE):
+            R.ref_set_expert(L, e, *[O._p(a) for a in M.expert_views(blocks[L], e)])
+    ones = np.full(M.H, 0x3F80, np.uint16)
+    x = M.synth_hidden(SEED, 77, 1)[0].copy()
+    hn = np.empty_like(x)
+
+    def token():
+        for L in range(NL):
+            R.ref_rmsnorm(O._p(x), O._p(ones), M.H, O._p(hn))
+            R.ref_moe_step(L, O._p(hn), O._p(x), None, None, None, None, None)
+    token()  # touch the pages once
+    n, t0 = 0, time.perf_counter()
+    while True:
+        token(); n += 1
+        if time.perf_counter() - t0 >= seconds or n >= 2000:
+            break
+    dt = time.perf_counter() - t0
+    return dict(value=n / dt, unit="tokens/s", cores=nt, kind="reference",
+                sample=f"{n} decode tokens x 24 layers through maple.c's step() MoE block (int8 AVX2, "
+                       f"-O3 -ffast-math -mavx2 -mfma -mf16c, {nt} threads of run()), same synthetic weights")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--graph", type=int, default=1, help="replay the 24-layer decode as a HIP graph")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(json.dumps({"error": "this build measures one GPU only: the MoE path of one MI355X; "
+                                   "multi-GPU sharding is a design note (DESIGN.md), run with --gpus 1"}))
+        sys.exit(2)
+    lib = M.lib()
+    M.check(lib.mmoe_init(2048), "mmoe_init")
+    name, cus, clk = M.device_info()
+    log(f"device {name}, {cus} CUs, {clk / 1e3:.0f} MHz")
+
+    # ---- 24 synthetic layers, codes resident in HBM (config 1: uniform router weights)
+    t = time.perf_counter()
+    blocks, routers = [], []
+    ones = np.full(M.H, 0x3F80, np.uint16)
+    rids = []
+    for L in range(NL):
+        blk = M.synth_layer_block(SEED, L, nthreads=min(os.cpu_count() or 1, 16))
+        rw = M.synth_router(SEED, L, dist=1)
+        rids.append(M.register_layer(L, blk, rw, ones))
+        blocks.append(blk); routers.append(rw)
+    log(f"24 layers generated and resident in HBM in {time.perf_counter() - t:.1f} s")
+
+    x0 = M.synth_hidden(SEED, 1, 1)
+    d_x = lib.mmoe_dev_alloc(x0.nbytes)
+    d_x0 = lib.mmoe_dev_alloc(x0.nbytes)
+    lib.mmoe_h2d(d_x0, M.ptr(x0), x0.nbytes)
+    lib.mmoe_h2d(d_x, M.ptr(x0), x0.nbytes)
+
+    def step_plain():
+        lib.mmoe_d2d(d_x, d_x0, x0.nbytes)
+        M.check(lib.mmoe_stack_dev(0, NL, d_x, 1, M.ORDER_STEP), "stack")
+
+    if args.graph:
+        def step():
+            lib.mmoe_d2d(d_x, d_x0, x0.nbytes)
+            M.check(lib.mmoe_stack_graph(0, NL, d_x, 1, M.ORDER_STEP, 1), "graph")
+    else:
+        step = step_plain
+    ms, wall_ms = timed(step, args.steps, args.warmup)
+    tok_s = 1e3 / ms
+    bytes_tok = NL * 8 * CODES_SCALES_PER_EXPERT
+    log(f"decode: {ms * 1e3:.1f} us/token (wall {wall_ms * 1e3:.1f} us), {tok_s:.0f} tok/s, "
+        f"{bytes_tok / ms / 1e6:.0f} GB/s on codes+scales over the whole step")
+    kt = prof_pass(step_plain, 5)
+    for k, (tot, n) in sorted(kt.items(), key=lambda kv: -kv[1][0]):
+        log(f"  {k:10s} {tot / n * 1e3:8.2f} us avg x {n}")
+    gu_ms = kt["gateup"][0] / kt["gateup"][1]
+    gu_bytes = 8 * GU_BYTES_PER_EXPERT
+    roof = dict(bound="hbm", kernel="k_gateup (decode, 8 experts x 1024 rows)", achieved=round(gu_bytes / gu_ms / 1e6, 1),
+                peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gu_bytes / gu_ms / 1e6 / HBM_PEAK_GBS, 4), traffic=None,
+                algorithmic_bytes_per_launch=gu_bytes, avg_launch_us=round(gu_ms * 1e3, 2),
+                step_gbs=round(bytes_tok / ms / 1e6, 1), step_frac=round(bytes_tok / ms / 1e6 / HBM_PEAK_GBS, 4))
+
+    # ---- config 2: 2048-token prefill, one layer, Zipf(1.1)-skewed routing
+    prefill = None
+    if not args.no_prefill:
+        LP = 40
+        rw = M.synth_router(SEED, 0, dist=0)
+        regs = np.array([rids[0], -1, -1, -1], np.int32)
+        M.check(lib.mmoe_set_layer(LP, M.ptr(M.block_loc()), M.ptr(regs), M.ptr(rw), None), "set_layer")
+        M.check(lib.mmoe_set_bias(LP, M.ptr(M.zipf_bias(SEED, 1.1))), "bias")
+        T = 2048
+        xs = M.synth_hidden(SEED, 2, T)
+        hn = xs / np.sqrt((xs.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6).astype(np.float32)
+        hn = hn.astype(np.float32)
+        d_hn = lib.mmoe_dev_alloc(hn.nbytes); d_xp = lib.mmoe_dev_alloc(hn.nbytes)
+        lib.mmoe_h2d(d_hn, M.ptr(hn), hn.nbytes); lib.mmoe_h2d(d_xp, M.ptr(xs), xs.nbytes)
+
+        def pstep():
+            M.check(lib.mmoe_moe_dev(LP, d_hn, T, d_xp, M.ORDER_BATCH), "moe_dev")
+        pms, pwall = timed(pstep, max(5, args.steps // 5), 2)
+        plan = M.read_plan()
+        cnt = np.diff(plan["ustart"])
+        ops = T * 8 * (OPS_GU_PER_PAIR + OPS_DN_PER_PAIR)
+        log(f"prefill 2048: {pms * 1e3:.1f} us/layer, {T / pms * 1e3:.0f} tok/s, {ops / pms / 1e9:.1f} TOPS "
+            f"({ops / pms / 1e9 / INT8_PEAK_TOPS * 100:.1f}% of int8 MFMA peak); {plan['nu']} experts used, max load {cnt.max()}")
+        pk = prof_pass(pstep, 3)
+        for k, (tot, n) in sorted(pk.items(), key=lambda kv: -kv[1][0]):
+            log(f"  {k:10s} {tot / n * 1e3:8.2f} us avg x {n}")
+        g_ms = pk["gateup"][0] / pk["gateup"][1]
+        g_ops = T * 8 * OPS_GU_PER_PAIR
+        prefill = dict(workload="config 2: 2048-token prefill chunk, 1 MoE layer, Zipf(1.1) expert bias",
+                       value=round(T / pms * 1e3, 1), unit="tokens/s", ms_per_layer=round(pms, 4),
+                       layer_tops=round(ops / pms / 1e9, 1), layer_frac_int8_peak=round(ops / pms / 1e9 / INT8_PEAK_TOPS, 4),
+                       experts_used=plan["nu"], max_expert_load=int(cnt.max()),
+                       roofline=dict(bound="mfma", kernel="k_gateup (grouped int8 MFMA)", achieved=round(g_ops / g_ms / 1e9, 1),
+                                     peak=INT8_PEAK_TOPS, unit="TOPS", frac=round(g_ops / g_ms / 1e9 / INT8_PEAK_TOPS, 4),
+                                     traffic=None, avg_launch_us=round(g_ms * 1e3, 2)),
+                       kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()})
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline_decode(blocks, routers, args.cpu_seconds)
+        if cpu:
+            log(f"cpu baseline: {cpu['value']:.2f} tok/s on {cpu['cores']} threads")
+
+    out = {"metric": "MoE decode tokens/s (1 token x 24 MoE layers); % HBM peak", "value": round(tok_s, 1),
+           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8xternary->int32, fp32",
+           "data": "synthetic (seeded Maple-shaped ternary experts, uniform router, N(0,1) hidden)",
+           "config": {"workload": "config 1: decode 1 token x 24 stacked MoE layers (d=2048, 256 experts, top-8, FF=512)",
+                      "tokens_per_step": 1, "layers": NL, "hip_graph": bool(args.graph), "device": name},
+           "roofline": roof, "cpu_baseline": cpu, "prefill": prefill,
+           "decode_kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in kt.items()}}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

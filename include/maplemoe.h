@@ -1,0 +1,184 @@
+/* maplemoe.h -- C ABI of libmaplemoe, the MI355X (gfx950) MoE hot path for maple-runtime.
+ *
+ * Part 1 declares the entry points maple.c binds when built with -DGPU_HEAD, with maple.c's own signatures
+ * (maple.c:247-272, implemented in the reference by gpu_pre.m, gpu_exp.m and gpu_head.m). A maple.c build
+ * that links libmaplemoe.so instead of the Objective-C/Metal files runs its expert work on the MI355X.
+ * Part 2 declares new mmoe_* entry points that keep the whole MoE layer on the device (router logits,
+ * softmax/top-8, grouping, quantisation, expert products, combine), which maple.c would call in place of its
+ * CPU routing (maple.c:734-755) and expert block (maple.c:824-834).
+ *
+ * Conventions, as in the reference: plain C; int returns are 0 on success and -1 on failure, double
+ * returns are seconds (or -1.0 on failure); messages go to stderr (and mmoe_last_error()); host arrays
+ * stay owned by the caller and are copied; one global context, not thread-safe.
+ * Shapes are fixed by the model: H = 2048, 256 experts, top-8, expert width 512 (maple.c:21-30).
+ */
+#ifndef MAPLEMOE_H
+#define MAPLEMOE_H
+#include <stddef.h>
+#include <stdint.h>
+
+#define MMOE_MAXTOK 2048      /* largest chunk (maple.c:413 BMAX) */
+#define MMOE_MAXREG 64        /* regions (gpu_pre.m:21 MAXREG) */
+#define MMOE_GPUX_MAXTOK 64   /* vectors per gpux call (maple.c:322 MAXSEQ) */
+
+/* ============================ Part 1: maple.c:247-272 ============================ */
+
+/* gpu_head.m: output head. Not part of the MoE path: init returns -1, maple.c keeps its CPU head
+ * (maple.c:1096, 1100). Replaces gpu_head.m's gpu_head_init / _init_i8 / _run / _run_multi. */
+int gpu_head_init(const uint16_t *w, int rows, int cols);
+int gpu_head_init_i8(const int8_t *w, const float *scale, int rows, int cols);
+void gpu_head_run(const float *x, float *y);
+void gpu_head_run_multi(const float *x, int n, float *y);
+
+/* Decode expert cache, replaces gpu_exp.m:155-291 (declared maple.c:251-256).
+ * gpux_init: slots per layer in HBM; 0 / -1.
+ * gpux_upload: one expert's six tensors (reference layout) into slot `slot` of layer L.
+ * gpux_begin: x[2048] (post-norm), n hit experts given by slot -> handle; gpux_end waits and writes
+ *   out[n][2048] = each hit expert's down output (unweighted), computed with maple.c's int8 semantics.
+ * gpux_begin_multi/_end_multi: nb vectors, nu slot experts with pair runs pstart[nu+1] over tokens ptok[]
+ *   -> out[np][2048] per pair. */
+int gpux_init(int layers, int slots);
+void gpux_upload(int L, int slot, const uint8_t *gc, const float *gs, const uint8_t *uc, const float *us,
+                 const uint8_t *dc, const float *ds);
+void *gpux_begin(int L, const float *x, int n, const int *slots);
+void gpux_end(void *h, float *out, int n);
+void *gpux_begin_multi(int L, const float *x, int nb, int nu, const int *slots, const int *pstart, const int *ptok);
+void gpux_end_multi(void *h, float *out, int np);
+
+/* Prompt experts, replaces gpu_pre.m:173-385 (declared maple.c:257-262).
+ * gpre_init(maxtok, topk): work buffers for chunks of up to maxtok (<= 2048) tokens, topk must be 8; 0 / -1.
+ * gpre_region(p, len): page-aligned span of an mmapped shard -> region id (copied once into HBM), or -1.
+ * gpre_moe: synchronous. x[nb][2048] post-norm input; nu used experts; loc[nu][12] = (region slot, byte
+ *   offset) of gate codes, gate scales, up codes, up scales, down codes, down scales (maple.c:276-277);
+ *   regs[4] region ids behind slots 0..3; next: ignored (weights are resident); ustart[nu+1], ptok[P], pw[P]
+ *   the grouping of maple.c:924-938; tp[nb][8] pair ids per token. y[nb][2048] = sum of pw * down over the
+ *   token's pairs (overwritten, not added). Returns device seconds or -1.0.
+ * gpre_stage: no-op (weights are already in HBM), returns 0.
+ * gpre_blit_seconds: seconds spent copying regions into HBM. */
+int gpre_init(int maxtok, int topk);
+int gpre_region(const void *p, size_t len);
+double gpre_moe(const float *x, int nb, int nu, const uint32_t *loc, const int *regs, const int *next,
+                const int *ustart, const int *ptok, const float *pw, const int *tp, float *y);
+int gpre_stage(size_t bytes);
+/* Dense q/k/v/o projections (gpu_pre.m:200-256): not part of the MoE path; gpre_dense_done returns -1 so
+ * maple.c keeps them on the CPU (maple.c:1141). */
+void gpre_dense_add(int g, const uint8_t *codes, const float *scales, int rows, int cols);
+int gpre_dense_done(int maxtok);
+double gpre_dense(int g, const float *x, int nb, float *y);
+double gpre_blit_seconds(void);
+
+/* Whole layer on the card, replaces gpu_pre.m:387-594 (declared maple.c:265-272). Attention is not part of
+ * this build: gfull_init returns -1 and gfull_attn -1.0, so maple.c uses gpre_moe (maple.c:1156-1158).
+ * gfull_begin / gfull_moe / gfull_read / gfull_write_x / gfull_maxtok / gfull_report keep their meaning
+ * on a device hidden state prepared with mmoe_gfull_setup and mmoe_gfull_post_norm (below): gfull_moe is
+ * asynchronous and adds each token's weighted expert outputs into that state; gfull_read waits and copies
+ * it back (*ko is set to NULL: no K/V cache here). */
+int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t *router, const float *cs);
+void gfull_begin(const float *x, int nb, int pos0);
+double gfull_attn(int L, int glob, float *rl);
+void gfull_moe(int nu, const uint32_t *loc, const int *regs, const int *ustart, const int *ptok, const float *pw, const int *tp);
+void gfull_read(float *x, const uint16_t **ko);
+void gfull_write_x(const float *x);
+int gfull_maxtok(void);
+void gfull_report(void);
+
+/* ============================ Part 2: the layer on the device ============================ */
+
+/* Summation orders (maple.c has two router and two combine orders) */
+#define MMOE_ORDER_BATCH 0    /* step_batch: router maple.c:853-889, combine maple.c:834 */
+#define MMOE_ORDER_STEP 1     /* step (one token): router bf_row maple.c:146-157, combine maple.c:664 */
+
+/* Combine modes (flag bits; used internally and by tests): 1 start from x, 2 slot order, 4 add at end */
+#define MMOE_COMBINE_OVERWRITE 0
+#define MMOE_COMBINE_BATCH 1
+#define MMOE_COMBINE_ADD 4
+#define MMOE_COMBINE_STEP 6
+
+/* mmoe_init(maxtok): context and work buffers for up to maxtok (<= 2048) tokens. Same buffers as gpre_init. */
+int mmoe_init(int maxtok);
+/* Layer L's experts (all 256) through maple.c's location table GLOC[L] (loc[256][12], maple.c:276) and
+ * region ids GREG[L] (regs[4]); router[256][2048] bf16 (maple.c:38 Layer.router); post_ln[2048] bf16 or
+ * NULL (used by the stacked path only). The router is copied to HBM. */
+int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *router, const uint16_t *post_ln);
+/* Optional per-expert logit bias[256] added after the router dot (no counterpart in maple.c: it skews
+ * expert loads for the imbalance workload); NULL removes it. */
+int mmoe_set_bias(int L, const float *bias);
+/* The MoE block of step_batch (order BATCH, maple.c:733-834) or step (order STEP, maple.c:605-665) on host
+ * arrays: hn[nb][2048] post-norm input; x[nb][2048] updated in place (x += MoE). Synchronous. */
+int mmoe_moe(int L, const float *hn, int nb, float *x, int order);
+/* The same on device pointers, queued on the library stream (mmoe_stream) without waiting. */
+int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order);
+/* maple.c:398-402 rmsnorm on device pointers; d_w bf16[2048] or NULL (unit weight). */
+int mmoe_rmsnorm_dev(const float *d_x, const uint16_t *d_w, int nb, float *d_out);
+/* nl stacked MoE layers: for L in L0..L0+nl-1: hn = rmsnorm(x, post_ln[L]); x += MoE_L(hn). */
+int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order);
+/* The same captured once into a HIP graph, then replayed `replays` times; mmoe_graph_reset drops it. */
+int mmoe_stack_graph(int L0, int nl, float *d_x, int nb, int order, int replays);
+int mmoe_graph_reset(void);
+/* Router stage of gfull_attn (gpu_full.metal:12-27 rms, 169-209 rtr) on the gfull hidden state:
+ * hn = rmsnorm(x, post_ln[L]), rl[nb][256] = router logits (copied to the host if rl != NULL). */
+int mmoe_gfull_setup(int maxtok);
+int mmoe_gfull_post_norm(int L, float *rl);
+
+/* Intermediate results of the last call on the main context (tests and checks, like GPRE_CHECK) */
+#define MMOE_R_LOGITS 0   /* float [nb][256] */
+#define MMOE_R_TOP 1      /* int [nb][8] */
+#define MMOE_R_TW 2       /* float [nb][8] */
+#define MMOE_R_PLAN 3     /* int nu, np, ntile, tn, ue[256], ustart[257], tstart[257] */
+#define MMOE_R_UTOK 4     /* int [P] */
+#define MMOE_R_UW 5       /* float [P] */
+#define MMOE_R_TP 6       /* int [nb][8] pair ids, ascending */
+#define MMOE_R_SP 7       /* int [nb][8] pair id of each slot */
+#define MMOE_R_QX 8       /* int8 [nb][2048] in mfma order (see kernels.h) */
+#define MMOE_R_QSX 9      /* float [nb] */
+#define MMOE_R_QSUMX 10   /* int [nb] */
+#define MMOE_R_ACT 11     /* float [P][512] */
+#define MMOE_R_QA 12      /* int8 [P][512] in mfma order */
+#define MMOE_R_QSA 13     /* float [P] */
+#define MMOE_R_QSUMA 14   /* int [P] */
+#define MMOE_R_DOWN 15    /* float [P][2048] */
+#define MMOE_R_GU_I32 16  /* int [P][1024] gate then up code*q sums (needs mmoe_set_debug(1)) */
+#define MMOE_R_DN_I32 17  /* int [P][2048] down code*q sums (needs mmoe_set_debug(1)) */
+#define MMOE_R_X 18       /* float [nb][2048] work hidden state */
+#define MMOE_R_HN 19      /* float [nb][2048] work input */
+int mmoe_read(int what, void *dst, size_t bytes);
+int mmoe_set_debug(int on);
+const char *mmoe_last_error(void);
+
+/* Device memory on the library's device, and the library stream */
+void *mmoe_dev_alloc(size_t bytes);
+int mmoe_dev_free(void *p);
+int mmoe_h2d(void *d, const void *h, size_t bytes);
+int mmoe_d2h(void *h, const void *d, size_t bytes);
+int mmoe_d2d(void *d, const void *s, size_t bytes);
+int mmoe_sync(void);
+void *mmoe_stream(void);
+
+/* Timing with HIP events on the library stream: record slot 0 and 1, elapsed ms between them.
+ * mmoe_prof(1) brackets every kernel launch with events and sums the time per kernel id (serialises). */
+#define MMOE_K_RMSNORM 0
+#define MMOE_K_ROUTER 1
+#define MMOE_K_TOPK 2
+#define MMOE_K_GROUP 3
+#define MMOE_K_QUANT 4
+#define MMOE_K_GATEUP 5
+#define MMOE_K_QUANT_ACT 6
+#define MMOE_K_DOWN 7
+#define MMOE_K_COMBINE 8
+#define MMOE_PROF_NKERNELS 9
+int mmoe_event_record(int slot);
+double mmoe_event_elapsed_ms(void);
+int mmoe_prof(int on);
+int mmoe_prof_reset(void);
+int mmoe_prof_get(int kid, double *ms_total, long *count);
+int mmoe_device_info(char *name, int len, int *cus, int *clock_khz);
+
+/* Synthetic Maple-shaped data in the reference layout (see csrc/synth.c) */
+void mmoe_synth_expert(uint64_t seed, int L, int e, uint8_t *gc, float *gs, uint8_t *uc, float *us, uint8_t *dc, float *ds);
+size_t mmoe_synth_expert_bytes(void);
+void mmoe_synth_layer(uint64_t seed, int L, uint8_t *base, int nthreads);
+void mmoe_synth_router(uint64_t seed, int L, int dist, uint16_t *w);
+void mmoe_synth_hidden(uint64_t seed, int sid, int nb, float *x);
+void mmoe_synth_zipf_bias(uint64_t seed, double s, float *bias);
+
+#endif

@@ -1,0 +1,629 @@
+// kernels.h -- gfx950 (CDNA4) kernels of the Maple MoE hot path. Included by mmoe.hip only.
+//
+// Data layouts in HBM (shapes of maple.c:21-30: H = 2048, NE = 256, TOPK = 8, FF = 512):
+//   expert codes      the reference's packed layout, unchanged (convert.py:29-33): rows of cols/4 bytes,
+//                     128-column groups of 32 bytes, byte j holding columns j, j+32, j+64, j+96 at bits
+//                     0,2,4,6, code c = w+1 in {0,1,2}; one fp32 scale per row. Read in place from the
+//                     regions (gpre_region) or expert slots (gpux_upload).
+//   int8 activations  "mfma order": within each 128-column group, column s*32 + h*16 + t*4 + b is stored at
+//                     byte h*64 + t*16 + s*4 + b (s,t,b in 0..3, h in 0..1). Then the 16 bytes one MFMA lane
+//                     needs for one code dword are contiguous (see the gate/up kernel).
+//   pairs             (token, expert) assignments grouped by expert exactly as maple.c:924-938: used experts
+//                     ascending, tokens ascending inside an expert; ustart[u] is the first pair of used expert u.
+//
+// Integer work (quantisation, code*q sums, routing indices, grouping) is exact. Floating-point work follows
+// the fixed IEEE operation sequence of the C oracle: no FMA contraction (-ffp-contract=off), explicit fmaf where
+// maple.c's AVX2 build has an FMA, correctly rounded division and sqrt.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MH 2048
+#define MNE 256
+#define MTOPK 8
+#define MFF 512
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct ExpPtr {  // one expert's six tensors (maple.c:276-277 GLOC order: gate codes/scales, up, down)
+    const uint8_t *gc; const float *gs;
+    const uint8_t *uc; const float *us;
+    const uint8_t *dc; const float *ds;
+};
+
+// Plan of one grouped launch, written on the device by the grouping kernels (or from a host grouping).
+struct Plan {
+    int nu;                 // used experts
+    int np;                 // pairs
+    int ntile_gu;           // token tiles of the gate/up GEMM (sum over u of ceil(cnt_u / TN))
+    int tn;                 // token-tile width the tile starts were computed for
+    int ue[MNE];            // used expert -> expert id
+    int ustart[MNE + 1];    // pair offsets
+    int tstart[MNE + 1];    // token-tile offsets
+};
+
+__device__ __forceinline__ float bf16f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
+
+// exp for fp32 through a fixed fp64 sequence (range reduction by ln2 split in two, Taylor series to r^13 by
+// Horner with FMA, scaling by 2^k), rounded once to fp32. Identical operation-for-operation to the oracle.
+__device__ __forceinline__ float dexp(float xf) {
+    double x = (double)xf;
+    if (x > 100.0) return __int_as_float(0x7f800000);
+    if (x < -110.0) return 0.0f;
+    const double LOG2E = 1.4426950408889634, LN2_HI = 6.93147180369123816490e-01, LN2_LO = 1.90821492927058770002e-10;
+    double k = __builtin_rint(x * LOG2E);
+    double r = __builtin_fma(-k, LN2_HI, x);
+    r = __builtin_fma(-k, LN2_LO, r);
+    double p = 1.0 / 6227020800.0;
+    p = __builtin_fma(p, r, 1.0 / 479001600.0);
+    p = __builtin_fma(p, r, 1.0 / 39916800.0);
+    p = __builtin_fma(p, r, 1.0 / 3628800.0);
+    p = __builtin_fma(p, r, 1.0 / 362880.0);
+    p = __builtin_fma(p, r, 1.0 / 40320.0);
+    p = __builtin_fma(p, r, 1.0 / 5040.0);
+    p = __builtin_fma(p, r, 1.0 / 720.0);
+    p = __builtin_fma(p, r, 1.0 / 120.0);
+    p = __builtin_fma(p, r, 1.0 / 24.0);
+    p = __builtin_fma(p, r, 1.0 / 6.0);
+    p = __builtin_fma(p, r, 0.5);
+    p = __builtin_fma(p, r, 1.0);
+    p = __builtin_fma(p, r, 1.0);
+    double sc = __longlong_as_double((long long)((long long)k + 1023) << 52);
+    return (float)(p * sc);
+}
+
+// ---- wave64 reductions (order-free operations only: max, integer sum) ----
+__device__ __forceinline__ float wave_max(float v) {
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_sum_i(int v) {
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// =====================================================================================================
+// RMSNorm, maple.c:398-402: k = 1 / sqrtf((float)(sum x^2 / n) + 1e-6), out = x * k * w. The sum of squares
+// is in fp64 as in maple.c; each square is exact in fp64, so only the fp64 additions depend on order.
+// One block of 256 threads per row.
+// =====================================================================================================
+__global__ void __launch_bounds__(256) k_rmsnorm(const float *__restrict__ x, const uint16_t *__restrict__ w,
+                                                  float *__restrict__ out, int nb) {
+    __shared__ double red[256];
+    __shared__ float kk;
+    int b = blockIdx.x, t = threadIdx.x;
+    const float *xr = x + (size_t)b * MH;
+    float v[8]; double s = 0.0;
+    for (int i = 0; i < 8; i++) { v[i] = xr[t + i * 256]; s += (double)v[i] * (double)v[i]; }
+    red[t] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) { if (t < o) red[t] += red[t + o]; __syncthreads(); }
+    if (t == 0) kk = 1.0f / sqrtf((float)(red[0] / (double)MH) + 1e-6f);
+    __syncthreads();
+    float k = kk;
+    float *o = out + (size_t)b * MH;
+    for (int i = 0; i < 8; i++) { float wv = w ? bf16f(w[t + i * 256]) : 1.0f; o[t + i * 256] = v[i] * k * wv; }
+}
+
+// =====================================================================================================
+// Router logits, maple.c:853-889 (batch, NCH = 8) and maple.c:146-157 (decode bf_row, NCH = 16).
+// A logit is NCH independent FMA chains: chain j runs over columns j, j+NCH, j+2NCH, ... in order,
+// acc = fma(w, x, acc). Batch: v[j] = chain j; decode: v[j] = chain j + chain j+8. Then
+// ((v0+v4)+(v1+v5)) + ((v2+v6)+(v3+v7)) (maple.c:111-115 hsum). Bias (optional) is added last.
+// =====================================================================================================
+__device__ __forceinline__ float hsum8(const float *v) {
+    float a0 = v[0] + v[4], a1 = v[1] + v[5], a2 = v[2] + v[6], a3 = v[3] + v[7];
+    return (a0 + a1) + (a2 + a3);
+}
+
+// Small batches: one thread per (token, expert, chain). Block 256 = 256/NCH (token, expert) logits.
+template <int NCH>
+__global__ void __launch_bounds__(256) k_router_lanes(const float *__restrict__ hn, int nb, const uint16_t *__restrict__ w,
+                                                       const float *__restrict__ bias, float *__restrict__ rl) {
+    int gid = blockIdx.x * 256 + threadIdx.x;
+    int j = gid % NCH, te = gid / NCH;
+    int e = te % MNE, b = te / MNE;
+    bool on = b < nb;
+    const uint16_t *wr = w + (size_t)e * MH;
+    const float *xr = hn + (size_t)(on ? b : 0) * MH;
+    float acc = 0.0f;
+    if (on)
+        for (int c = j; c < MH; c += NCH) acc = __builtin_fmaf(bf16f(wr[c]), xr[c], acc);
+    float v[NCH];
+    int base = (threadIdx.x & 63) & ~(NCH - 1);  // lanes of one logit are consecutive and inside one wave
+#pragma unroll
+    for (int i = 0; i < NCH; i++) v[i] = __shfl(acc, base + i, 64);
+    if (on && j == 0) {
+        float s[8];
+        if (NCH == 16) { for (int i = 0; i < 8; i++) s[i] = v[i] + v[i + 8]; }
+        else { for (int i = 0; i < 8; i++) s[i] = v[i]; }
+        float r = hsum8(s);
+        if (bias) r = r + bias[e];
+        rl[(size_t)b * MNE + e] = r;
+    }
+}
+
+// Large batches (batch order only): block = 256 experts (one per thread) x RT tokens; the token's
+// activations are wave-uniform (scalar loads), the expert row streams per lane.
+template <int RT>
+__global__ void __launch_bounds__(256) k_router_tiled(const float *__restrict__ hn, int nb, const uint16_t *__restrict__ w,
+                                                       const float *__restrict__ bias, float *__restrict__ rl) {
+    int e = threadIdx.x, b0 = blockIdx.x * RT;
+    const uint16_t *wr = w + (size_t)e * MH;
+    float acc[RT][8];
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+#pragma unroll
+        for (int j = 0; j < 8; j++) acc[t][j] = 0.0f;
+    const float *xb[RT];
+#pragma unroll
+    for (int t = 0; t < RT; t++) xb[t] = hn + (size_t)min(b0 + t, nb - 1) * MH;
+    for (int c = 0; c < MH; c += 8) {
+        uint4 wv = *(const uint4 *)(wr + c);
+        float wf[8] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u), __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u),
+                       __uint_as_float(wv.z << 16), __uint_as_float(wv.z & 0xffff0000u), __uint_as_float(wv.w << 16), __uint_as_float(wv.w & 0xffff0000u)};
+#pragma unroll
+        for (int t = 0; t < RT; t++) {
+            float4 x0 = *(const float4 *)(xb[t] + c), x1 = *(const float4 *)(xb[t] + c + 4);
+            acc[t][0] = __builtin_fmaf(wf[0], x0.x, acc[t][0]); acc[t][1] = __builtin_fmaf(wf[1], x0.y, acc[t][1]);
+            acc[t][2] = __builtin_fmaf(wf[2], x0.z, acc[t][2]); acc[t][3] = __builtin_fmaf(wf[3], x0.w, acc[t][3]);
+            acc[t][4] = __builtin_fmaf(wf[4], x1.x, acc[t][4]); acc[t][5] = __builtin_fmaf(wf[5], x1.y, acc[t][5]);
+            acc[t][6] = __builtin_fmaf(wf[6], x1.z, acc[t][6]); acc[t][7] = __builtin_fmaf(wf[7], x1.w, acc[t][7]);
+        }
+    }
+    float bv = bias ? bias[e] : 0.0f;
+#pragma unroll
+    for (int t = 0; t < RT; t++)
+        if (b0 + t < nb) {
+            float r = hsum8(acc[t]);
+            if (bias) r = r + bv;
+            rl[(size_t)(b0 + t) * MNE + e] = r;
+        }
+}
+
+// =====================================================================================================
+// Softmax + top-8 + renormalisation, maple.c:910-923. One wave per token; lane l holds experts l, l+64,
+// l+128, l+192. Probabilities: p_e = exp(l_e - max) / sum, the sum taken as 8 interleaved partial sums
+// (lane j: experts j, j+8, ... in order) folded by hsum8 -- the same order the oracle uses. Top-8: 8 rounds
+// of argmax on p with the lowest index winning ties (maple.c's strict >), picked entries set to -1; weights
+// p / (sum of picked, in pick order, + 1e-20). Also writes slot -> expert (top) and weight (tw).
+// =====================================================================================================
+__global__ void __launch_bounds__(256) k_topk(const float *__restrict__ rl, int nb, int *__restrict__ top, float *__restrict__ tw) {
+    __shared__ float E[4][MNE];
+    int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    int b = blockIdx.x * 4 + wv;
+    if (b >= nb) return;  // whole wave exits together
+    const float *r = rl + (size_t)b * MNE;
+    float lg[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) lg[i] = r[l + 64 * i];
+    float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
+    mx = wave_max(mx);
+    mx = fmaxf(mx, -1e30f);  // maple.c starts its max at -1e30
+#pragma unroll
+    for (int i = 0; i < 4; i++) { lg[i] = dexp(lg[i] - mx); E[wv][l + 64 * i] = lg[i]; }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    float part = 0.0f;
+    if (l < 8)
+        for (int e = l; e < MNE; e += 8) part = part + E[wv][e];
+    float pv[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) pv[i] = __shfl(part, i, 64);
+    float sum = hsum8(pv);
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) p[i] = lg[i] / sum;
+    float tsum = 0.0f, pk[MTOPK]; int ek[MTOPK];
+#pragma unroll
+    for (int k = 0; k < MTOPK; k++) {
+        // lane-local best (lowest index among equals: i ascending means e ascending)
+        float bp = p[0]; int be = l;
+#pragma unroll
+        for (int i = 1; i < 4; i++) if (p[i] > bp) { bp = p[i]; be = l + 64 * i; }
+        for (int o = 32; o > 0; o >>= 1) {
+            float op = __shfl_xor(bp, o, 64); int oe = __shfl_xor(be, o, 64);
+            if (op > bp || (op == bp && oe < be)) { bp = op; be = oe; }
+        }
+        pk[k] = bp; ek[k] = be;
+        tsum = tsum + bp;
+        if ((be & 63) == l) p[be >> 6] = -1.0f;
+    }
+    if (l == 0) {
+#pragma unroll
+        for (int k = 0; k < MTOPK; k++) { top[b * MTOPK + k] = ek[k]; tw[b * MTOPK + k] = pk[k] / (tsum + 1e-20f); }
+    }
+}
+
+// =====================================================================================================
+// Grouping by expert, maple.c:924-938 (counting sort, stable in token order) + tp (maple.c:1018-1019).
+// Three kernels: per-chunk histograms (64 tokens per chunk), one block scanning them into the plan, and a
+// scatter in which every (token, slot) finds its rank among earlier tokens of its chunk with that expert.
+// =====================================================================================================
+__global__ void __launch_bounds__(256) k_hist(const int *__restrict__ top, int nb, int *__restrict__ hist) {
+    __shared__ int cnt[MNE];
+    int c = blockIdx.x, t = threadIdx.x;
+    cnt[t] = 0;
+    __syncthreads();
+    for (int i = t; i < 64 * MTOPK; i += 256) {
+        int b = c * 64 + i / MTOPK;
+        if (b < nb) atomicAdd(&cnt[top[b * MTOPK + (i % MTOPK)]], 1);
+    }
+    __syncthreads();
+    hist[c * MNE + t] = cnt[t];
+}
+
+// One block of 256 threads (thread = expert). hist[nchunk][256] -> base[nchunk][256] (first pair slot of
+// chunk c's pairs of expert e) and the plan; eptr_u[u] = layer table entry of expert ue[u] if table given.
+__global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int nchunk, int *__restrict__ base, Plan *__restrict__ plan,
+                                              const ExpPtr *__restrict__ layer_tab, ExpPtr *__restrict__ eptr_u, int tn) {
+    __shared__ int sc[MNE], su[MNE], st[MNE];
+    int e = threadIdx.x;
+    int run = 0;
+    for (int c = 0; c < nchunk; c++) { int h = hist[c * MNE + e]; base[c * MNE + e] = run; run += h; }
+    int used = run > 0, nt = (run + tn - 1) / tn;
+    sc[e] = run; su[e] = used; st[e] = nt;
+    __syncthreads();
+    // inclusive Hillis-Steele scans over 256 entries (integer, exact)
+    for (int o = 1; o < MNE; o <<= 1) {
+        int a = e >= o ? sc[e - o] : 0, bq = e >= o ? su[e - o] : 0, cq = e >= o ? st[e - o] : 0;
+        __syncthreads();
+        sc[e] += a; su[e] += bq; st[e] += cq;
+        __syncthreads();
+    }
+    int pstart = sc[e] - run, uidx = su[e] - used, tstart = st[e] - nt;
+    if (used) {
+        plan->ue[uidx] = e;
+        plan->ustart[uidx] = pstart;
+        plan->tstart[uidx] = tstart;
+        if (layer_tab) eptr_u[uidx] = layer_tab[e];
+    }
+    for (int c = 0; c < nchunk; c++) base[c * MNE + e] += pstart;
+    if (e == MNE - 1) {
+        int nu = su[e];
+        plan->nu = nu; plan->np = sc[e]; plan->ntile_gu = st[e]; plan->tn = tn;
+        plan->ustart[nu] = sc[e]; plan->tstart[nu] = st[e];
+    }
+}
+
+// Block = one chunk of 64 tokens, thread = token. Pair slot of (b, s) = base[chunk][e] + number of earlier
+// tokens of the chunk that picked e. Writes utok/uw (maple.c:934-936), tp (pair ids of token b ascending)
+// and sp (pair id of slot s, for the decode combine order).
+__global__ void __launch_bounds__(64) k_scatter(const int *__restrict__ top, const float *__restrict__ tw, int nb,
+                                                const int *__restrict__ base, int *__restrict__ utok, float *__restrict__ uw,
+                                                int *__restrict__ tp, int *__restrict__ sp) {
+    __shared__ int tk[64 * MTOPK];
+    int c = blockIdx.x, t = threadIdx.x, b = c * 64 + t;
+    for (int s = 0; s < MTOPK; s++) tk[t * MTOPK + s] = b < nb ? top[b * MTOPK + s] : -1;
+    __syncthreads();
+    if (b >= nb) return;
+    int a[MTOPK];
+    for (int s = 0; s < MTOPK; s++) {
+        int e = tk[t * MTOPK + s], r = 0;
+        for (int o = 0; o < t; o++)
+            for (int q = 0; q < MTOPK; q++) r += tk[o * MTOPK + q] == e;
+        int slot = base[c * MNE + e] + r;
+        utok[slot] = b; uw[slot] = tw[b * MTOPK + s];
+        a[s] = slot;
+        if (sp) sp[b * MTOPK + s] = slot;
+    }
+    for (int i = 1; i < MTOPK; i++) { int v = a[i], j = i - 1; while (j >= 0 && a[j] > v) { a[j + 1] = a[j]; j--; } a[j + 1] = v; }
+    for (int s = 0; s < MTOPK; s++) tp[b * MTOPK + s] = a[s];
+}
+
+// Host-given grouping (gpre_moe / gfull_moe / gpux): plan from ustart; one thread.
+__global__ void k_plan_from_ustart(const int *__restrict__ ustart, int nu, Plan *__restrict__ plan, int tn) {
+    if (threadIdx.x != 0) return;
+    int t = 0;
+    for (int u = 0; u < nu; u++) { plan->ue[u] = u; plan->ustart[u] = ustart[u]; plan->tstart[u] = t; t += (ustart[u + 1] - ustart[u] + tn - 1) / tn; }
+    plan->ustart[nu] = ustart[nu]; plan->tstart[nu] = t;
+    plan->nu = nu; plan->np = ustart[nu]; plan->ntile_gu = t; plan->tn = tn;
+}
+
+// =====================================================================================================
+// Per-vector int8 quantisation, maple.c:183-194 as compiled with maple.c's -ffast-math flags:
+// qs = mx * fl(1/127), inv = 127 / mx (both 1 when mx = 0), q = rint(x * inv). One wave per vector of
+// n = 2048 or 512 values; output in mfma order (see top of file) plus qs and qsum. Optionally the source
+// rows are gathered (src_row = rows ? rows[i] : i) -- not used by the current path.
+// =====================================================================================================
+template <int N>
+__global__ void __launch_bounds__(256) k_quant(const float *__restrict__ x, int nrows, int8_t *__restrict__ q,
+                                               float *__restrict__ qs, int *__restrict__ qsum) {
+    constexpr int NCHK = N / 16;                    // 16-byte output chunks per vector
+    constexpr int PER = (NCHK + 63) / 64;           // chunks per lane
+    int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    int row = blockIdx.x * 4 + wv;
+    if (row >= nrows) return;
+    const float *xr = x + (size_t)row * N;
+    float v[PER][16];
+    float mx = 0.0f;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        int o = l + 64 * k;
+        if (o < NCHK) {
+            int g = o >> 3, h = (o >> 2) & 1, t = o & 3;
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                float4 f = *(const float4 *)(xr + g * 128 + s * 32 + h * 16 + t * 4);
+                v[k][s * 4 + 0] = f.x; v[k][s * 4 + 1] = f.y; v[k][s * 4 + 2] = f.z; v[k][s * 4 + 3] = f.w;
+            }
+#pragma unroll
+            for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[k][i]));
+        }
+    }
+    mx = wave_max(mx);
+    float qsv = 1.0f, inv = 1.0f;
+    if (mx > 0.0f) { qsv = mx * (1.0f / 127.0f); inv = 127.0f / mx; }
+    int sum = 0;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        int o = l + 64 * k;
+        if (o < NCHK) {
+            uint32_t wds[4];
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+                uint32_t wd = 0;
+#pragma unroll
+                for (int bb = 0; bb < 4; bb++) {
+                    int qi = (int)__builtin_rintf(v[k][d * 4 + bb] * inv);
+                    sum += qi;
+                    wd |= (uint32_t)(qi & 0xff) << (8 * bb);
+                }
+                wds[d] = wd;
+            }
+            *(uint4 *)(q + (size_t)row * N + o * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+        }
+    }
+    sum = wave_sum_i(sum);
+    if (l == 0) { qs[row] = qsv; qsum[row] = sum; }
+}
+
+// =====================================================================================================
+// Grouped ternary x int8 GEMM on CDNA4 int8 MFMA (v_mfma_i32_16x16x64_i8), shared by gate/up and down.
+//
+// MFMA operand mapping. A = codes (16 weight rows x 64 k), B = activations (64 k x 16 tokens). A lane
+// (G = lane/16, r = lane%16) holds 16 int8 of row r; B lane (G, n) holds the same 16 k positions of token n;
+// which 16 k positions a (G, byte) slot stands for is the same for A and B, so any consistent assignment of
+// columns to slots gives the exact integer dot product. We assign them so that one 32-bit word of packed
+// codes is one lane's A operand: code word at byte j0 of a 128-group, shifted by 2s and masked with
+// 0x03030303, is the int8 codes of columns s*32 + j0 + 0..3 (s = 0..3). Lane (G, r) loads 16 code bytes
+// (group G/2 of a 256-column chunk, bytes (G%2)*16 .. +16) = 4 code words = the A operands of 4 MFMA steps;
+// the matching activation bytes are 64 contiguous bytes in mfma order. Codes stay {0,1,2}: the sum of
+// (c - 1) q is the MFMA result minus qsum, exactly as maple.c does (maple.c:226).
+// Result D lane (G, n): rows 4G..4G+3 of the 16-row block, token n.
+// =====================================================================================================
+__device__ __forceinline__ v4i decode_word(uint32_t w) {
+    const uint32_t M = 0x03030303u;
+    v4i a;
+    a.x = (int)(w & M); a.y = (int)((w >> 2) & M); a.z = (int)((w >> 4) & M); a.w = (int)((w >> 6) & M);
+    return a;
+}
+
+// Find the token tile: used expert u with tstart[u] <= tile < tstart[u+1] (binary search, nu <= 256).
+__device__ __forceinline__ int find_u(const Plan *plan, int tile) {
+    int lo = 0, hi = plan->nu - 1;
+    while (lo < hi) { int mid = (lo + hi + 1) >> 1; if (plan->tstart[mid] <= tile) lo = mid; else hi = mid - 1; }
+    return lo;
+}
+
+// Gate+up with fused SiLU*up (maple.c:471-479, 825-830). Block = WAVES waves; wave w owns RF 16-row
+// fragments of gate rows and the same RF fragments of up rows; the block covers WAVES*RF*16 rows of both.
+// Grid: x = token tile (early exit beyond plan->ntile_gu), y = row block. TN tokens per tile (16 or 64).
+// Activations of the tile's tokens are staged in LDS 256 columns at a time (double buffered).
+template <int TN, int WAVES, int RF>
+__global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ plan, const ExpPtr *__restrict__ eptr,
+                                                        const int *__restrict__ utok, const int8_t *__restrict__ qx,
+                                                        const float *__restrict__ qsx, const int *__restrict__ qsumx,
+                                                        float *__restrict__ act, int *__restrict__ dbg) {
+    constexpr int NT = WAVES * 64;
+    constexpr int NF = TN / 16;                // token fragments
+    constexpr int LDSW = 256 + 16;             // bytes per token row in LDS (padded)
+    __shared__ __attribute__((aligned(16))) int8_t bs[2][TN * LDSW];
+    __shared__ int toks[TN];
+    int tile = blockIdx.x;
+    if (tile >= plan->ntile_gu) return;
+    int u = find_u(plan, tile);
+    int p0 = plan->ustart[u] + (tile - plan->tstart[u]) * TN;
+    int ntok = min(TN, plan->ustart[u + 1] - p0);
+    ExpPtr ex = eptr[u];
+    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G = l >> 4, r16 = l & 15;
+    if (tid < TN) toks[tid] = tid < ntok ? utok[p0 + tid] : -1;
+    __syncthreads();
+
+    // B staging: TN tokens x 256 bytes per chunk; each thread moves 16-byte pieces
+    auto stage = [&](int chunk, int buf) {
+        for (int i = tid; i < TN * 16; i += NT) {
+            int tk = i >> 4, part = i & 15;
+            int tok = toks[tk];
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (tok >= 0) v = *(const uint4 *)(qx + (size_t)tok * MH + chunk * 256 + part * 16);
+            *(uint4 *)(&bs[buf][tk * LDSW + part * 16]) = v;
+        }
+    };
+    // A rows of this lane
+    int rowblk = blockIdx.y * (WAVES * RF * 16) + wv * RF * 16;
+    const uint8_t *arow[2 * RF];
+#pragma unroll
+    for (int f = 0; f < RF; f++) {
+        arow[f] = ex.gc + (size_t)(rowblk + f * 16 + r16) * (MH / 4);
+        arow[RF + f] = ex.uc + (size_t)(rowblk + f * 16 + r16) * (MH / 4);
+    }
+    v4i acc[2 * RF][NF];
+#pragma unroll
+    for (int f = 0; f < 2 * RF; f++)
+#pragma unroll
+        for (int j = 0; j < NF; j++) acc[f][j] = v4i{0, 0, 0, 0};
+
+    uint4 cw[2 * RF];
+    int aoff = (G >> 1) * 32 + (G & 1) * 16;  // byte offset of this lane's 16 code bytes in a 64-byte chunk
+#pragma unroll
+    for (int f = 0; f < 2 * RF; f++) cw[f] = *(const uint4 *)(arow[f] + aoff);
+    stage(0, 0);
+    __syncthreads();
+    constexpr int NCH = MH / 256;
+    for (int ch = 0; ch < NCH; ch++) {
+        int buf = ch & 1;
+        uint4 cn[2 * RF];
+        if (ch + 1 < NCH) {
+#pragma unroll
+            for (int f = 0; f < 2 * RF; f++) cn[f] = *(const uint4 *)(arow[f] + (ch + 1) * 64 + aoff);
+            stage(ch + 1, buf ^ 1);
+        }
+        const int8_t *bb = &bs[buf][0];
+        int boff = (G >> 1) * 128 + (G & 1) * 64;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            v4i bv[NF];
+#pragma unroll
+            for (int j = 0; j < NF; j++) bv[j] = *(const v4i *)(bb + (j * 16 + r16) * LDSW + boff + t * 16);
+#pragma unroll
+            for (int f = 0; f < 2 * RF; f++) {
+                uint32_t w = t == 0 ? cw[f].x : t == 1 ? cw[f].y : t == 2 ? cw[f].z : cw[f].w;
+                v4i av = decode_word(w);
+#pragma unroll
+                for (int j = 0; j < NF; j++) acc[f][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[j], acc[f][j], 0, 0, 0);
+            }
+        }
+        if (ch + 1 < NCH) {
+#pragma unroll
+            for (int f = 0; f < 2 * RF; f++) cw[f] = cn[f];
+        }
+        __syncthreads();
+    }
+    // epilogue: G, U -> act
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        int tk = j * 16 + r16;
+        if (tk >= ntok) continue;
+        int tok = toks[tk];
+        float qs = qsx[tok]; int qsum = qsumx[tok];
+        int pair = p0 + tk;
+#pragma unroll
+        for (int f = 0; f < RF; f++) {
+            int row0 = rowblk + f * 16 + 4 * G;
+            float4 sg = *(const float4 *)(ex.gs + row0), su = *(const float4 *)(ex.us + row0);
+            float sgv[4] = {sg.x, sg.y, sg.z, sg.w}, suv[4] = {su.x, su.y, su.z, su.w};
+            int ag[4] = {acc[f][j].x, acc[f][j].y, acc[f][j].z, acc[f][j].w};
+            int au[4] = {acc[RF + f][j].x, acc[RF + f][j].y, acc[RF + f][j].z, acc[RF + f][j].w};
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                float gv = (float)(ag[i] - qsum) * qs * sgv[i];
+                float uv = (float)(au[i] - qsum) * qs * suv[i];
+                float g = gv < 7.0f ? gv : 7.0f;
+                float uu = uv < -7.0f ? -7.0f : (uv > 7.0f ? 7.0f : uv);
+                o[i] = g / (1.0f + dexp(-g)) * uu;
+            }
+            *(float4 *)(act + (size_t)pair * MFF + row0) = make_float4(o[0], o[1], o[2], o[3]);
+            if (dbg) {
+                *(int4 *)(dbg + (size_t)pair * 2 * MFF + row0) = make_int4(ag[0], ag[1], ag[2], ag[3]);
+                *(int4 *)(dbg + (size_t)pair * 2 * MFF + MFF + row0) = make_int4(au[0], au[1], au[2], au[3]);
+            }
+        }
+    }
+}
+
+// Down (maple.c:498-505): D[pair][row] = (float)(sum c*qa - qsuma) * qsa * s_down[row]. Block = WAVES waves
+// of RF 16-row fragments; K = 512 staged in LDS at once. Pairs of a tile are contiguous (no gather).
+template <int TN, int WAVES, int RF>
+__global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ plan, const ExpPtr *__restrict__ eptr,
+                                                      const int8_t *__restrict__ qa, const float *__restrict__ qsa,
+                                                      const int *__restrict__ qsuma, float *__restrict__ down, int *__restrict__ dbg) {
+    constexpr int NT = WAVES * 64;
+    constexpr int NF = TN / 16;
+    constexpr int LDSW = MFF + 16;
+    __shared__ __attribute__((aligned(16))) int8_t bs[TN * LDSW];
+    int tile = blockIdx.x;
+    if (tile >= plan->ntile_gu) return;
+    int u = find_u(plan, tile);
+    int p0 = plan->ustart[u] + (tile - plan->tstart[u]) * TN;
+    int ntok = min(TN, plan->ustart[u + 1] - p0);
+    ExpPtr ex = eptr[u];
+    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G = l >> 4, r16 = l & 15;
+    int rowblk = blockIdx.y * (WAVES * RF * 16) + wv * RF * 16;
+    const uint8_t *arow[RF];
+#pragma unroll
+    for (int f = 0; f < RF; f++) arow[f] = ex.dc + (size_t)(rowblk + f * 16 + r16) * (MFF / 4);
+    int aoff = (G >> 1) * 32 + (G & 1) * 16;
+    uint4 cw[2][RF];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int f = 0; f < RF; f++) cw[h][f] = *(const uint4 *)(arow[f] + h * 64 + aoff);
+    for (int i = tid; i < TN * (MFF / 16); i += NT) {
+        int tk = i / (MFF / 16), part = i % (MFF / 16);
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (tk < ntok) v = *(const uint4 *)(qa + (size_t)(p0 + tk) * MFF + part * 16);
+        *(uint4 *)(&bs[tk * LDSW + part * 16]) = v;
+    }
+    __syncthreads();
+    v4i acc[RF][NF];
+#pragma unroll
+    for (int f = 0; f < RF; f++)
+#pragma unroll
+        for (int j = 0; j < NF; j++) acc[f][j] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+        int boff = h * 256 + (G >> 1) * 128 + (G & 1) * 64;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            v4i bv[NF];
+#pragma unroll
+            for (int j = 0; j < NF; j++) bv[j] = *(const v4i *)(bs + (j * 16 + r16) * LDSW + boff + t * 16);
+#pragma unroll
+            for (int f = 0; f < RF; f++) {
+                uint32_t w = t == 0 ? cw[h][f].x : t == 1 ? cw[h][f].y : t == 2 ? cw[h][f].z : cw[h][f].w;
+                v4i av = decode_word(w);
+#pragma unroll
+                for (int j = 0; j < NF; j++) acc[f][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[j], acc[f][j], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        int tk = j * 16 + r16;
+        if (tk >= ntok) continue;
+        int pair = p0 + tk;
+        float qs = qsa[pair]; int qsum = qsuma[pair];
+#pragma unroll
+        for (int f = 0; f < RF; f++) {
+            int row0 = rowblk + f * 16 + 4 * G;
+            float4 sd = *(const float4 *)(ex.ds + row0);
+            float sdv[4] = {sd.x, sd.y, sd.z, sd.w};
+            int ad[4] = {acc[f][j].x, acc[f][j].y, acc[f][j].z, acc[f][j].w};
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) o[i] = (float)(ad[i] - qsum) * qs * sdv[i];
+            *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
+            if (dbg) *(int4 *)(dbg + (size_t)pair * MH + row0) = make_int4(ad[0], ad[1], ad[2], ad[3]);
+        }
+    }
+}
+
+// =====================================================================================================
+// Combine, flag bits of mode: 1 = start from x (else from 0), 2 = slot order (sp/tw, else ascending pair
+// order tp/uw), 4 = add the chain to x at the end (else store it).
+//   step_batch maple.c:834            mode 1: x[b] = fma(uw[a], D[a], x[b]) over b's pairs in ascending order
+//   gpre_moe cmb gpu_pre.m:158-163    mode 0: y[b] = the same FMA chain from 0
+//   gfull_moe cmba gpu_full.metal:212 mode 4: x[b] += (FMA chain from 0)
+//   step maple.c:664                  mode 6: y = FMA chain over slots 0..7 from 0, x[b] += y
+// Thread = 4 columns of one token.
+// =====================================================================================================
+__global__ void __launch_bounds__(256) k_combine(const float *__restrict__ down, const float *__restrict__ uw,
+                                                 const int *__restrict__ tp, const int *__restrict__ sp,
+                                                 const float *__restrict__ tw, int nb, float *__restrict__ x, int mode) {
+    int gid = blockIdx.x * 256 + threadIdx.x;
+    int b = gid / (MH / 4), c = (gid % (MH / 4)) * 4;
+    if (b >= nb) return;
+    float4 *xp = (float4 *)(x + (size_t)b * MH + c);
+    float4 acc = (mode & 1) ? *xp : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < MTOPK; j++) {
+        int a = (mode & 2) ? sp[b * MTOPK + j] : tp[b * MTOPK + j];
+        float w = (mode & 2) ? tw[b * MTOPK + j] : uw[a];
+        float4 d = *(const float4 *)(down + (size_t)a * MH + c);
+        acc.x = __builtin_fmaf(w, d.x, acc.x); acc.y = __builtin_fmaf(w, d.y, acc.y);
+        acc.z = __builtin_fmaf(w, d.z, acc.z); acc.w = __builtin_fmaf(w, d.w, acc.w);
+    }
+    if (mode & 4) { float4 xv = *xp; acc.x = xv.x + acc.x; acc.y = xv.y + acc.y; acc.z = xv.z + acc.z; acc.w = xv.w + acc.w; }
+    *xp = acc;
+}

@@ -1,0 +1,598 @@
+// mmoe.hip -- libmaplemoe: the MI355X (gfx950) MoE hot path behind maple.c's GPU entry points.
+//
+// Exports, with maple.c's own C signatures (maple.c:247-272), the entry points maple.c links against when
+// built with -DGPU_HEAD: gpre_* (experts of a prompt chunk), gfull_* (device-resident hidden state), gpux_*
+// (decode experts) and gpu_head_*. Those outside the MoE path return the failure value maple.c already
+// handles by falling back to its CPU code. New mmoe_* entry points run the whole layer on the device:
+// router logits, softmax/top-8, grouping, int8 quantisation, gate/up + SiLU, re-quantisation, down and the
+// combine (declared in include/maplemoe.h).
+//
+// One global context, like the reference (gpu_pre.m keeps file-scope state); not thread-safe; all work is
+// queued on one default-priority HIP stream owned by the library.
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+#include <vector>
+#include "kernels.h"
+
+extern "C" {
+#include "../../include/maplemoe.h"
+}
+
+#define NLMAX 64
+#define EXPERT_BYTES 798720u
+
+static char g_err[512];
+static void seterr(const char *fmt, ...) {
+    va_list ap; va_start(ap, fmt); vsnprintf(g_err, sizeof g_err, fmt, ap); va_end(ap);
+    fprintf(stderr, "maplemoe: %s\n", g_err);
+}
+#define HC(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { seterr("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); return -1; } } while (0)
+#define HCV(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { seterr("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); return; } } while (0)
+#define HCN(call) do { hipError_t e_ = (call); if (e_ != hipSuccess) { seterr("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), __FILE__, __LINE__); return NULL; } } while (0)
+
+// ------------------------------------------------------------------------------------------------------
+// Device work buffers for up to maxtok tokens (maxp = maxtok * 8 pairs)
+// ------------------------------------------------------------------------------------------------------
+struct Work {
+    int maxtok = 0, maxp = 0;
+    float *hn = nullptr, *x = nullptr, *rl = nullptr, *tw = nullptr, *uw = nullptr;
+    int *top = nullptr, *hist = nullptr, *base = nullptr, *utok = nullptr, *tp = nullptr, *sp = nullptr, *ustart = nullptr;
+    Plan *plan = nullptr;
+    ExpPtr *eptr = nullptr;
+    int8_t *qx = nullptr, *qa = nullptr;
+    float *qsx = nullptr, *qsa = nullptr, *act = nullptr, *down = nullptr;
+    int *qsumx = nullptr, *qsuma = nullptr;
+    int *dbg_gu = nullptr, *dbg_dn = nullptr;
+};
+
+static int work_alloc(Work &w, int maxtok) {
+    if (maxtok < 1 || maxtok > MMOE_MAXTOK) { seterr("maxtok %d outside 1..%d", maxtok, MMOE_MAXTOK); return -1; }
+    w.maxtok = maxtok; w.maxp = maxtok * MTOPK;
+    int nch = (maxtok + 63) / 64;
+    size_t T = maxtok, P = w.maxp;
+    HC(hipMalloc(&w.hn, T * MH * 4)); HC(hipMalloc(&w.x, T * MH * 4)); HC(hipMalloc(&w.rl, T * MNE * 4));
+    HC(hipMalloc(&w.top, T * MTOPK * 4)); HC(hipMalloc(&w.tw, T * MTOPK * 4));
+    HC(hipMalloc(&w.hist, (size_t)nch * MNE * 4)); HC(hipMalloc(&w.base, (size_t)nch * MNE * 4));
+    HC(hipMalloc(&w.plan, sizeof(Plan))); HC(hipMalloc(&w.eptr, MNE * sizeof(ExpPtr)));
+    HC(hipMalloc(&w.utok, P * 4)); HC(hipMalloc(&w.uw, P * 4)); HC(hipMalloc(&w.tp, P * 4)); HC(hipMalloc(&w.sp, P * 4));
+    HC(hipMalloc(&w.ustart, (MNE + 1) * 4));
+    HC(hipMalloc(&w.qx, T * MH)); HC(hipMalloc(&w.qsx, T * 4)); HC(hipMalloc(&w.qsumx, T * 4));
+    HC(hipMalloc(&w.act, P * MFF * 4)); HC(hipMalloc(&w.qa, P * MFF)); HC(hipMalloc(&w.qsa, P * 4)); HC(hipMalloc(&w.qsuma, P * 4));
+    HC(hipMalloc(&w.down, P * MH * 4));
+    return 0;
+}
+
+static int work_debug(Work &w, int on) {
+    if (on && !w.dbg_gu) {
+        HC(hipMalloc(&w.dbg_gu, (size_t)w.maxp * 2 * MFF * 4));
+        HC(hipMalloc(&w.dbg_dn, (size_t)w.maxp * MH * 4));
+    }
+    if (!on && w.dbg_gu) { HC(hipFree(w.dbg_gu)); HC(hipFree(w.dbg_dn)); w.dbg_gu = w.dbg_dn = nullptr; }
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------------------------
+// Global state
+// ------------------------------------------------------------------------------------------------------
+struct Region { const void *host; size_t len; uint8_t *dev; };
+struct LayerW { ExpPtr *tab = nullptr; uint16_t *router = nullptr; uint16_t *post_ln = nullptr; float *bias = nullptr; };
+
+static struct {
+    bool ready = false;
+    hipStream_t st = nullptr;
+    Work main;                 // gpre / gfull / mmoe
+    Work dec;                  // gpux
+    bool debug = false;
+    std::vector<Region> regions;
+    LayerW layers[NLMAX];
+    double t_region = 0.0;     // seconds spent copying regions into HBM
+    // gpux
+    int gx_layers = 0, gx_slots = 0; uint8_t *gx_mem = nullptr;
+    hipEvent_t gx_ev = nullptr; int gx_np = 0;
+    // gfull
+    bool gfull = false; int gfull_nb = 0;
+    double t_moe = 0.0;
+    // profiling
+    bool prof = false;
+    hipEvent_t pe[2];
+    double prof_ms[MMOE_PROF_NKERNELS]; long prof_n[MMOE_PROF_NKERNELS];
+    hipGraphExec_t graph = nullptr;
+} S;
+
+static int ctx_ready() {
+    if (S.ready) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n < 1) { seterr("no HIP device"); return -1; }
+    HC(hipStreamCreateWithFlags(&S.st, hipStreamNonBlocking));
+    HC(hipEventCreate(&S.pe[0])); HC(hipEventCreate(&S.pe[1]));
+    HC(hipEventCreate(&S.gx_ev));
+    S.ready = true;
+    return 0;
+}
+
+// Launch helper: optional per-kernel event timing on the library stream.
+template <typename F>
+static int launch(int kid, F &&f) {
+    if (S.prof) HC(hipEventRecord(S.pe[0], S.st));
+    f();
+    HC(hipGetLastError());
+    if (S.prof) {
+        HC(hipEventRecord(S.pe[1], S.st));
+        HC(hipEventSynchronize(S.pe[1]));
+        float ms = 0; HC(hipEventElapsedTime(&ms, S.pe[0], S.pe[1]));
+        S.prof_ms[kid] += ms; S.prof_n[kid]++;
+    }
+    return 0;
+}
+
+// ------------------------------------------------------------------------------------------------------
+// Pipeline stages
+// ------------------------------------------------------------------------------------------------------
+static int tile_tn(int np) { return np >= 2048 ? 64 : 16; }
+
+// Router logits of nb tokens (d_hn) with layer L's router; order 0 = batch (maple.c:853-889), 1 = step (bf_row)
+static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
+    LayerW &lw = S.layers[L];
+    if (!lw.router) { seterr("layer %d has no router (mmoe_set_layer)", L); return -1; }
+    if (order == MMOE_ORDER_STEP) {
+        int n = nb * MNE * 16;
+        return launch(MMOE_K_ROUTER, [&] { k_router_lanes<16><<<(n + 255) / 256, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
+    }
+    if (nb <= 16) {
+        int n = nb * MNE * 8;
+        return launch(MMOE_K_ROUTER, [&] { k_router_lanes<8><<<(n + 255) / 256, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
+    }
+    return launch(MMOE_K_ROUTER, [&] { k_router_tiled<4><<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
+}
+
+// softmax/top-8 and grouping of nb tokens; eptr filled from layer L's table
+static int stage_route_group(Work &w, int L, int nb, int tn) {
+    int nch = (nb + 63) / 64;
+    if (launch(MMOE_K_TOPK, [&] { k_topk<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rl, nb, w.top, w.tw); })) return -1;
+    if (launch(MMOE_K_GROUP, [&] {
+            k_hist<<<nch, 256, 0, S.st>>>(w.top, nb, w.hist);
+            k_plan<<<1, 256, 0, S.st>>>(w.hist, nch, w.base, w.plan, S.layers[L].tab, w.eptr, tn);
+            k_scatter<<<nch, 64, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp);
+        })) return -1;
+    return 0;
+}
+
+static int stage_quant_x(Work &w, const float *d_hn, int nb) {
+    return launch(MMOE_K_QUANT, [&] { k_quant<MH><<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, w.qx, w.qsx, w.qsumx); });
+}
+
+// gate/up (+SiLU), act quantisation, down for np pairs under w.plan / w.eptr / w.utok
+static int stage_experts(Work &w, int np, int nu_max, int tn) {
+    int maxtiles = np / tn + (nu_max < np ? nu_max : np);
+    int *dg = S.debug ? w.dbg_gu : nullptr, *dd = S.debug ? w.dbg_dn : nullptr;
+    if (tn == 64) {
+        if (launch(MMOE_K_GATEUP, [&] { k_gateup<64, 4, 2><<<dim3(maxtiles, MFF / 128), 256, 0, S.st>>>(w.plan, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); })) return -1;
+    } else {
+        if (launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<dim3(maxtiles, MFF / 16), 64, 0, S.st>>>(w.plan, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); })) return -1;
+    }
+    if (launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(np + 3) / 4, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); })) return -1;
+    if (tn == 64) {
+        if (launch(MMOE_K_DOWN, [&] { k_down<64, 4, 4><<<dim3(maxtiles, MH / 256), 256, 0, S.st>>>(w.plan, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); })) return -1;
+    } else {
+        if (launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<dim3(maxtiles, MH / 64), 64, 0, S.st>>>(w.plan, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); })) return -1;
+    }
+    return 0;
+}
+
+static int stage_combine(Work &w, int nb, float *d_x, int mode) {
+    int n = nb * (MH / 4);
+    return launch(MMOE_K_COMBINE, [&] { k_combine<<<(n + 255) / 256, 256, 0, S.st>>>(w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode); });
+}
+
+// Whole MoE layer on device buffers: x[b] += MoE_L(hn[b])
+static int moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) {
+    Work &w = S.main;
+    if (nb < 1 || nb > w.maxtok) { seterr("nb %d outside 1..%d (mmoe_init)", nb, w.maxtok); return -1; }
+    if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("layer %d not set (mmoe_set_layer)", L); return -1; }
+    int np = nb * MTOPK, tn = tile_tn(np);
+    if (stage_router(w, L, d_hn, nb, order)) return -1;
+    if (stage_route_group(w, L, nb, tn)) return -1;
+    if (stage_quant_x(w, d_hn, nb)) return -1;
+    if (stage_experts(w, np, MNE, tn)) return -1;
+    return stage_combine(w, nb, d_x, order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH);
+}
+
+// Experts for a host-given grouping (gpre_moe, gfull_moe, gpux): ustart[nu+1], ptok, pw, tp on the host,
+// eptr[nu] resolved on the host. Input activations in w.hn.
+static int experts_host_grouping(Work &w, int nb, int nu, const ExpPtr *eptr_h, const int *ustart, const int *ptok,
+                                 const float *pw, const int *tp) {
+    if (nu < 1 || nu > MNE) { seterr("nu %d outside 1..256", nu); return -1; }
+    int np = ustart[nu];
+    if (nb < 1 || nb > w.maxtok || np < 1 || np > w.maxp) { seterr("nb %d / pairs %d exceed capacity %d / %d", nb, np, w.maxtok, w.maxp); return -1; }
+    for (int u = 0; u < nu; u++) if (ustart[u + 1] < ustart[u]) { seterr("ustart not ascending at %d", u); return -1; }
+    for (int a = 0; a < np; a++) if (ptok[a] < 0 || ptok[a] >= nb) { seterr("ptok[%d] = %d outside 0..%d", a, ptok[a], nb - 1); return -1; }
+    if (tp) for (int i = 0; i < nb * MTOPK; i++) if (tp[i] < 0 || tp[i] >= np) { seterr("tp[%d] = %d outside 0..%d", i, tp[i], np - 1); return -1; }
+    int tn = tile_tn(np);
+    HC(hipMemcpyAsync(w.eptr, eptr_h, sizeof(ExpPtr) * nu, hipMemcpyHostToDevice, S.st));
+    HC(hipMemcpyAsync(w.ustart, ustart, sizeof(int) * (nu + 1), hipMemcpyHostToDevice, S.st));
+    HC(hipMemcpyAsync(w.utok, ptok, sizeof(int) * np, hipMemcpyHostToDevice, S.st));
+    if (pw) HC(hipMemcpyAsync(w.uw, pw, sizeof(float) * np, hipMemcpyHostToDevice, S.st));
+    if (tp) HC(hipMemcpyAsync(w.tp, tp, sizeof(int) * nb * MTOPK, hipMemcpyHostToDevice, S.st));
+    if (launch(MMOE_K_GROUP, [&] { k_plan_from_ustart<<<1, 64, 0, S.st>>>(w.ustart, nu, w.plan, tn); })) return -1;
+    if (stage_quant_x(w, w.hn, nb)) return -1;
+    return stage_experts(w, np, nu, tn);
+}
+
+// loc (maple.c:276-277: per used expert 6 x (region slot, byte offset)) + regs -> device pointers
+static int resolve_loc(const uint32_t *loc, const int *regs, int n, ExpPtr *out) {
+    for (int u = 0; u < n; u++) {
+        const uint8_t *p[6];
+        for (int m = 0; m < 6; m++) {
+            uint32_t slot = loc[u * 12 + 2 * m], off = loc[u * 12 + 2 * m + 1];
+            if (slot > 3 || regs[slot] < 0 || regs[slot] >= (int)S.regions.size()) { seterr("loc[%d][%d]: region slot %u has no region", u, m, slot); return -1; }
+            const Region &R = S.regions[regs[slot]];
+            size_t len = m == 1 || m == 3 ? 512 * 4 : m == 5 ? 2048 * 4 : 262144;
+            if ((size_t)off + len > R.len || (off & 15)) { seterr("loc[%d][%d]: offset %u outside region %d or not 16-byte aligned", u, m, off, regs[slot]); return -1; }
+            p[m] = R.dev + off;
+        }
+        out[u] = ExpPtr{p[0], (const float *)p[1], p[2], (const float *)p[3], p[4], (const float *)p[5]};
+    }
+    return 0;
+}
+
+// ======================================================================================================
+// maple.c's entry points (maple.c:247-272)
+// ======================================================================================================
+extern "C" {
+
+// gpu_pre.m:266-316. Allocates the work buffers for chunks of up to maxtok tokens.
+int gpre_init(int maxtok, int topk) {
+    if (topk != MTOPK) { seterr("gpre_init: topk %d unsupported (this build is for TOPK = 8)", topk); return -1; }
+    if (ctx_ready()) return -1;
+    if (S.main.maxtok) return maxtok <= S.main.maxtok ? 0 : (seterr("gpre_init: already initialised for %d tokens", S.main.maxtok), -1);
+    if (work_alloc(S.main, maxtok)) return -1;
+    if (work_debug(S.main, S.debug)) return -1;
+    fprintf(stderr, "maplemoe: MI355X MoE path, chunks up to %d tokens, expert codes resident in HBM\n", maxtok);
+    return 0;
+}
+
+// gpu_pre.m:173-181. A page-aligned span of an mmapped shard becomes a region. On MI355X the span is copied
+// into HBM once (it stays resident; the reference read it over PCIe in place).
+int gpre_region(const void *p, size_t len) {
+    if (ctx_ready()) return -1;
+    size_t pg = (size_t)getpagesize();
+    if (((uintptr_t)p % pg) || (len % pg) || !len) { seterr("gpre_region: region not page-aligned"); return -1; }
+    if (S.regions.size() >= MMOE_MAXREG) { seterr("gpre_region: more than %d regions", MMOE_MAXREG); return -1; }
+    uint8_t *d = nullptr;
+    HC(hipMalloc(&d, len));
+    hipEvent_t a, b; HC(hipEventCreate(&a)); HC(hipEventCreate(&b));
+    HC(hipEventRecord(a, S.st));
+    HC(hipMemcpyAsync(d, p, len, hipMemcpyHostToDevice, S.st));
+    HC(hipEventRecord(b, S.st));
+    HC(hipEventSynchronize(b));
+    float ms = 0; HC(hipEventElapsedTime(&ms, a, b)); S.t_region += ms * 1e-3;
+    HC(hipEventDestroy(a)); HC(hipEventDestroy(b));
+    S.regions.push_back(Region{p, len, d});
+    return (int)S.regions.size() - 1;
+}
+
+// gpu_pre.m:183-188. Weights are already resident in HBM: nothing to stage.
+int gpre_stage(size_t bytes) { (void)bytes; return 0; }
+
+// gpu_pre.m:321-385. Synchronous: x[nb][2048] post-norm (host), grouping from the host, y[nb][2048] =
+// sum over each token's pairs of pw * down (overwritten). Returns device seconds. next: unused (resident).
+double gpre_moe(const float *x, int nb, int nu, const uint32_t *loc, const int *regs, const int *next, const int *ustart,
+                const int *ptok, const float *pw, const int *tp, float *y) {
+    (void)next;
+    Work &w = S.main;
+    if (!w.maxtok) { seterr("gpre_moe before gpre_init"); return -1.0; }
+    if (nb < 1 || nb > w.maxtok) { seterr("gpre_moe: nb %d outside 1..%d", nb, w.maxtok); return -1.0; }
+    ExpPtr ep[MNE];
+    if (nu < 1 || nu > MNE || resolve_loc(loc, regs, nu, ep)) { if (nu < 1 || nu > MNE) seterr("gpre_moe: nu %d", nu); return -1.0; }
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { seterr("gpre_moe: event"); return -1.0; }
+    (void)hipEventRecord(a, S.st);
+    if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_moe: copy x"); return -1.0; }
+    if (experts_host_grouping(w, nb, nu, ep, ustart, ptok, pw, tp)) return -1.0;
+    if (stage_combine(w, nb, w.x, MMOE_COMBINE_OVERWRITE)) return -1.0;
+    (void)hipEventRecord(b, S.st);
+    if (hipMemcpyAsync(y, w.x, (size_t)nb * MH * 4, hipMemcpyDeviceToHost, S.st) != hipSuccess || hipStreamSynchronize(S.st) != hipSuccess) {
+        seterr("gpre_moe: %s", hipGetErrorString(hipGetLastError())); return -1.0;
+    }
+    float ms = 0; (void)hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a); (void)hipEventDestroy(b);
+    S.t_moe += ms * 1e-3;
+    return ms * 1e-3;
+}
+
+// gpu_pre.m:257-264: seconds spent moving weights to the card (here: the one-time region copies)
+double gpre_blit_seconds(void) { return S.t_region; }
+
+// Dense attention projections (gpu_pre.m:200-256) are not part of the MoE path: gpre_dense_done reports
+// failure, which makes maple.c keep q/k/v/o on the CPU (maple.c:1141).
+void gpre_dense_add(int g, const uint8_t *codes, const float *scales, int rows, int cols) { (void)g; (void)codes; (void)scales; (void)rows; (void)cols; }
+int gpre_dense_done(int maxtok) { (void)maxtok; fprintf(stderr, "maplemoe: attention projections stay on the CPU (not part of this build)\n"); return -1; }
+double gpre_dense(int g, const float *x, int nb, float *y) { (void)g; (void)x; (void)nb; (void)y; seterr("gpre_dense: not part of this build"); return -1.0; }
+
+// Output head (gpu_head.m): not part of the MoE path; init failure makes maple.c use its CPU head.
+int gpu_head_init(const uint16_t *w, int rows, int cols) { (void)w; (void)rows; (void)cols; return -1; }
+int gpu_head_init_i8(const int8_t *w, const float *scale, int rows, int cols) { (void)w; (void)scale; (void)rows; (void)cols; return -1; }
+void gpu_head_run(const float *x, float *y) { (void)x; (void)y; seterr("gpu_head_run: not part of this build"); }
+void gpu_head_run_multi(const float *x, int n, float *y) { (void)x; (void)n; (void)y; seterr("gpu_head_run_multi: not part of this build"); }
+
+// ---- whole-layer state (gpu_pre.m:387-594). Attention is not part of this build, so gfull_init reports
+// failure and maple.c runs gpre_moe with CPU attention (maple.c:1156-1158). The device hidden state and
+// gfull_moe work for callers that prepare the MoE input with mmoe_gfull_setup / mmoe_gfull_post_norm.
+int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t *router, const float *cs) {
+    (void)ctx; (void)maxtok; (void)win; (void)norms; (void)router; (void)cs;
+    fprintf(stderr, "maplemoe: whole layers need attention on the card, not part of this build\n");
+    return -1;
+}
+void gfull_begin(const float *x, int nb, int pos0) {
+    (void)pos0;
+    if (!S.gfull || nb < 1 || nb > S.main.maxtok) { seterr("gfull_begin: not set up or nb %d out of range", nb); return; }
+    S.gfull_nb = nb;
+    HCV(hipMemcpyAsync(S.main.x, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st));
+}
+double gfull_attn(int L, int glob, float *rl) { (void)L; (void)glob; (void)rl; seterr("gfull_attn: attention is not part of this build"); return -1.0; }
+// gpu_pre.m:508-566: asynchronous; adds each token's weighted expert outputs into the device hidden state
+void gfull_moe(int nu, const uint32_t *loc, const int *regs, const int *ustart, const int *ptok, const float *pw, const int *tp) {
+    if (!S.gfull) { seterr("gfull_moe: gfull state not set up"); return; }
+    ExpPtr ep[MNE];
+    if (nu < 1 || nu > MNE) { seterr("gfull_moe: nu %d", nu); return; }
+    if (resolve_loc(loc, regs, nu, ep)) return;
+    if (experts_host_grouping(S.main, S.gfull_nb, nu, ep, ustart, ptok, pw, tp)) return;
+    stage_combine(S.main, S.gfull_nb, S.main.x, MMOE_COMBINE_ADD);
+}
+// gpu_pre.m:569-584: waits, copies the hidden state back; K/V are not kept by this build (*ko = NULL)
+void gfull_read(float *x, const uint16_t **ko) {
+    if (ko) *ko = NULL;
+    HCV(hipStreamSynchronize(S.st));
+    if (x && S.gfull) HCV(hipMemcpy(x, S.main.x, (size_t)S.gfull_nb * MH * 4, hipMemcpyDeviceToHost));
+}
+void gfull_write_x(const float *x) {
+    if (!S.gfull) { seterr("gfull_write_x: not set up"); return; }
+    HCV(hipMemcpyAsync(S.main.x, x, (size_t)S.gfull_nb * MH * 4, hipMemcpyHostToDevice, S.st));
+}
+int gfull_maxtok(void) { return S.main.maxtok; }
+void gfull_report(void) { fprintf(stderr, "maplemoe: %.3f s of expert work on the card\n", S.t_moe); }
+
+// ---- decode expert cache (gpu_exp.m:155-291). Slots hold experts in the reference layout in HBM; a hit
+// runs prep, gate/up, SiLU, re-quant and down on the device with maple.c's int8 semantics.
+int gpux_init(int layers, int slots) {
+    if (ctx_ready()) return -1;
+    if (layers < 1 || layers > NLMAX || slots < 1 || slots > 256) { seterr("gpux_init: layers %d / slots %d out of range", layers, slots); return -1; }
+    if (!S.dec.maxtok && work_alloc(S.dec, MMOE_GPUX_MAXTOK)) return -1;
+    if (work_debug(S.dec, S.debug)) return -1;
+    if (S.gx_mem) HC(hipFree(S.gx_mem));
+    HC(hipMalloc(&S.gx_mem, (size_t)layers * slots * EXPERT_BYTES));
+    S.gx_layers = layers; S.gx_slots = slots;
+    return 0;
+}
+static ExpPtr slot_ptr(int L, int slot) {
+    uint8_t *b = S.gx_mem + ((size_t)L * S.gx_slots + slot) * EXPERT_BYTES;
+    return ExpPtr{b, (const float *)(b + 262144), b + 264192, (const float *)(b + 526336), b + 528384, (const float *)(b + 790528)};
+}
+void gpux_upload(int L, int slot, const uint8_t *gc, const float *gs, const uint8_t *uc, const float *us, const uint8_t *dc, const float *ds) {
+    if (!S.gx_mem || L < 0 || L >= S.gx_layers || slot < 0 || slot >= S.gx_slots) { seterr("gpux_upload: L %d slot %d out of range", L, slot); return; }
+    ExpPtr p = slot_ptr(L, slot);
+    HCV(hipMemcpyAsync((void *)p.gc, gc, 262144, hipMemcpyHostToDevice, S.st));
+    HCV(hipMemcpyAsync((void *)p.gs, gs, 2048, hipMemcpyHostToDevice, S.st));
+    HCV(hipMemcpyAsync((void *)p.uc, uc, 262144, hipMemcpyHostToDevice, S.st));
+    HCV(hipMemcpyAsync((void *)p.us, us, 2048, hipMemcpyHostToDevice, S.st));
+    HCV(hipMemcpyAsync((void *)p.dc, dc, 262144, hipMemcpyHostToDevice, S.st));
+    HCV(hipMemcpyAsync((void *)p.ds, ds, 8192, hipMemcpyHostToDevice, S.st));
+    HCV(hipStreamSynchronize(S.st));  // the host buffers are the caller's mmap; keep the copy synchronous
+}
+static void *gpux_start(int L, const float *x, int nb, int nu, const int *slots, const int *pstart, const int *ptok) {
+    if (!S.gx_mem || L < 0 || L >= S.gx_layers) { seterr("gpux: not initialised or layer %d out of range", L); return NULL; }
+    Work &w = S.dec;
+    if (nb < 1 || nb > w.maxtok) { seterr("gpux: %d vectors exceed %d", nb, w.maxtok); return NULL; }
+    ExpPtr ep[MNE];
+    if (nu < 1 || nu > MNE) { seterr("gpux: %d experts", nu); return NULL; }
+    for (int k = 0; k < nu; k++) {
+        if (slots[k] < 0 || slots[k] >= S.gx_slots) { seterr("gpux: slot %d out of range", slots[k]); return NULL; }
+        ep[k] = slot_ptr(L, slots[k]);
+    }
+    HCN(hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st));
+    if (experts_host_grouping(w, nb, nu, ep, pstart, ptok, NULL, NULL)) return NULL;
+    HCN(hipEventRecord(S.gx_ev, S.st));
+    S.gx_np = pstart[nu];
+    return (void *)&S.gx_ev;
+}
+static void gpux_finish(void *h, float *out, int np) {
+    if (h != (void *)&S.gx_ev) { seterr("gpux_end: unknown handle"); return; }
+    if (np != S.gx_np) { seterr("gpux_end: %d outputs asked, %d computed", np, S.gx_np); return; }
+    HCV(hipMemcpyAsync(out, S.dec.down, (size_t)np * MH * 4, hipMemcpyDeviceToHost, S.st));
+    HCV(hipStreamSynchronize(S.st));
+}
+// n hits of one token: outputs out[k][2048] = down of slot k's expert (unweighted), maple.c:628-642
+void *gpux_begin(int L, const float *x, int n, const int *slots) {
+    int ps[MNE + 1], pt[MNE];
+    if (n < 1 || n > MNE) { seterr("gpux_begin: n %d", n); return NULL; }
+    for (int k = 0; k <= n; k++) ps[k] = k;
+    for (int k = 0; k < n; k++) pt[k] = 0;
+    return gpux_start(L, x, 1, n, slots, ps, pt);
+}
+void gpux_end(void *h, float *out, int n) { gpux_finish(h, out, n); }
+void *gpux_begin_multi(int L, const float *x, int nb, int nu, const int *slots, const int *pstart, const int *ptok) {
+    return gpux_start(L, x, nb, nu, slots, pstart, ptok);
+}
+void gpux_end_multi(void *h, float *out, int np) { gpux_finish(h, out, np); }
+
+// ======================================================================================================
+// mmoe_*: the whole MoE layer on the device
+// ======================================================================================================
+const char *mmoe_last_error(void) { return g_err; }
+
+int mmoe_init(int maxtok) {
+    if (ctx_ready()) return -1;
+    if (S.main.maxtok) return maxtok <= S.main.maxtok ? 0 : (seterr("mmoe_init: already initialised for %d tokens", S.main.maxtok), -1);
+    if (work_alloc(S.main, maxtok)) return -1;
+    return work_debug(S.main, S.debug);
+}
+
+int mmoe_set_debug(int on) {
+    S.debug = on != 0;
+    if (S.main.maxtok && work_debug(S.main, S.debug)) return -1;
+    if (S.dec.maxtok && work_debug(S.dec, S.debug)) return -1;
+    return 0;
+}
+
+int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *router, const uint16_t *post_ln) {
+    if (ctx_ready()) return -1;
+    if (L < 0 || L >= NLMAX) { seterr("mmoe_set_layer: layer %d outside 0..%d", L, NLMAX - 1); return -1; }
+    LayerW &lw = S.layers[L];
+    ExpPtr ep[MNE];
+    if (resolve_loc(loc, regs, MNE, ep)) return -1;
+    if (!lw.tab) HC(hipMalloc(&lw.tab, sizeof(ExpPtr) * MNE));
+    if (!lw.router) HC(hipMalloc(&lw.router, (size_t)MNE * MH * 2));
+    HC(hipMemcpy(lw.tab, ep, sizeof ep, hipMemcpyHostToDevice));
+    HC(hipMemcpy(lw.router, router, (size_t)MNE * MH * 2, hipMemcpyHostToDevice));
+    if (post_ln) {
+        if (!lw.post_ln) HC(hipMalloc(&lw.post_ln, MH * 2));
+        HC(hipMemcpy(lw.post_ln, post_ln, MH * 2, hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
+int mmoe_set_bias(int L, const float *bias) {
+    if (ctx_ready()) return -1;
+    if (L < 0 || L >= NLMAX) { seterr("mmoe_set_bias: layer %d", L); return -1; }
+    LayerW &lw = S.layers[L];
+    if (!bias) { if (lw.bias) HC(hipFree(lw.bias)); lw.bias = nullptr; return 0; }
+    if (!lw.bias) HC(hipMalloc(&lw.bias, MNE * 4));
+    HC(hipMemcpy(lw.bias, bias, MNE * 4, hipMemcpyHostToDevice));
+    return 0;
+}
+
+int mmoe_moe(int L, const float *hn, int nb, float *x, int order) {
+    Work &w = S.main;
+    if (!w.maxtok) { seterr("mmoe_moe before mmoe_init"); return -1; }
+    if (nb < 1 || nb > w.maxtok) { seterr("mmoe_moe: nb %d outside 1..%d", nb, w.maxtok); return -1; }
+    HC(hipMemcpyAsync(w.hn, hn, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st));
+    HC(hipMemcpyAsync(w.x, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st));
+    if (moe_dev(L, w.hn, nb, w.x, order)) return -1;
+    HC(hipMemcpyAsync(x, w.x, (size_t)nb * MH * 4, hipMemcpyDeviceToHost, S.st));
+    HC(hipStreamSynchronize(S.st));
+    return 0;
+}
+
+int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) { return moe_dev(L, d_hn, nb, d_x, order); }
+
+int mmoe_rmsnorm_dev(const float *d_x, const uint16_t *d_w, int nb, float *d_out) {
+    if (ctx_ready()) return -1;
+    return launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(d_x, d_w, d_out, nb); });
+}
+
+int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order) {
+    Work &w = S.main;
+    if (!w.maxtok || nb < 1 || nb > w.maxtok) { seterr("mmoe_stack_dev: nb %d outside capacity %d", nb, w.maxtok); return -1; }
+    for (int L = L0; L < L0 + nl; L++) {
+        if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("mmoe_stack_dev: layer %d not set", L); return -1; }
+        const uint16_t *pw = S.layers[L].post_ln;
+        if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(d_x, pw, w.hn, nb); })) return -1;
+        if (moe_dev(L, w.hn, nb, d_x, order)) return -1;
+    }
+    return 0;
+}
+
+// Capture mmoe_stack_dev into a HIP graph and replay it (launch-bound decode). Profiling must be off.
+int mmoe_stack_graph(int L0, int nl, float *d_x, int nb, int order, int replays) {
+    if (S.prof) { seterr("mmoe_stack_graph: profiling is on"); return -1; }
+    if (!S.graph) {
+        hipGraph_t g;
+        HC(hipStreamBeginCapture(S.st, hipStreamCaptureModeThreadLocal));
+        int rc = mmoe_stack_dev(L0, nl, d_x, nb, order);
+        hipError_t e = hipStreamEndCapture(S.st, &g);
+        if (rc || e != hipSuccess) { seterr("graph capture failed: %s", hipGetErrorString(e)); return -1; }
+        HC(hipGraphInstantiate(&S.graph, g, nullptr, nullptr, 0));
+        HC(hipGraphDestroy(g));
+    }
+    for (int i = 0; i < replays; i++) HC(hipGraphLaunch(S.graph, S.st));
+    return 0;
+}
+int mmoe_graph_reset(void) { if (S.graph) { HC(hipGraphExecDestroy(S.graph)); S.graph = nullptr; } return 0; }
+
+// Intermediate results of the last main-context call (debug/test access)
+int mmoe_read(int what, void *dst, size_t bytes) {
+    Work &w = S.main;
+    const void *src = nullptr; size_t cap = 0;
+    size_t T = w.maxtok, P = w.maxp;
+    switch (what) {
+        case MMOE_R_LOGITS: src = w.rl; cap = T * MNE * 4; break;
+        case MMOE_R_TOP: src = w.top; cap = T * MTOPK * 4; break;
+        case MMOE_R_TW: src = w.tw; cap = T * MTOPK * 4; break;
+        case MMOE_R_PLAN: src = w.plan; cap = sizeof(Plan); break;
+        case MMOE_R_UTOK: src = w.utok; cap = P * 4; break;
+        case MMOE_R_UW: src = w.uw; cap = P * 4; break;
+        case MMOE_R_TP: src = w.tp; cap = P * 4; break;
+        case MMOE_R_SP: src = w.sp; cap = P * 4; break;
+        case MMOE_R_QX: src = w.qx; cap = T * MH; break;
+        case MMOE_R_QSX: src = w.qsx; cap = T * 4; break;
+        case MMOE_R_QSUMX: src = w.qsumx; cap = T * 4; break;
+        case MMOE_R_ACT: src = w.act; cap = P * MFF * 4; break;
+        case MMOE_R_QA: src = w.qa; cap = P * MFF; break;
+        case MMOE_R_QSA: src = w.qsa; cap = P * 4; break;
+        case MMOE_R_QSUMA: src = w.qsuma; cap = P * 4; break;
+        case MMOE_R_DOWN: src = w.down; cap = P * MH * 4; break;
+        case MMOE_R_GU_I32: src = w.dbg_gu; cap = P * 2 * MFF * 4; break;
+        case MMOE_R_DN_I32: src = w.dbg_dn; cap = P * MH * 4; break;
+        case MMOE_R_X: src = w.x; cap = T * MH * 4; break;
+        case MMOE_R_HN: src = w.hn; cap = T * MH * 4; break;
+        default: seterr("mmoe_read: unknown item %d", what); return -1;
+    }
+    if (!src) { seterr("mmoe_read: item %d not allocated (init / debug)", what); return -1; }
+    if (bytes > cap) { seterr("mmoe_read: %zu bytes asked, %zu held", bytes, cap); return -1; }
+    HC(hipStreamSynchronize(S.st));
+    HC(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int mmoe_gfull_setup(int maxtok) {
+    if (mmoe_init(maxtok)) return -1;
+    S.gfull = true;
+    return 0;
+}
+// The router stage of gfull_attn (gpu_full.metal rms + rtr): hn = rmsnorm(x, post_ln[L]), rl = router logits
+int mmoe_gfull_post_norm(int L, float *rl) {
+    if (!S.gfull || L < 0 || L >= NLMAX || !S.layers[L].router) { seterr("mmoe_gfull_post_norm: not set up / layer %d", L); return -1; }
+    Work &w = S.main; int nb = S.gfull_nb;
+    const uint16_t *pw = S.layers[L].post_ln;
+    if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(w.x, pw, w.hn, nb); })) return -1;
+    if (stage_router(w, L, w.hn, nb, MMOE_ORDER_BATCH)) return -1;
+    if (rl) { HC(hipMemcpyAsync(rl, w.rl, (size_t)nb * MNE * 4, hipMemcpyDeviceToHost, S.st)); HC(hipStreamSynchronize(S.st)); }
+    return 0;
+}
+
+// ---- device memory helpers (plain pointers; the caller owns them) ----
+void *mmoe_dev_alloc(size_t bytes) { if (ctx_ready()) return NULL; void *p = nullptr; HCN(hipMalloc(&p, bytes)); return p; }
+int mmoe_dev_free(void *p) { HC(hipFree(p)); return 0; }
+int mmoe_h2d(void *d, const void *h, size_t bytes) { if (ctx_ready()) return -1; HC(hipMemcpyAsync(d, h, bytes, hipMemcpyHostToDevice, S.st)); HC(hipStreamSynchronize(S.st)); return 0; }
+int mmoe_d2h(void *h, const void *d, size_t bytes) { if (ctx_ready()) return -1; HC(hipStreamSynchronize(S.st)); HC(hipMemcpy(h, d, bytes, hipMemcpyDeviceToHost)); return 0; }
+int mmoe_d2d(void *d, const void *s, size_t bytes) { if (ctx_ready()) return -1; HC(hipMemcpyAsync(d, s, bytes, hipMemcpyDeviceToDevice, S.st)); return 0; }
+int mmoe_sync(void) { if (ctx_ready()) return -1; HC(hipStreamSynchronize(S.st)); return 0; }
+void *mmoe_stream(void) { return ctx_ready() ? NULL : (void *)S.st; }
+
+// ---- timing on the library stream ----
+int mmoe_event_record(int slot) { if (ctx_ready() || slot < 0 || slot > 1) return -1; HC(hipEventRecord(S.pe[slot], S.st)); return 0; }
+double mmoe_event_elapsed_ms(void) {
+    if (hipEventSynchronize(S.pe[1]) != hipSuccess) return -1.0;
+    float ms = 0; if (hipEventElapsedTime(&ms, S.pe[0], S.pe[1]) != hipSuccess) return -1.0;
+    return ms;
+}
+int mmoe_prof(int on) { S.prof = on != 0; return 0; }
+int mmoe_prof_reset(void) { memset(S.prof_ms, 0, sizeof S.prof_ms); memset(S.prof_n, 0, sizeof S.prof_n); return 0; }
+int mmoe_prof_get(int kid, double *ms_total, long *count) {
+    if (kid < 0 || kid >= MMOE_PROF_NKERNELS) return -1;
+    *ms_total = S.prof_ms[kid]; *count = S.prof_n[kid]; return 0;
+}
+int mmoe_device_info(char *name, int len, int *cus, int *clock_khz) {
+    if (ctx_ready()) return -1;
+    hipDeviceProp_t p; HC(hipGetDeviceProperties(&p, 0));
+    if (name && len > 0) { strncpy(name, p.gcnArchName, len - 1); name[len - 1] = 0; }
+    if (cus) *cus = p.multiProcessorCount;
+    if (clock_khz) *clock_khz = p.clockRate;
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,154 @@
+"""ctypes bindings of the checker: liboracle.so (the C restatement) and _ref/libmaple_ref.so (maple.c itself).
+
+TEST INFRASTRUCTURE: imported only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+"""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+H, NE, TOPK, FF = 2048, 256, 8, 512
+
+
+def _p(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+class Expert(C.Structure):
+    _fields_ = [("gc", C.c_void_p), ("gs", C.c_void_p), ("uc", C.c_void_p), ("us", C.c_void_p),
+                ("dc", C.c_void_p), ("ds", C.c_void_p)]
+
+
+class Trace(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("rl", "top", "tw", "nu", "ue", "ustart", "utok", "uw", "tp", "qx", "qsx",
+                                           "qsumx", "gu_i32", "gate", "up", "act", "qa", "qsa", "qsuma", "dn_i32", "down")]
+
+
+_or = None
+_ref = None
+
+
+def oracle():
+    global _or
+    if _or is None:
+        path = os.path.join(HERE, "liboracle.so")
+        if not os.path.exists(path):
+            raise RuntimeError("oracle/liboracle.so not built (make -C oracle)")
+        _or = C.CDLL(path)
+        vp, i = C.c_void_p, C.c_int
+        for n, r, a in [("mo_prep", C.c_float, [vp, i, vp, vp]), ("mo_dot_i32", C.c_int32, [vp, vp, i]),
+                        ("mo_router_batch", None, [vp, i, vp, vp, vp]), ("mo_router_step", None, [vp, vp, vp, vp]),
+                        ("mo_exp", C.c_float, [C.c_float]), ("mo_topk", None, [vp, i, vp, vp]),
+                        ("mo_group", i, [vp, vp, i, vp, vp, vp, vp, vp, vp]), ("mo_act", None, [vp, vp, vp, i]),
+                        ("mo_rmsnorm", None, [vp, vp, i, vp]), ("mo_pack", None, [vp, i, i, vp]),
+                        ("mo_unpack", None, [vp, i, i, vp]),
+                        ("mo_moe_batch", None, [vp, i, vp, vp, vp, vp, vp, vp]),
+                        ("mo_moe_step", None, [vp, vp, vp, vp, vp, vp]),
+                        ("mo_experts_grouped", None, [vp, i, i, vp, vp, vp, vp, vp, vp, vp])]:
+            f = getattr(_or, n)
+            f.restype, f.argtypes = r, a
+    return _or
+
+
+def ref_available():
+    return os.path.exists(os.path.join(HERE, "_ref", "libmaple_ref.so"))
+
+
+def ref():
+    """maple.c compiled from /root/reference (oracle/Makefile `ref`)."""
+    global _ref
+    if _ref is None:
+        path = os.path.join(HERE, "_ref", "libmaple_ref.so")
+        if not os.path.exists(path):
+            raise RuntimeError("oracle/_ref/libmaple_ref.so not built (make -C oracle ref)")
+        _ref = C.CDLL(path)
+        vp, i = C.c_void_p, C.c_int
+        for n, r, a in [("ref_set_threads", i, [i]), ("ref_set_router", None, [i, vp]),
+                        ("ref_set_expert", None, [i, i, vp, vp, vp, vp, vp, vp]),
+                        ("ref_prep", C.c_float, [vp, i, vp, vp]), ("ref_dot_i32", None, [vp, i, i, vp, i, vp]),
+                        ("ref_route_batch", None, [i, vp, i, vp]), ("ref_route_step", None, [i, vp, vp]),
+                        ("ref_topk", None, [vp, i, vp, vp]), ("ref_group", i, [vp, vp, i, vp, vp, vp, vp, vp, vp]),
+                        ("ref_rmsnorm", None, [vp, vp, i, vp]), ("ref_act", None, [vp, vp, vp, i]),
+                        ("ref_moe_batch", None, [i, vp, i, vp] + [vp] * 14),
+                        ("ref_moe_step", None, [i, vp, vp, vp, vp, vp, vp, vp]), ("ref_now", C.c_double, [])]:
+            f = getattr(_ref, n)
+            f.restype, f.argtypes = r, a
+    return _ref
+
+
+# ------------------------------------------------------------------ oracle wrappers
+def prep(x):
+    x = np.ascontiguousarray(x, np.float32)
+    q = np.empty(x.shape[-1], np.int8); s = np.zeros(1, np.int32)
+    qs = oracle().mo_prep(_p(x), x.shape[-1], _p(q), _p(s))
+    return q, np.float32(qs), int(s[0])
+
+
+def router_batch(hn, w, bias=None):
+    hn = np.ascontiguousarray(hn, np.float32)
+    rl = np.empty((hn.shape[0], NE), np.float32)
+    oracle().mo_router_batch(_p(hn), hn.shape[0], _p(w), _p(bias), _p(rl))
+    return rl
+
+
+def router_step(hn, w, bias=None):
+    hn = np.ascontiguousarray(hn, np.float32)
+    rl = np.empty(NE, np.float32)
+    oracle().mo_router_step(_p(hn), _p(w), _p(bias), _p(rl))
+    return rl
+
+
+def topk(rl):
+    rl = np.ascontiguousarray(rl, np.float32).reshape(-1, NE)
+    top = np.empty((rl.shape[0], TOPK), np.int32); tw = np.empty((rl.shape[0], TOPK), np.float32)
+    oracle().mo_topk(_p(rl), rl.shape[0], _p(top), _p(tw))
+    return top, tw
+
+
+def group(top, tw):
+    nb = top.shape[0]; P = nb * TOPK
+    nu = np.zeros(1, np.int32); ue = np.zeros(NE, np.int32); us = np.zeros(NE + 1, np.int32)
+    utok = np.zeros(P, np.int32); uw = np.zeros(P, np.float32); tp = np.zeros(P, np.int32)
+    oracle().mo_group(_p(np.ascontiguousarray(top, np.int32)), _p(np.ascontiguousarray(tw, np.float32)), nb,
+                      _p(nu), _p(ue), _p(us), _p(utok), _p(uw), _p(tp))
+    n = int(nu[0])
+    return dict(nu=n, ue=ue[:n], ustart=us[:n + 1], utok=utok, uw=uw, tp=tp.reshape(nb, TOPK))
+
+
+def experts_table(blk):
+    """Expert structs (oracle layout) for all 256 experts of a synthetic layer block"""
+    from_base = blk.ctypes.data
+    tab = (Expert * NE)()
+    offs = (0, 262144, 264192, 526336, 528384, 790528)
+    for e in range(NE):
+        b = from_base + e * 798720
+        tab[e] = Expert(*[b + o for o in offs])
+    return tab
+
+
+def new_trace(nb, P, want=("rl", "top", "tw", "nu", "ue", "ustart", "utok", "uw", "tp", "qx", "qsx", "qsumx", "gu_i32",
+                           "gate", "up", "act", "qa", "qsa", "qsuma", "dn_i32", "down")):
+    shapes = dict(rl=((nb, NE), np.float32), top=((nb, TOPK), np.int32), tw=((nb, TOPK), np.float32),
+                  nu=((1,), np.int32), ue=((NE,), np.int32), ustart=((NE + 1,), np.int32), utok=((P,), np.int32),
+                  uw=((P,), np.float32), tp=((nb, TOPK), np.int32), qx=((nb, H), np.int8), qsx=((nb,), np.float32),
+                  qsumx=((nb,), np.int32), gu_i32=((P, 2 * FF), np.int32), gate=((P, FF), np.float32),
+                  up=((P, FF), np.float32), act=((P, FF), np.float32), qa=((P, FF), np.int8), qsa=((P,), np.float32),
+                  qsuma=((P,), np.int32), dn_i32=((P, H), np.int32), down=((P, H), np.float32))
+    arrs = {k: np.zeros(*shapes[k]) for k in want}
+    tr = Trace(**{k: v.ctypes.data for k, v in arrs.items()})
+    return tr, arrs
+
+
+def moe_batch(hn, router, experts, x, bias=None, rl_in=None, want=None):
+    hn = np.ascontiguousarray(hn, np.float32); nb = hn.shape[0]
+    tr, arrs = new_trace(nb, nb * TOPK, **({} if want is None else dict(want=want)))
+    oracle().mo_moe_batch(_p(hn), nb, _p(router), _p(bias), _p(rl_in), C.cast(experts, C.c_void_p), _p(x), C.byref(tr))
+    return arrs
+
+
+def moe_step(hn, router, experts, x, bias=None):
+    hn = np.ascontiguousarray(hn, np.float32)
+    tr, arrs = new_trace(1, TOPK)
+    oracle().mo_moe_step(_p(hn), _p(router), _p(bias), C.cast(experts, C.c_void_p), _p(x), C.byref(tr))
+    return arrs

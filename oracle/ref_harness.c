@@ -1,0 +1,168 @@
+/* ref_harness.c -- exposes maple.c's own MoE functions (compiled from /root/reference/maple.c as it lies)
+ * through a small C API, so tests can check the oracle and the HIP path against the reference itself.
+ *
+ * TEST INFRASTRUCTURE. Built by oracle/Makefile into oracle/_ref/libmaple_ref.so with maple.c's documented
+ * flags (-O3 -ffast-math) for the AVX2 ISA it targets (-mavx2 -mfma -mf16c). No reference source is copied:
+ * maple.c is included by path; its `main` is renamed so the file links as a library.
+ *
+ * What runs is maple.c's code: prep, tdot_multi, bf_row, job_route_small/multi, job_topk, group_pairs,
+ * job_gateup/job_down, jobB_gateup/jobB_down and run(). Three statements that maple.c writes inline inside
+ * step()/step_batch() are restated here because they are not functions of their own: the SiLU*up loop
+ * (maple.c:825-830 / 655-660), the batched combine (maple.c:834) and the decode combine (maple.c:664).
+ * They are compiled with the same flags, in the same translation unit.
+ */
+#define main maple_reference_main_unused
+#include "maple.c"
+#undef main
+
+static int REF_WORKERS;
+
+/* maple.c:1095 starts NT-1 spinning workers; the caller thread takes the first slice of each job */
+int ref_set_threads(int nt) {
+    if (nt < 1) nt = 1;
+    if (REF_WORKERS) return NT;  /* workers are started once, like maple.c's main */
+    NT = nt;
+    pthread_t th;
+    for (int i = 1; i < NT; i++) pthread_create(&th, NULL, worker, (void *)(intptr_t)i);
+    REF_WORKERS = NT > 1;
+    return NT;
+}
+
+/* Point layer L's router and experts at caller memory (maple.c:61-81 does this from layout.bin) */
+void ref_set_router(int L, const uint16_t *w) { LY[L].router.p = w; LY[L].router.rows = NE; LY[L].router.cols = H; }
+void ref_set_expert(int L, int e, const uint8_t *gc, const float *gs, const uint8_t *uc, const float *us,
+                    const uint8_t *dc, const float *ds) {
+    Layer *l = &LY[L];
+    l->eg[e] = (T2){gc, gs, FF, H};
+    l->eu[e] = (T2){uc, us, FF, H};
+    l->ed[e] = (T2){dc, ds, H, FF};
+}
+
+/* maple.c:183-194 */
+float ref_prep(const float *x, int n, int8_t *q, int32_t *qsum) {
+    static Vin v;
+    prep(&v, x, n);
+    memcpy(q, v.q, (size_t)n);
+    *qsum = v.qsum;
+    return v.qs;
+}
+
+/* maple.c:423-458 tdot_multi with qs = 1, qsum = 0 and unit row scale: the fp32 result is the exact
+ * integer sum of code*q (|sum| < 2^24). rows x cols codes, nv int8 vectors (each cols long). */
+void ref_dot_i32(const uint8_t *codes, int rows, int cols, const int8_t *q, int nv, int32_t *out) {
+    static Vin *vs[BMAX]; static Vin pool[64];
+    float *ones = malloc(sizeof(float) * rows), *res = malloc(sizeof(float) * (size_t)rows * nv);
+    for (int r = 0; r < rows; r++) ones[r] = 1.0f;
+    T2 w = {codes, ones, rows, cols};
+    for (int i0 = 0; i0 < nv; i0 += 64) {
+        int n = nv - i0 < 64 ? nv - i0 : 64;
+        for (int i = 0; i < n; i++) { memcpy(pool[i].q, q + (size_t)(i0 + i) * cols, (size_t)cols); pool[i].qs = 1.0f; pool[i].qsum = 0; vs[i] = &pool[i]; }
+        for (int r = 0; r < rows; r++) tdot_multi(&w, r, vs, n, res + (size_t)r * nv + i0, 1);
+    }
+    for (int r = 0; r < rows; r++) for (int i = 0; i < nv; i++) out[(size_t)i * rows + r] = (int32_t)res[(size_t)r * nv + i];
+    free(ones); free(res);
+}
+
+/* maple.c:734: router logits of nb tokens of layer L the way step_batch does (<= 32: route_small) */
+void ref_route_batch(int L, const float *hn, int nb, float *rl) {
+    BN = nb; BL = &LY[L];
+    memcpy(HNB, hn, sizeof(float) * (size_t)nb * H);
+    if (nb <= 32) run(job_route_small, NULL, NE); else run(job_route_multi, NULL, (nb + 7) / 8);
+    memcpy(rl, RLG, sizeof(float) * (size_t)nb * NE);
+}
+/* maple.c:609: decode router, bf_row per expert */
+void ref_route_step(int L, const float *hn, float *rl) {
+    for (int e = 0; e < NE; e++) rl[e] = bf_row(&LY[L].router, e, hn);
+}
+/* maple.c:910-923 */
+void ref_topk(const float *rl, int nb, int32_t *top, float *tw) {
+    memcpy(RLG, rl, sizeof(float) * (size_t)nb * NE);
+    run(job_topk, NULL, nb);
+    memcpy(top, TOPB, sizeof(int) * (size_t)nb * TOPK);
+    memcpy(tw, TWB, sizeof(float) * (size_t)nb * TOPK);
+}
+/* maple.c:924-938 + 1018-1019, on TOPB/TWB given by the caller */
+int ref_group(const int32_t *top, const float *tw, int nb, int *nu, int32_t *ue, int32_t *ustart,
+              int32_t *utok, float *uw, int32_t *tp) {
+    memcpy(TOPB, top, sizeof(int) * (size_t)nb * TOPK);
+    memcpy(TWB, tw, sizeof(float) * (size_t)nb * TOPK);
+    int pos[BMAX]; for (int b = 0; b < nb; b++) pos[b] = b;
+    int na = group_pairs(nb, pos, 0);
+    *nu = NU;
+    memcpy(ue, UE, sizeof(int) * NU); memcpy(ustart, USTART, sizeof(int) * (NU + 1));
+    memcpy(utok, UTOK, sizeof(int) * na); memcpy(uw, UW, sizeof(float) * na);
+    int fl[BMAX]; memset(fl, 0, sizeof(int) * nb);
+    for (int a = 0; a < na; a++) { int b = UTOK[a]; tp[b * TOPK + fl[b]++] = a; }
+    return na;
+}
+/* maple.c:398-402 */
+void ref_rmsnorm(const float *x, const uint16_t *w, int n, float *out) {
+    BF bw = {w, 1, n};
+    rmsnorm(out, x, &bw, n);
+}
+/* the act loop maple.c:825-830 */
+void ref_act(const float *G, const float *U, float *act, int n) {
+    for (int k = 0; k < n; k++) {
+        float g = G[k] < 7.0f ? G[k] : 7.0f, u = U[k];
+        u = u < -7.0f ? -7.0f : (u > 7.0f ? 7.0f : u);
+        act[k] = g / (1.0f + expf(-g)) * u;
+    }
+}
+
+/* The MoE block of step_batch (maple.c:733-755, 824-834) for layer L: hn[nb][2048] post-norm input,
+ * x[nb][2048] updated in place. Optional outputs as in the oracle's mo_trace (NULL = skip). */
+void ref_moe_batch(int L, const float *hn, int nb, float *x, float *rl_out, int32_t *top_out, float *tw_out,
+                   int *nu_out, int32_t *ue_out, int32_t *ustart_out, int32_t *utok_out, float *uw_out,
+                   float *gate_out, float *up_out, float *act_out, int8_t *qa_out, float *qsa_out, float *down_out) {
+    BN = nb; BL = &LY[L];
+    memcpy(HNB, hn, sizeof(float) * (size_t)nb * H);
+    for (int b = 0; b < nb; b++) prep(&VHB[b], HNB[b], H);
+    if (nb <= 32) run(job_route_small, NULL, NE); else run(job_route_multi, NULL, (nb + 7) / 8);
+    if (rl_out) memcpy(rl_out, RLG, sizeof(float) * (size_t)nb * NE);
+    run(job_topk, NULL, nb);
+    if (top_out) memcpy(top_out, TOPB, sizeof(int) * (size_t)nb * TOPK);
+    if (tw_out) memcpy(tw_out, TWB, sizeof(float) * (size_t)nb * TOPK);
+    int pos[BMAX]; for (int b = 0; b < nb; b++) pos[b] = b;
+    int na = group_pairs(nb, pos, L);
+    if (nu_out) *nu_out = NU;
+    if (ue_out) memcpy(ue_out, UE, sizeof(int) * NU);
+    if (ustart_out) memcpy(ustart_out, USTART, sizeof(int) * (NU + 1));
+    if (utok_out) memcpy(utok_out, UTOK, sizeof(int) * na);
+    if (uw_out) memcpy(uw_out, UW, sizeof(float) * na);
+    run(jobB_gateup, NULL, NU * 2 * FF);
+    for (int a = 0; a < na; a++) {
+        ref_act(GATEB[a], UPB[a], ACTB[a], FF);
+        prep(&VAB[a], ACTB[a], FF);
+    }
+    run(jobB_down, NULL, NU * H);
+    for (int a = 0; a < na; a++) { float *xb = x + (size_t)UTOK[a] * H; for (int i = 0; i < H; i++) xb[i] += UW[a] * DOWNB[a][i]; }
+    if (gate_out) memcpy(gate_out, GATEB, sizeof(float) * (size_t)na * FF);
+    if (up_out) memcpy(up_out, UPB, sizeof(float) * (size_t)na * FF);
+    if (act_out) memcpy(act_out, ACTB, sizeof(float) * (size_t)na * FF);
+    if (qa_out) for (int a = 0; a < na; a++) memcpy(qa_out + (size_t)a * FF, VAB[a].q, FF);
+    if (qsa_out) for (int a = 0; a < na; a++) qsa_out[a] = VAB[a].qs;
+    if (down_out) memcpy(down_out, DOWNB, sizeof(float) * (size_t)na * H);
+}
+
+/* The MoE block of step() (maple.c:606-665, no expert cache) for layer L: one token. */
+void ref_moe_step(int L, const float *hn, float *x, float *rl_out, int32_t *top_out, float *tw_out,
+                  float *act_out, float *down_out) {
+    const Layer *l = &LY[L];
+    memcpy(HN, hn, sizeof(float) * H);
+    prep(&V_H, HN, H);
+    for (int e = 0; e < NE; e++) RLG[0][e] = bf_row(&l->router, e, HN);
+    if (rl_out) memcpy(rl_out, RLG[0], sizeof(float) * NE);
+    run(job_topk, NULL, 1);
+    for (int s = 0; s < TOPK; s++) { TOPI[s] = TOPB[0][s]; TOPW[s] = TWB[0][s]; }
+    if (top_out) memcpy(top_out, TOPI, sizeof TOPI);
+    if (tw_out) memcpy(tw_out, TOPW, sizeof TOPW);
+    run(job_gateup, (void *)l, TOPK * 2 * FF);
+    for (int s = 0; s < TOPK; s++) { ref_act(GATE[s], UP[s], ACT[s], FF); prep(&V_A[s], ACT[s], FF); }
+    run(job_down, (void *)l, TOPK * H);
+    for (int i = 0; i < H; i++) { float y = 0; for (int s = 0; s < TOPK; s++) y += TOPW[s] * DOWN[s][i]; x[i] += y; }
+    if (act_out) memcpy(act_out, ACT, sizeof(float) * TOPK * FF);
+    if (down_out) memcpy(down_out, DOWN, sizeof(float) * TOPK * H);
+}
+
+/* Wall-clock helper for the CPU baseline (maple.c:47) */
+double ref_now(void) { return now(); }
