@@ -157,7 +157,10 @@ def main():
     kt = prof_pass(step_plain, 5)
     for k, (tot, n) in sorted(kt.items(), key=lambda kv: -kv[1][0]):
         log(f"  {k:10s} {tot / n * 1e3:8.2f} us avg x {n}")
-    gu_ms = kt["gateup"][0] / kt["gateup"][1]
+    step_plain(); lib.mmoe_sync()
+    gu_ms = lib.mmoe_bench_stage(5, 200)  # k_gateup of the last layer, back to back
+    dn_ms = lib.mmoe_bench_stage(7, 200)
+    log(f"  back-to-back: gateup {gu_ms * 1e3:.2f} us, down {dn_ms * 1e3:.2f} us per launch")
     gu_bytes = 8 * GU_BYTES_PER_EXPERT
     roof = dict(bound="hbm", kernel="k_gateup (decode, 8 experts x 1024 rows)", achieved=round(gu_bytes / gu_ms / 1e6, 1),
                 peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gu_bytes / gu_ms / 1e6 / HBM_PEAK_GBS, 4), traffic=None,
@@ -170,8 +173,10 @@ def main():
         LP = 40
         rw = M.synth_router(SEED, 0, dist=0)
         regs = np.array([rids[0], -1, -1, -1], np.int32)
-        M.check(lib.mmoe_set_layer(LP, M.ptr(M.block_loc()), M.ptr(regs), M.ptr(rw), None), "set_layer")
-        M.check(lib.mmoe_set_bias(LP, M.ptr(M.zipf_bias(SEED, 1.1))), "bias")
+        loc = M.block_loc()
+        zb = M.zipf_bias(SEED, 1.1)
+        M.check(lib.mmoe_set_layer(LP, M.ptr(loc), M.ptr(regs), M.ptr(rw), None), "set_layer")
+        M.check(lib.mmoe_set_bias(LP, M.ptr(zb)), "bias")
         T = 2048
         xs = M.synth_hidden(SEED, 2, T)
         hn = xs / np.sqrt((xs.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6).astype(np.float32)
@@ -190,7 +195,11 @@ def main():
         pk = prof_pass(pstep, 3)
         for k, (tot, n) in sorted(pk.items(), key=lambda kv: -kv[1][0]):
             log(f"  {k:10s} {tot / n * 1e3:8.2f} us avg x {n}")
-        g_ms = pk["gateup"][0] / pk["gateup"][1]
+        pstep(); lib.mmoe_sync()
+        g_ms = lib.mmoe_bench_stage(5, 20)
+        d_ms = lib.mmoe_bench_stage(7, 20)
+        log(f"  back-to-back: gateup {g_ms * 1e3:.2f} us ({T * 8 * OPS_GU_PER_PAIR / g_ms / 1e9:.0f} TOPS), "
+            f"down {d_ms * 1e3:.2f} us ({T * 8 * OPS_DN_PER_PAIR / d_ms / 1e9:.0f} TOPS)")
         g_ops = T * 8 * OPS_GU_PER_PAIR
         prefill = dict(workload="config 2: 2048-token prefill chunk, 1 MoE layer, Zipf(1.1) expert bias",
                        value=round(T / pms * 1e3, 1), unit="tokens/s", ms_per_layer=round(pms, 4),

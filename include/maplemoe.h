@@ -167,6 +167,9 @@ void *mmoe_stream(void);
 #define MMOE_K_COMBINE 8
 #define MMOE_PROF_NKERNELS 9
 int mmoe_event_record(int slot);
+/* Re-launch one stage (MMOE_K_GATEUP, _DOWN, _QUANT_ACT, _ROUTER) of the last main-context call reps times
+ * back to back between two events; returns average ms per launch, or -1.0. */
+double mmoe_bench_stage(int kid, int reps);
 double mmoe_event_elapsed_ms(void);
 int mmoe_prof(int on);
 int mmoe_prof_reset(void);

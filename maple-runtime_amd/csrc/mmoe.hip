@@ -166,20 +166,24 @@ static int stage_quant_x(Work &w, const float *d_hn, int nb) {
 }
 
 // gate/up (+SiLU), act quantisation, down for np pairs under w.plan / w.eptr / w.utok
+static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; } LAST;
+
+static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
+    if (tn == 64) return launch(MMOE_K_GATEUP, [&] { k_gateup<64, 4, 2><<<dim3(maxtiles, MFF / 128), 256, 0, S.st>>>(w.plan, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
+    return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<dim3(maxtiles, MFF / 16), 64, 0, S.st>>>(w.plan, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
+}
+static int launch_down(Work &w, int maxtiles, int tn, int *dd) {
+    if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down<64, 4, 4><<<dim3(maxtiles, MH / 256), 256, 0, S.st>>>(w.plan, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
+    return launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<dim3(maxtiles, MH / 64), 64, 0, S.st>>>(w.plan, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
+}
+
 static int stage_experts(Work &w, int np, int nu_max, int tn) {
+    LAST.w = &w; LAST.np = np; LAST.nu_max = nu_max; LAST.tn = tn;
     int maxtiles = np / tn + (nu_max < np ? nu_max : np);
     int *dg = S.debug ? w.dbg_gu : nullptr, *dd = S.debug ? w.dbg_dn : nullptr;
-    if (tn == 64) {
-        if (launch(MMOE_K_GATEUP, [&] { k_gateup<64, 4, 2><<<dim3(maxtiles, MFF / 128), 256, 0, S.st>>>(w.plan, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); })) return -1;
-    } else {
-        if (launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<dim3(maxtiles, MFF / 16), 64, 0, S.st>>>(w.plan, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); })) return -1;
-    }
+    if (launch_gateup(w, maxtiles, tn, dg)) return -1;
     if (launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(np + 3) / 4, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); })) return -1;
-    if (tn == 64) {
-        if (launch(MMOE_K_DOWN, [&] { k_down<64, 4, 4><<<dim3(maxtiles, MH / 256), 256, 0, S.st>>>(w.plan, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); })) return -1;
-    } else {
-        if (launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<dim3(maxtiles, MH / 64), 64, 0, S.st>>>(w.plan, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); })) return -1;
-    }
+    if (launch_down(w, maxtiles, tn, dd)) return -1;
     return 0;
 }
 
@@ -194,6 +198,7 @@ static int moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) {
     if (nb < 1 || nb > w.maxtok) { seterr("nb %d outside 1..%d (mmoe_init)", nb, w.maxtok); return -1; }
     if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("layer %d not set (mmoe_set_layer)", L); return -1; }
     int np = nb * MTOPK, tn = tile_tn(np);
+    LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = d_hn;
     if (stage_router(w, L, d_hn, nb, order)) return -1;
     if (stage_route_group(w, L, nb, tn)) return -1;
     if (stage_quant_x(w, d_hn, nb)) return -1;
@@ -580,6 +585,29 @@ double mmoe_event_elapsed_ms(void) {
     float ms = 0; if (hipEventElapsedTime(&ms, S.pe[0], S.pe[1]) != hipSuccess) return -1.0;
     return ms;
 }
+// Re-launch one stage of the last mmoe_moe / mmoe_moe_dev / gpre_moe call `reps` times back to back between
+// two events; returns the average milliseconds per launch (the stages are idempotent on their inputs).
+double mmoe_bench_stage(int kid, int reps) {
+    if (!LAST.w || reps < 1 || S.prof) { seterr("mmoe_bench_stage: nothing to repeat"); return -1.0; }
+    Work &w = *LAST.w;
+    int maxtiles = LAST.np / LAST.tn + (LAST.nu_max < LAST.np ? LAST.nu_max : LAST.np);
+    if (hipEventRecord(S.pe[0], S.st) != hipSuccess) return -1.0;
+    for (int i = 0; i < reps; i++) {
+        int rc = 0;
+        switch (kid) {
+            case MMOE_K_GATEUP: rc = launch_gateup(w, maxtiles, LAST.tn, nullptr); break;
+            case MMOE_K_DOWN: rc = launch_down(w, maxtiles, LAST.tn, nullptr); break;
+            case MMOE_K_QUANT_ACT: rc = launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(LAST.np + 3) / 4, 256, 0, S.st>>>(w.act, LAST.np, w.qa, w.qsa, w.qsuma); }); break;
+            case MMOE_K_ROUTER: rc = LAST.hn ? stage_router(w, LAST.L, LAST.hn, LAST.nb, LAST.order) : -1; break;
+            default: seterr("mmoe_bench_stage: kernel %d not repeatable", kid); return -1.0;
+        }
+        if (rc) return -1.0;
+    }
+    if (hipEventRecord(S.pe[1], S.st) != hipSuccess || hipEventSynchronize(S.pe[1]) != hipSuccess) return -1.0;
+    float ms = 0; (void)hipEventElapsedTime(&ms, S.pe[0], S.pe[1]);
+    return ms / reps;
+}
+
 int mmoe_prof(int on) { S.prof = on != 0; return 0; }
 int mmoe_prof_reset(void) { memset(S.prof_ms, 0, sizeof S.prof_ms); memset(S.prof_n, 0, sizeof S.prof_n); return 0; }
 int mmoe_prof_get(int kid, double *ms_total, long *count) {

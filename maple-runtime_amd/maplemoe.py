@@ -61,7 +61,7 @@ def _declare(L):
         "mmoe_read": (i, [i, vp, sz]), "mmoe_set_debug": (i, [i]), "mmoe_last_error": (C.c_char_p, []),
         "mmoe_dev_alloc": (vp, [sz]), "mmoe_dev_free": (i, [vp]), "mmoe_h2d": (i, [vp, vp, sz]),
         "mmoe_d2h": (i, [vp, vp, sz]), "mmoe_d2d": (i, [vp, vp, sz]), "mmoe_sync": (i, []), "mmoe_stream": (vp, []),
-        "mmoe_event_record": (i, [i]), "mmoe_event_elapsed_ms": (d, []), "mmoe_prof": (i, [i]),
+        "mmoe_event_record": (i, [i]), "mmoe_bench_stage": (d, [i, i]), "mmoe_event_elapsed_ms": (d, []), "mmoe_prof": (i, [i]),
         "mmoe_prof_reset": (i, []), "mmoe_prof_get": (i, [i, C.POINTER(C.c_double), C.POINTER(C.c_long)]),
         "mmoe_device_info": (i, [C.c_char_p, i, ip, ip]),
         "mmoe_synth_expert": (None, [u64, i, i, vp, vp, vp, vp, vp, vp]), "mmoe_synth_expert_bytes": (sz, []),
@@ -74,6 +74,7 @@ def _declare(L):
 
 
 def ptr(a):
+    """data pointer of a numpy array; the caller must keep the array referenced until the call returns"""
     return None if a is None else C.c_void_p(a.ctypes.data)
 
 
@@ -143,7 +144,9 @@ def register_layer(L, blk, router, post_ln=None):
     if rid < 0:
         raise RuntimeError("gpre_region: " + lib().mmoe_last_error().decode())
     regs = np.array([rid, -1, -1, -1], np.int32)
-    check(lib().mmoe_set_layer(L, ptr(block_loc()), ptr(regs), ptr(np.ascontiguousarray(router)), ptr(post_ln)), "mmoe_set_layer")
+    loc = block_loc()  # keep every array alive across the call
+    rw = np.ascontiguousarray(router)
+    check(lib().mmoe_set_layer(L, ptr(loc), ptr(regs), ptr(rw), ptr(post_ln)), "mmoe_set_layer")
     return rid
 
 

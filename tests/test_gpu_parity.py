@@ -104,8 +104,9 @@ def test_gpre_moe(layer0):
     loc = M.block_loc(0, list(g["ue"]))
     regs = np.array([layer0.rid, -1, -1, -1], np.int32)
     y = np.zeros((nb, 2048), np.float32)
+    tp = np.ascontiguousarray(g["tp"])
     sec = lib.gpre_moe(M.ptr(hn), nb, nu, M.ptr(loc), M.ptr(regs), None, M.ptr(g["ustart"]), M.ptr(g["utok"]),
-                       M.ptr(g["uw"]), M.ptr(np.ascontiguousarray(g["tp"])), M.ptr(y))
+                       M.ptr(g["uw"]), M.ptr(tp), M.ptr(y))
     assert sec >= 0, lib.mmoe_last_error()
     import ctypes as C
     exu = (O.Expert * nu)(*[layer0.table[int(e)] for e in g["ue"]])
