@@ -17,8 +17,20 @@
 
 static int REF_WORKERS;
 
+/* A maple.c executable linked with -ffast-math starts with flush-to-zero and denormals-are-zero set
+ * (crtfastmath). This library is linked without it so that it does not change the floating-point mode of
+ * the process that loads it; instead every ref_* entry point runs maple.c's code under FTZ/DAZ and restores
+ * the caller's mode on return. Worker threads inherit the mode from ref_set_threads. */
+#include <xmmintrin.h>
+#define FAST_ENTER unsigned int csr_saved_ = _mm_getcsr(); _mm_setcsr(csr_saved_ | 0x8040u)
+#define FAST_LEAVE _mm_setcsr(csr_saved_)
+
+/* maple.c starts NT = 4 (maple.c:85) and main() spawns the workers; without main, run() must not wait for
+ * workers that do not exist, so the library starts single-threaded until ref_set_threads. */
+__attribute__((constructor)) static void ref_single_thread(void) { NT = 1; }
+
 /* maple.c:1095 starts NT-1 spinning workers; the caller thread takes the first slice of each job */
-int ref_set_threads(int nt) {
+static int ref_set_threads_impl(int nt) {
     if (nt < 1) nt = 1;
     if (REF_WORKERS) return NT;  /* workers are started once, like maple.c's main */
     NT = nt;
@@ -27,29 +39,48 @@ int ref_set_threads(int nt) {
     REF_WORKERS = NT > 1;
     return NT;
 }
+int ref_set_threads(int nt) {
+    FAST_ENTER;
+    int r_ = ref_set_threads_impl(nt);
+    FAST_LEAVE;
+    return r_;
+}
 
 /* Point layer L's router and experts at caller memory (maple.c:61-81 does this from layout.bin) */
-void ref_set_router(int L, const uint16_t *w) { LY[L].router.p = w; LY[L].router.rows = NE; LY[L].router.cols = H; }
+void ref_set_router(int L, const uint16_t *w) {
+    FAST_ENTER;
+    LY[L].router.p = w; LY[L].router.rows = NE; LY[L].router.cols = H;
+    FAST_LEAVE;
+}
 void ref_set_expert(int L, int e, const uint8_t *gc, const float *gs, const uint8_t *uc, const float *us,
                     const uint8_t *dc, const float *ds) {
+    FAST_ENTER;
     Layer *l = &LY[L];
     l->eg[e] = (T2){gc, gs, FF, H};
     l->eu[e] = (T2){uc, us, FF, H};
     l->ed[e] = (T2){dc, ds, H, FF};
+    FAST_LEAVE;
 }
 
 /* maple.c:183-194 */
-float ref_prep(const float *x, int n, int8_t *q, int32_t *qsum) {
+static float ref_prep_impl(const float *x, int n, int8_t *q, int32_t *qsum) {
     static Vin v;
     prep(&v, x, n);
     memcpy(q, v.q, (size_t)n);
     *qsum = v.qsum;
     return v.qs;
 }
+float ref_prep(const float *x, int n, int8_t *q, int32_t *qsum) {
+    FAST_ENTER;
+    float r_ = ref_prep_impl(x, n, q, qsum);
+    FAST_LEAVE;
+    return r_;
+}
 
 /* maple.c:423-458 tdot_multi with qs = 1, qsum = 0 and unit row scale: the fp32 result is the exact
  * integer sum of code*q (|sum| < 2^24). rows x cols codes, nv int8 vectors (each cols long). */
 void ref_dot_i32(const uint8_t *codes, int rows, int cols, const int8_t *q, int nv, int32_t *out) {
+    FAST_ENTER;
     static Vin *vs[BMAX]; static Vin pool[64];
     float *ones = malloc(sizeof(float) * rows), *res = malloc(sizeof(float) * (size_t)rows * nv);
     for (int r = 0; r < rows; r++) ones[r] = 1.0f;
@@ -61,28 +92,35 @@ void ref_dot_i32(const uint8_t *codes, int rows, int cols, const int8_t *q, int 
     }
     for (int r = 0; r < rows; r++) for (int i = 0; i < nv; i++) out[(size_t)i * rows + r] = (int32_t)res[(size_t)r * nv + i];
     free(ones); free(res);
+    FAST_LEAVE;
 }
 
 /* maple.c:734: router logits of nb tokens of layer L the way step_batch does (<= 32: route_small) */
 void ref_route_batch(int L, const float *hn, int nb, float *rl) {
+    FAST_ENTER;
     BN = nb; BL = &LY[L];
     memcpy(HNB, hn, sizeof(float) * (size_t)nb * H);
     if (nb <= 32) run(job_route_small, NULL, NE); else run(job_route_multi, NULL, (nb + 7) / 8);
     memcpy(rl, RLG, sizeof(float) * (size_t)nb * NE);
+    FAST_LEAVE;
 }
 /* maple.c:609: decode router, bf_row per expert */
 void ref_route_step(int L, const float *hn, float *rl) {
+    FAST_ENTER;
     for (int e = 0; e < NE; e++) rl[e] = bf_row(&LY[L].router, e, hn);
+    FAST_LEAVE;
 }
 /* maple.c:910-923 */
 void ref_topk(const float *rl, int nb, int32_t *top, float *tw) {
+    FAST_ENTER;
     memcpy(RLG, rl, sizeof(float) * (size_t)nb * NE);
     run(job_topk, NULL, nb);
     memcpy(top, TOPB, sizeof(int) * (size_t)nb * TOPK);
     memcpy(tw, TWB, sizeof(float) * (size_t)nb * TOPK);
+    FAST_LEAVE;
 }
 /* maple.c:924-938 + 1018-1019, on TOPB/TWB given by the caller */
-int ref_group(const int32_t *top, const float *tw, int nb, int *nu, int32_t *ue, int32_t *ustart,
+static int ref_group_impl(const int32_t *top, const float *tw, int nb, int *nu, int32_t *ue, int32_t *ustart,
               int32_t *utok, float *uw, int32_t *tp) {
     memcpy(TOPB, top, sizeof(int) * (size_t)nb * TOPK);
     memcpy(TWB, tw, sizeof(float) * (size_t)nb * TOPK);
@@ -95,18 +133,29 @@ int ref_group(const int32_t *top, const float *tw, int nb, int *nu, int32_t *ue,
     for (int a = 0; a < na; a++) { int b = UTOK[a]; tp[b * TOPK + fl[b]++] = a; }
     return na;
 }
+int ref_group(const int32_t *top, const float *tw, int nb, int *nu, int32_t *ue, int32_t *ustart,
+              int32_t *utok, float *uw, int32_t *tp) {
+    FAST_ENTER;
+    int r_ = ref_group_impl(top, tw, nb, nu, ue, ustart, utok, uw, tp);
+    FAST_LEAVE;
+    return r_;
+}
 /* maple.c:398-402 */
 void ref_rmsnorm(const float *x, const uint16_t *w, int n, float *out) {
+    FAST_ENTER;
     BF bw = {w, 1, n};
     rmsnorm(out, x, &bw, n);
+    FAST_LEAVE;
 }
 /* the act loop maple.c:825-830 */
 void ref_act(const float *G, const float *U, float *act, int n) {
+    FAST_ENTER;
     for (int k = 0; k < n; k++) {
         float g = G[k] < 7.0f ? G[k] : 7.0f, u = U[k];
         u = u < -7.0f ? -7.0f : (u > 7.0f ? 7.0f : u);
         act[k] = g / (1.0f + expf(-g)) * u;
     }
+    FAST_LEAVE;
 }
 
 /* The MoE block of step_batch (maple.c:733-755, 824-834) for layer L: hn[nb][2048] post-norm input,
@@ -114,6 +163,7 @@ void ref_act(const float *G, const float *U, float *act, int n) {
 void ref_moe_batch(int L, const float *hn, int nb, float *x, float *rl_out, int32_t *top_out, float *tw_out,
                    int *nu_out, int32_t *ue_out, int32_t *ustart_out, int32_t *utok_out, float *uw_out,
                    float *gate_out, float *up_out, float *act_out, int8_t *qa_out, float *qsa_out, float *down_out) {
+    FAST_ENTER;
     BN = nb; BL = &LY[L];
     memcpy(HNB, hn, sizeof(float) * (size_t)nb * H);
     for (int b = 0; b < nb; b++) prep(&VHB[b], HNB[b], H);
@@ -142,11 +192,13 @@ void ref_moe_batch(int L, const float *hn, int nb, float *x, float *rl_out, int3
     if (qa_out) for (int a = 0; a < na; a++) memcpy(qa_out + (size_t)a * FF, VAB[a].q, FF);
     if (qsa_out) for (int a = 0; a < na; a++) qsa_out[a] = VAB[a].qs;
     if (down_out) memcpy(down_out, DOWNB, sizeof(float) * (size_t)na * H);
+    FAST_LEAVE;
 }
 
 /* The MoE block of step() (maple.c:606-665, no expert cache) for layer L: one token. */
 void ref_moe_step(int L, const float *hn, float *x, float *rl_out, int32_t *top_out, float *tw_out,
                   float *act_out, float *down_out) {
+    FAST_ENTER;
     const Layer *l = &LY[L];
     memcpy(HN, hn, sizeof(float) * H);
     prep(&V_H, HN, H);
@@ -162,6 +214,7 @@ void ref_moe_step(int L, const float *hn, float *x, float *rl_out, int32_t *top_
     for (int i = 0; i < H; i++) { float y = 0; for (int s = 0; s < TOPK; s++) y += TOPW[s] * DOWN[s][i]; x[i] += y; }
     if (act_out) memcpy(act_out, ACT, sizeof(float) * TOPK * FF);
     if (down_out) memcpy(down_out, DOWN, sizeof(float) * TOPK * H);
+    FAST_LEAVE;
 }
 
 /* Wall-clock helper for the CPU baseline (maple.c:47) */
