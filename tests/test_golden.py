@@ -46,7 +46,7 @@ def test_moe_batch_fixture(fx):
     assert np.array_equal(o["top"], d["b_top"])                                 # top-8 indices
     assert relmax(o["tw"], d["b_tw"]) < 1e-6
     assert int(o["nu"][0]) == nu and np.array_equal(o["ue"][:nu], d["b_ue"]) and np.array_equal(o["ustart"][:nu + 1], d["b_ustart"])
-    assert np.array_equal(o["utok"], d["b_utok"]) and np.array_equal(o["uw"].view(np.int32), d["b_uw"].view(np.int32))
+    assert np.array_equal(o["utok"], d["b_utok"]) and relmax(o["uw"], d["b_uw"]) < 1e-6
     assert relmax(o["gate"], d["b_gate"]) < 1e-6 and relmax(o["act"], d["b_act"]) < 1e-6
     assert np.array_equal(o["qa"], d["b_qa"])          # no rounding-boundary flips in this fixture
     assert relmax(o["qsa"], d["b_qsa"]) < 1e-6
