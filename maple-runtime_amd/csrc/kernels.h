@@ -24,6 +24,8 @@
 #define MFF 512
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(1))) v4i gptr_u4;   // global-memory 16 bytes (global_load, not flat_load)
 
 struct ExpPtr {  // one expert's six tensors (maple.c:276-277 GLOC order: gate codes/scales, up, down)
     const uint8_t *gc; const float *gs;
@@ -41,35 +43,31 @@ struct Plan {
     int ustart[MNE + 1];    // pair offsets
     int tstart[MNE + 1];    // token-tile offsets
 };
+// One token tile of a grouped launch: used expert, first pair, pairs in the tile (<= TN)
+struct Tile { int u, p0, n, pad; };
 
 __device__ __forceinline__ float bf16f(uint16_t v) { return __uint_as_float((uint32_t)v << 16); }
 
-// exp for fp32 through a fixed fp64 sequence (range reduction by ln2 split in two, Taylor series to r^13 by
-// Horner with FMA, scaling by 2^k), rounded once to fp32. Identical operation-for-operation to the oracle.
-__device__ __forceinline__ float dexp(float xf) {
-    double x = (double)xf;
-    if (x > 100.0) return __int_as_float(0x7f800000);
-    if (x < -110.0) return 0.0f;
-    const double LOG2E = 1.4426950408889634, LN2_HI = 6.93147180369123816490e-01, LN2_LO = 1.90821492927058770002e-10;
-    double k = __builtin_rint(x * LOG2E);
-    double r = __builtin_fma(-k, LN2_HI, x);
-    r = __builtin_fma(-k, LN2_LO, r);
-    double p = 1.0 / 6227020800.0;
-    p = __builtin_fma(p, r, 1.0 / 479001600.0);
-    p = __builtin_fma(p, r, 1.0 / 39916800.0);
-    p = __builtin_fma(p, r, 1.0 / 3628800.0);
-    p = __builtin_fma(p, r, 1.0 / 362880.0);
-    p = __builtin_fma(p, r, 1.0 / 40320.0);
-    p = __builtin_fma(p, r, 1.0 / 5040.0);
-    p = __builtin_fma(p, r, 1.0 / 720.0);
-    p = __builtin_fma(p, r, 1.0 / 120.0);
-    p = __builtin_fma(p, r, 1.0 / 24.0);
-    p = __builtin_fma(p, r, 1.0 / 6.0);
-    p = __builtin_fma(p, r, 0.5);
-    p = __builtin_fma(p, r, 1.0);
-    p = __builtin_fma(p, r, 1.0);
-    double sc = __longlong_as_double((long long)((long long)k + 1023) << 52);
-    return (float)(p * sc);
+// exp in fp32 arithmetic: k = rint(x * log2(e)), r = x - k ln2 with ln2 split in two (two FMAs), Taylor
+// series to r^7 by Horner with FMA, times 2^k in two exponent-field steps. Overflow gives inf, x < -104
+// gives 0. Identical operation-for-operation to the oracle's mo_exp.
+__device__ __forceinline__ float pow2i(int k) { return __uint_as_float((uint32_t)(k + 127) << 23); }
+__device__ __forceinline__ float dexp(float x) {
+    if (x > 88.8f) return __int_as_float(0x7f800000);
+    if (x < -104.0f) return 0.0f;
+    float k = __builtin_rintf(x * 1.44269504f);
+    float r = __builtin_fmaf(-k, 0.693145752f, x);
+    r = __builtin_fmaf(-k, 1.42860677e-06f, r);
+    float p = 1.98412698e-04f;
+    p = __builtin_fmaf(p, r, 1.38888889e-03f);
+    p = __builtin_fmaf(p, r, 8.33333333e-03f);
+    p = __builtin_fmaf(p, r, 4.16666667e-02f);
+    p = __builtin_fmaf(p, r, 1.66666667e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    int ki = (int)k, k1 = ki / 2, k2 = ki - k1;
+    return p * pow2i(k1) * pow2i(k2);
 }
 
 // ---- wave64 reductions (order-free operations only: max, integer sum) ----
@@ -256,11 +254,17 @@ __global__ void __launch_bounds__(256) k_hist(const int *__restrict__ top, int n
 // One block of 256 threads (thread = expert). hist[nchunk][256] -> base[nchunk][256] (first pair slot of
 // chunk c's pairs of expert e) and the plan; eptr_u[u] = layer table entry of expert ue[u] if table given.
 __global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int nchunk, int *__restrict__ base, Plan *__restrict__ plan,
-                                              const ExpPtr *__restrict__ layer_tab, ExpPtr *__restrict__ eptr_u, int tn) {
+                                              const ExpPtr *__restrict__ layer_tab, ExpPtr *__restrict__ eptr_u, int tn,
+                                              Tile *__restrict__ tiles) {
     __shared__ int sc[MNE], su[MNE], st[MNE];
     int e = threadIdx.x;
     int run = 0;
-    for (int c = 0; c < nchunk; c++) { int h = hist[c * MNE + e]; base[c * MNE + e] = run; run += h; }
+    constexpr int MAXCH = (2048 + 63) / 64;          // chunks of 64 tokens at the largest batch
+    int hv[MAXCH];
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) hv[c] = c < nchunk ? hist[c * MNE + e] : 0;   // independent loads
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) if (c < nchunk) { base[c * MNE + e] = run; run += hv[c]; }
     int used = run > 0, nt = (run + tn - 1) / tn;
     sc[e] = run; su[e] = used; st[e] = nt;
     __syncthreads();
@@ -277,6 +281,7 @@ __global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int 
         plan->ustart[uidx] = pstart;
         plan->tstart[uidx] = tstart;
         if (layer_tab) eptr_u[uidx] = layer_tab[e];
+        for (int i = 0; i < nt; i++) tiles[tstart + i] = Tile{uidx, pstart + i * tn, min(tn, run - i * tn), 0};
     }
     for (int c = 0; c < nchunk; c++) base[c * MNE + e] += pstart;
     if (e == MNE - 1) {
@@ -287,22 +292,26 @@ __global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int 
 }
 
 // Block = one chunk of 64 tokens, thread = token. Pair slot of (b, s) = base[chunk][e] + number of earlier
-// tokens of the chunk that picked e. Writes utok/uw (maple.c:934-936), tp (pair ids of token b ascending)
-// and sp (pair id of slot s, for the decode combine order).
+// tokens of the chunk that picked e, counted as popcount of a per-expert 64-bit token mask of the chunk.
+// Writes utok/uw (maple.c:934-936), tp (pair ids of token b ascending) and sp (pair id of slot s, for the
+// decode combine order).
 __global__ void __launch_bounds__(64) k_scatter(const int *__restrict__ top, const float *__restrict__ tw, int nb,
                                                 const int *__restrict__ base, int *__restrict__ utok, float *__restrict__ uw,
                                                 int *__restrict__ tp, int *__restrict__ sp) {
-    __shared__ int tk[64 * MTOPK];
+    __shared__ unsigned long long msk[MNE];
     int c = blockIdx.x, t = threadIdx.x, b = c * 64 + t;
-    for (int s = 0; s < MTOPK; s++) tk[t * MTOPK + s] = b < nb ? top[b * MTOPK + s] : -1;
+    for (int e = t; e < MNE; e += 64) msk[e] = 0ull;
+    __syncthreads();
+    int ex[MTOPK];
+    if (b < nb)
+        for (int s = 0; s < MTOPK; s++) { ex[s] = top[b * MTOPK + s]; atomicOr(&msk[ex[s]], 1ull << t); }
     __syncthreads();
     if (b >= nb) return;
+    unsigned long long below = (1ull << t) - 1ull;
     int a[MTOPK];
     for (int s = 0; s < MTOPK; s++) {
-        int e = tk[t * MTOPK + s], r = 0;
-        for (int o = 0; o < t; o++)
-            for (int q = 0; q < MTOPK; q++) r += tk[o * MTOPK + q] == e;
-        int slot = base[c * MNE + e] + r;
+        int e = ex[s];
+        int slot = base[c * MNE + e] + __popcll(msk[e] & below);
         utok[slot] = b; uw[slot] = tw[b * MTOPK + s];
         a[s] = slot;
         if (sp) sp[b * MTOPK + s] = slot;
@@ -312,10 +321,14 @@ __global__ void __launch_bounds__(64) k_scatter(const int *__restrict__ top, con
 }
 
 // Host-given grouping (gpre_moe / gfull_moe / gpux): plan from ustart; one thread.
-__global__ void k_plan_from_ustart(const int *__restrict__ ustart, int nu, Plan *__restrict__ plan, int tn) {
+__global__ void k_plan_from_ustart(const int *__restrict__ ustart, int nu, Plan *__restrict__ plan, int tn, Tile *__restrict__ tiles) {
     if (threadIdx.x != 0) return;
     int t = 0;
-    for (int u = 0; u < nu; u++) { plan->ue[u] = u; plan->ustart[u] = ustart[u]; plan->tstart[u] = t; t += (ustart[u + 1] - ustart[u] + tn - 1) / tn; }
+    for (int u = 0; u < nu; u++) {
+        int c = ustart[u + 1] - ustart[u];
+        plan->ue[u] = u; plan->ustart[u] = ustart[u]; plan->tstart[u] = t;
+        for (int i = 0; i * tn < c; i++) tiles[t++] = Tile{u, ustart[u] + i * tn, min(tn, c - i * tn), 0};
+    }
     plan->ustart[nu] = ustart[nu]; plan->tstart[nu] = t;
     plan->nu = nu; plan->np = ustart[nu]; plan->ntile_gu = t; plan->tn = tn;
 }
@@ -399,96 +412,114 @@ __device__ __forceinline__ v4i decode_word(uint32_t w) {
     return a;
 }
 
-// Find the token tile: used expert u with tstart[u] <= tile < tstart[u+1] (binary search, nu <= 256).
-__device__ __forceinline__ int find_u(const Plan *plan, int tile) {
-    int lo = 0, hi = plan->nu - 1;
-    while (lo < hi) { int mid = (lo + hi + 1) >> 1; if (plan->tstart[mid] <= tile) lo = mid; else hi = mid - 1; }
-    return lo;
-}
+// Work-item order for the 8 XCDs: the hardware hands consecutive workgroup ids to XCDs round robin, so
+// workgroup id b is mapped to logical item (b % 8) * (n / 8) + b / 8 (n padded to a multiple of 8). Each XCD
+// then walks a contiguous run of logical items; items are ordered (token tile, row block) with the row block
+// fastest, so the tiles of one expert -- sharing its codes -- and the row blocks of one tile -- sharing its
+// activations -- meet in the same XCD's L2.
+__device__ __forceinline__ int xcd_item(int b, int n) { return (b & 7) * (n >> 3) + (b >> 3); }
 
 // Gate+up with fused SiLU*up (maple.c:471-479, 825-830). Block = WAVES waves; wave w owns RF 16-row
 // fragments of gate rows and the same RF fragments of up rows; the block covers WAVES*RF*16 rows of both.
-// Grid: x = token tile (early exit beyond plan->ntile_gu), y = row block. TN tokens per tile (16 or 64).
-// Activations of the tile's tokens are staged in LDS 256 columns at a time (double buffered).
-template <int TN, int WAVES, int RF>
-__global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ plan, const ExpPtr *__restrict__ eptr,
+// 1-D grid of (token tile x row block) items, n = gridDim.x (multiple of 8); items past the plan exit.
+//
+// Pipeline over the 8 chunks of 256 columns, two chunks deep, ordinary loads only:
+//   iteration ch: barrier; issue the loads of chunk ch+2 (code words into a 3-deep register ring, the tile's
+//   activation pieces into a 2-deep register ring); MFMAs of chunk ch (codes from registers, activations from
+//   LDS stage ch%2); store the activation pieces of chunk ch+1 into LDS stage (ch+1)%2.
+// LDS activation rows: token tk, 256 bytes, its 16-byte part p at slot p ^ (tk & 15), so the 16 lanes that
+// read one B fragment (16 tokens, one part) hit 16 different banks. Padding tokens of a partial tile load a
+// valid token's row; their result columns are never stored. MODE is an experiment knob (0 = normal).
+template <int TN, int WAVES, int RF, int MODE = 0>
+__global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
+                                                        const ExpPtr *__restrict__ eptr,
                                                         const int *__restrict__ utok, const int8_t *__restrict__ qx,
                                                         const float *__restrict__ qsx, const int *__restrict__ qsumx,
                                                         float *__restrict__ act, int *__restrict__ dbg) {
     constexpr int NT = WAVES * 64;
-    constexpr int NF = TN / 16;                // token fragments
-    constexpr int LDSW = 256 + 16;             // bytes per token row in LDS (padded)
-    __shared__ __attribute__((aligned(16))) int8_t bs[2][TN * LDSW];
+    constexpr int NF = TN / 16;                 // token fragments
+    constexpr int NA = 2 * RF;                  // code fragments per wave (gate then up)
+    constexpr int RB = MFF / (WAVES * RF * 16);
+    constexpr int NCH = MH / 256;               // 8 chunks of 256 columns
+    constexpr int BB = TN * 256;                // activation bytes per LDS stage
+    constexpr int NPC = (TN * 16 + NT - 1) / NT;  // 16-byte activation pieces per thread per chunk
+    __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
     __shared__ int toks[TN];
-    int tile = blockIdx.x;
+    int item = xcd_item(blockIdx.x, gridDim.x);
+    int tile = item / RB, rb = item % RB;
     if (tile >= plan->ntile_gu) return;
-    int u = find_u(plan, tile);
-    int p0 = plan->ustart[u] + (tile - plan->tstart[u]) * TN;
-    int ntok = min(TN, plan->ustart[u + 1] - p0);
-    ExpPtr ex = eptr[u];
+    Tile tl = tiles[tile];
+    int p0 = tl.p0, ntok = tl.n;
+    ExpPtr ex = eptr[tl.u];
     int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G = l >> 4, r16 = l & 15;
-    if (tid < TN) toks[tid] = tid < ntok ? utok[p0 + tid] : -1;
+    if (tid < TN) toks[tid] = utok[p0 + (tid < ntok ? tid : 0)];
     __syncthreads();
 
-    // B staging: TN tokens x 256 bytes per chunk; each thread moves 16-byte pieces
-    auto stage = [&](int chunk, int buf) {
-        for (int i = tid; i < TN * 16; i += NT) {
-            int tk = i >> 4, part = i & 15;
-            int tok = toks[tk];
-            uint4 v = make_uint4(0, 0, 0, 0);
-            if (tok >= 0) v = *(const uint4 *)(qx + (size_t)tok * MH + chunk * 256 + part * 16);
-            *(uint4 *)(&bs[buf][tk * LDSW + part * 16]) = v;
-        }
-    };
-    // A rows of this lane
-    int rowblk = blockIdx.y * (WAVES * RF * 16) + wv * RF * 16;
-    const uint8_t *arow[2 * RF];
+    // activation pieces of this thread: piece i = tid + k*NT -> token i/16, part i%16 (slot part ^ (tk & 15))
+    const gptr_u4 *bsrc[NPC]; int bdst[NPC];
+#pragma unroll
+    for (int k = 0; k < NPC; k++) {
+        int i = tid + k * NT, tk = (i < TN * 16 ? i : 0) >> 4, part = i & 15;
+        bsrc[k] = (const gptr_u4 *)(qx + (size_t)toks[tk] * MH + part * 16);
+        bdst[k] = i < TN * 16 ? tk * 256 + ((part ^ (tk & 15)) * 16) : -1;
+    }
+    int rowblk = rb * (WAVES * RF * 16) + wv * RF * 16;   // first gate (and up) row of this wave
+    const gptr_u4 *arow[NA];
+    int aoff = (G >> 1) * 32 + (G & 1) * 16;  // byte offset of this lane's 16 code bytes in a 64-byte chunk
 #pragma unroll
     for (int f = 0; f < RF; f++) {
-        arow[f] = ex.gc + (size_t)(rowblk + f * 16 + r16) * (MH / 4);
-        arow[RF + f] = ex.uc + (size_t)(rowblk + f * 16 + r16) * (MH / 4);
+        arow[f] = (const gptr_u4 *)(ex.gc + (size_t)(rowblk + f * 16 + r16) * (MH / 4) + aoff);
+        arow[RF + f] = (const gptr_u4 *)(ex.uc + (size_t)(rowblk + f * 16 + r16) * (MH / 4) + aoff);
     }
-    v4i acc[2 * RF][NF];
+    v4i acc[NA][NF];
 #pragma unroll
-    for (int f = 0; f < 2 * RF; f++)
+    for (int f = 0; f < NA; f++)
 #pragma unroll
         for (int j = 0; j < NF; j++) acc[f][j] = v4i{0, 0, 0, 0};
 
-    uint4 cw[2 * RF];
-    int aoff = (G >> 1) * 32 + (G & 1) * 16;  // byte offset of this lane's 16 code bytes in a 64-byte chunk
+    v4i cw[3][NA];      // code words of chunks ch, ch+1, ch+2
+    v4i br[2][NPC];     // activation pieces of chunks ch+1, ch+2
 #pragma unroll
-    for (int f = 0; f < 2 * RF; f++) cw[f] = *(const uint4 *)(arow[f] + aoff);
-    stage(0, 0);
-    __syncthreads();
-    constexpr int NCH = MH / 256;
+    for (int c = 0; c < 2; c++) {
+#pragma unroll
+        for (int f = 0; f < NA; f++) cw[c][f] = arow[f][c * 4];
+#pragma unroll
+        for (int k = 0; k < NPC; k++) br[c][k] = bsrc[k][c * 16];
+    }
+#pragma unroll
+    for (int k = 0; k < NPC; k++) if (bdst[k] >= 0) *(v4i *)(&bs[0][bdst[k]]) = br[0][k];
+#pragma unroll
     for (int ch = 0; ch < NCH; ch++) {
-        int buf = ch & 1;
-        uint4 cn[2 * RF];
-        if (ch + 1 < NCH) {
+        __syncthreads();                                   // stage ch%2 written by everyone
+        if (ch + 2 < NCH) {
 #pragma unroll
-            for (int f = 0; f < 2 * RF; f++) cn[f] = *(const uint4 *)(arow[f] + (ch + 1) * 64 + aoff);
-            stage(ch + 1, buf ^ 1);
+            for (int f = 0; f < NA; f++) cw[(ch + 2) % 3][f] = arow[f][(ch + 2) * 4];
+            if (MODE != 1) {
+#pragma unroll
+                for (int k = 0; k < NPC; k++) br[ch % 2][k] = bsrc[k][(ch + 2) * 16];
+            }
         }
-        const int8_t *bb = &bs[buf][0];
-        int boff = (G >> 1) * 128 + (G & 1) * 64;
+        const int8_t *sp = &bs[ch % 2][0];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
+            int part = (G >> 1) * 8 + (G & 1) * 4 + t;
             v4i bv[NF];
 #pragma unroll
-            for (int j = 0; j < NF; j++) bv[j] = *(const v4i *)(bb + (j * 16 + r16) * LDSW + boff + t * 16);
+            for (int j = 0; j < NF; j++) bv[j] = *(const v4i *)(sp + (j * 16 + r16) * 256 + ((part ^ r16) * 16));
 #pragma unroll
-            for (int f = 0; f < 2 * RF; f++) {
-                uint32_t w = t == 0 ? cw[f].x : t == 1 ? cw[f].y : t == 2 ? cw[f].z : cw[f].w;
+            for (int f = 0; f < NA; f++) {
+                v4i c4 = cw[ch % 3][f];
+                uint32_t w = (uint32_t)(t == 0 ? c4.x : t == 1 ? c4.y : t == 2 ? c4.z : c4.w);
                 v4i av = decode_word(w);
 #pragma unroll
                 for (int j = 0; j < NF; j++) acc[f][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bv[j], acc[f][j], 0, 0, 0);
             }
         }
         if (ch + 1 < NCH) {
+            __builtin_amdgcn_sched_barrier(0);  // the store (and its wait on chunk ch+1's loads) after the MFMAs
 #pragma unroll
-            for (int f = 0; f < 2 * RF; f++) cw[f] = cn[f];
+            for (int k = 0; k < NPC; k++) if (bdst[k] >= 0) *(v4i *)(&bs[(ch + 1) % 2][bdst[k]]) = br[(ch + 1) % 2][k];
         }
-        __syncthreads();
     }
     // epilogue: G, U -> act
 #pragma unroll
@@ -512,7 +543,139 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
                 float uv = (float)(au[i] - qsum) * qs * suv[i];
                 float g = gv < 7.0f ? gv : 7.0f;
                 float uu = uv < -7.0f ? -7.0f : (uv > 7.0f ? 7.0f : uv);
-                o[i] = g / (1.0f + dexp(-g)) * uu;
+                o[i] = MODE == 3 ? g + uu : g / (1.0f + dexp(-g)) * uu;
+            }
+            *(float4 *)(act + (size_t)pair * MFF + row0) = make_float4(o[0], o[1], o[2], o[3]);
+            if (dbg) {
+                *(int4 *)(dbg + (size_t)pair * 2 * MFF + row0) = make_int4(ag[0], ag[1], ag[2], ag[3]);
+                *(int4 *)(dbg + (size_t)pair * 2 * MFF + MFF + row0) = make_int4(au[0], au[1], au[2], au[3]);
+            }
+        }
+    }
+}
+
+// Gate+up for large token tiles on the 32x32x32 int8 MFMA (v_mfma_i32_32x32x32_i8, twice the rate of the
+// 16x16x64 form on gfx950). Operand mapping: A lane (G2 = lane/32, r = lane%32) holds 16 int8 of row r, B lane
+// (G2, n) the same 16 k positions of token n. Lane group G2 takes 128-column group G2 of each 256-column
+// chunk; at step t (0..7) its A operand is code word t of that group decoded in registers, and its B operand
+// the 16 contiguous bytes 16t.. of the group in mfma order (see the top of this file). D (16 int32 per lane):
+// register i holds row (i/4)*8 + G2*4 + i%4 of the 32-row block, token lane%32.
+// Block = 4 waves; wave w owns 32 gate rows and the same 32 up rows; the block covers 128 of each and TN = 64
+// tokens (2 token fragments of 32). Pipeline as k_gateup: codes two chunks ahead in registers, activations
+// two chunks ahead in registers then LDS (2 stages, slot p ^ (tk & 15) swizzle).
+template <int MODE = 0>
+__global__ void __launch_bounds__(256) k_gateup32(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
+                                                  const ExpPtr *__restrict__ eptr,
+                                                  const int *__restrict__ utok, const int8_t *__restrict__ qx,
+                                                  const float *__restrict__ qsx, const int *__restrict__ qsumx,
+                                                  float *__restrict__ act, int *__restrict__ dbg) {
+    constexpr int TN = 64, NT = 256, NF = 2, NA = 2;
+    constexpr int RB = MFF / 128;
+    constexpr int NCH = MH / 256;
+    constexpr int BB = TN * 256;
+    constexpr int NPC = TN * 16 / NT;          // 4 activation pieces of 16 bytes per thread per chunk
+    __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
+    __shared__ int toks[TN];
+    int item = xcd_item(blockIdx.x, gridDim.x);
+    int tile = item / RB, rb = item % RB;
+    if (tile >= plan->ntile_gu) return;
+    Tile tl = tiles[tile];
+    int p0 = tl.p0, ntok = tl.n;
+    ExpPtr ex = eptr[tl.u];
+    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G2 = l >> 5, r32 = l & 31;
+    if (tid < TN) toks[tid] = utok[p0 + (tid < ntok ? tid : 0)];
+    __syncthreads();
+
+    const gptr_u4 *bsrc[NPC]; int bdst[NPC];
+#pragma unroll
+    for (int k = 0; k < NPC; k++) {
+        int i = tid + k * NT, tk = i >> 4, part = i & 15;
+        bsrc[k] = (const gptr_u4 *)(qx + (size_t)toks[tk] * MH + part * 16);
+        bdst[k] = tk * 256 + ((part ^ (tk & 15)) * 16);
+    }
+    int rowblk = rb * 128 + wv * 32;           // this wave's first gate (and up) row
+    const gptr_u4 *arow[NA];
+    arow[0] = (const gptr_u4 *)(ex.gc + (size_t)(rowblk + r32) * (MH / 4) + G2 * 32);
+    arow[1] = (const gptr_u4 *)(ex.uc + (size_t)(rowblk + r32) * (MH / 4) + G2 * 32);
+    v16i acc[NA][NF];
+#pragma unroll
+    for (int f = 0; f < NA; f++)
+#pragma unroll
+        for (int j = 0; j < NF; j++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
+
+    v4i cw[3][NA][2];   // 32 code bytes per fragment per chunk: chunks ch, ch+1, ch+2
+    v4i br[2][NPC];
+#pragma unroll
+    for (int c = 0; c < 2; c++) {
+#pragma unroll
+        for (int f = 0; f < NA; f++) { cw[c][f][0] = arow[f][c * 4]; cw[c][f][1] = arow[f][c * 4 + 1]; }
+#pragma unroll
+        for (int k = 0; k < NPC; k++) br[c][k] = bsrc[k][c * 16];
+    }
+#pragma unroll
+    for (int k = 0; k < NPC; k++) *(v4i *)(&bs[0][bdst[k]]) = br[0][k];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ch++) {
+        __syncthreads();
+        if (ch + 2 < NCH && MODE != 6 && MODE != 7) {
+#pragma unroll
+            for (int f = 0; f < NA; f++) { cw[(ch + 2) % 3][f][0] = arow[f][(ch + 2) * 4]; cw[(ch + 2) % 3][f][1] = arow[f][(ch + 2) * 4 + 1]; }
+            if (MODE != 1) {
+#pragma unroll
+                for (int k = 0; k < NPC; k++) br[ch % 2][k] = bsrc[k][(ch + 2) * 16];
+            }
+        }
+        const int8_t *sp = &bs[ch % 2][0];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            int part = G2 * 8 + t;
+            v4i bv[NF];
+#pragma unroll
+            for (int j = 0; j < NF; j++) {
+                int tk = j * 32 + r32;
+                bv[j] = (MODE == 5 || MODE == 7) ? cw[ch % 3][j][0] : *(const v4i *)(sp + tk * 256 + ((part ^ (tk & 15)) * 16));
+            }
+#pragma unroll
+            for (int f = 0; f < NA; f++) {
+                v4i c4 = cw[ch % 3][f][t >> 2];
+                int tt = t & 3;
+                uint32_t w = (uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w);
+                v4i av = (MODE == 4 || MODE == 7) ? c4 : decode_word(w);
+                acc[f][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[0], acc[f][0], 0, 0, 0);
+                if (ntok > 32) acc[f][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[1], acc[f][1], 0, 0, 0);
+            }
+        }
+        if (ch + 1 < NCH) {
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst[k]]) = br[(ch + 1) % 2][k];
+        }
+    }
+    // epilogue: G, U -> act. Lane holds token r32 of each token fragment; rows (i/4)*8 + G2*4 + i%4.
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        int tk = j * 32 + r32;
+        if (tk >= ntok) continue;
+        int tok = toks[tk];
+        float qs = qsx[tok]; int qsum = qsumx[tok];
+        int pair = p0 + tk;
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            int row0 = rowblk + g * 8 + G2 * 4;
+            float4 sg = *(const float4 *)(ex.gs + row0), su = *(const float4 *)(ex.us + row0);
+            float sgv[4] = {sg.x, sg.y, sg.z, sg.w}, suv[4] = {su.x, su.y, su.z, su.w};
+            int ag[4], au[4];
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                ag[i] = acc[0][j][g * 4 + i]; au[i] = acc[1][j][g * 4 + i];
+                float gv = (float)(ag[i] - qsum) * qs * sgv[i];
+                float uv = (float)(au[i] - qsum) * qs * suv[i];
+                float gg = gv < 7.0f ? gv : 7.0f;
+                float uu = uv < -7.0f ? -7.0f : (uv > 7.0f ? 7.0f : uv);
+                o[i] = (MODE == 3 || MODE == 7) ? gg + uu : gg / (1.0f + dexp(-gg)) * uu;
             }
             *(float4 *)(act + (size_t)pair * MFF + row0) = make_float4(o[0], o[1], o[2], o[3]);
             if (dbg) {
@@ -525,22 +688,24 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
 
 // Down (maple.c:498-505): D[pair][row] = (float)(sum c*qa - qsuma) * qsa * s_down[row]. Block = WAVES waves
 // of RF 16-row fragments; K = 512 staged in LDS at once. Pairs of a tile are contiguous (no gather).
+// 1-D grid of (token tile x row block) items in XCD order, as k_gateup.
 template <int TN, int WAVES, int RF>
-__global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ plan, const ExpPtr *__restrict__ eptr,
+__global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ plan, const Tile *__restrict__ tiles, const ExpPtr *__restrict__ eptr,
                                                       const int8_t *__restrict__ qa, const float *__restrict__ qsa,
                                                       const int *__restrict__ qsuma, float *__restrict__ down, int *__restrict__ dbg) {
     constexpr int NT = WAVES * 64;
     constexpr int NF = TN / 16;
     constexpr int LDSW = MFF + 16;
+    constexpr int RB = MH / (WAVES * RF * 16);
     __shared__ __attribute__((aligned(16))) int8_t bs[TN * LDSW];
-    int tile = blockIdx.x;
+    int item = xcd_item(blockIdx.x, gridDim.x);
+    int tile = item / RB, rb = item % RB;
     if (tile >= plan->ntile_gu) return;
-    int u = find_u(plan, tile);
-    int p0 = plan->ustart[u] + (tile - plan->tstart[u]) * TN;
-    int ntok = min(TN, plan->ustart[u + 1] - p0);
-    ExpPtr ex = eptr[u];
+    Tile tl = tiles[tile];
+    int p0 = tl.p0, ntok = tl.n;
+    ExpPtr ex = eptr[tl.u];
     int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G = l >> 4, r16 = l & 15;
-    int rowblk = blockIdx.y * (WAVES * RF * 16) + wv * RF * 16;
+    int rowblk = rb * (WAVES * RF * 16) + wv * RF * 16;
     const uint8_t *arow[RF];
 #pragma unroll
     for (int f = 0; f < RF; f++) arow[f] = ex.dc + (size_t)(rowblk + f * 16 + r16) * (MFF / 4);
@@ -597,6 +762,86 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
             *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
             if (dbg) *(int4 *)(dbg + (size_t)pair * MH + row0) = make_int4(ad[0], ad[1], ad[2], ad[3]);
         }
+    }
+}
+
+// Down on the 32x32x32 int8 MFMA (operand mapping as k_gateup32): D[pair][row] = (float)(sum c*qa - qsuma) *
+// qsa * s_down[row]. Block = 4 waves; wave w owns rows w*64 .. +64 of the block's 256 (two 32-row fragments);
+// tile = 64 pairs (contiguous, no gather). K = 512: both chunks' code words are loaded at once, the tile's
+// activations are staged in LDS at once (slot p ^ (tk & 15) swizzle within each 256-byte half).
+__global__ void __launch_bounds__(256) k_down32(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
+                                                const ExpPtr *__restrict__ eptr, const int8_t *__restrict__ qa,
+                                                const float *__restrict__ qsa, const int *__restrict__ qsuma,
+                                                float *__restrict__ down, int *__restrict__ dbg) {
+    constexpr int TN = 64, NT = 256, NF = 2, NA = 2, RB = MH / 256;
+    constexpr int NPC = TN * (MFF / 16) / NT;   // 8 pieces of 16 bytes per thread
+    __shared__ __attribute__((aligned(16))) int8_t bs[TN * MFF];
+    int item = xcd_item(blockIdx.x, gridDim.x);
+    int tile = item / RB, rb = item % RB;
+    if (tile >= plan->ntile_gu) return;
+    Tile tl = tiles[tile];
+    int p0 = tl.p0, ntok = tl.n;
+    ExpPtr ex = eptr[tl.u];
+    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G2 = l >> 5, r32 = l & 31;
+    int rowblk = rb * 256 + wv * 64;
+    v4i cw[NA][2][2];   // [fragment][chunk][16 bytes]
+#pragma unroll
+    for (int f = 0; f < NA; f++) {
+        const gptr_u4 *ar = (const gptr_u4 *)(ex.dc + (size_t)(rowblk + f * 32 + r32) * (MFF / 4) + G2 * 32);
+#pragma unroll
+        for (int c = 0; c < 2; c++) { cw[f][c][0] = ar[c * 4]; cw[f][c][1] = ar[c * 4 + 1]; }
+    }
+#pragma unroll
+    for (int k = 0; k < NPC; k++) {
+        int i = tid + k * NT, tk = i >> 5, part = i & 31;
+        int pr = p0 + (tk < ntok ? tk : 0);
+        v4i v = *(const gptr_u4 *)(qa + (size_t)pr * MFF + part * 16);
+        *(v4i *)(&bs[tk * MFF + ((part ^ (tk & 15)) * 16)]) = v;
+    }
+    __syncthreads();
+    v16i acc[NA][NF];
+#pragma unroll
+    for (int f = 0; f < NA; f++)
+#pragma unroll
+        for (int j = 0; j < NF; j++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            int part = c * 16 + G2 * 8 + t;
+            v4i bv[NF];
+#pragma unroll
+            for (int j = 0; j < NF; j++) { int tk = j * 32 + r32; bv[j] = *(const v4i *)(bs + tk * MFF + ((part ^ (tk & 15)) * 16)); }
+#pragma unroll
+            for (int f = 0; f < NA; f++) {
+                v4i c4 = cw[f][c][t >> 2];
+                int tt = t & 3;
+                v4i av = decode_word((uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w));
+                acc[f][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[0], acc[f][0], 0, 0, 0);
+                if (ntok > 32) acc[f][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[1], acc[f][1], 0, 0, 0);
+            }
+        }
+#pragma unroll
+    for (int j = 0; j < NF; j++) {
+        int tk = j * 32 + r32;
+        if (tk >= ntok) continue;
+        int pair = p0 + tk;
+        float qs = qsa[pair]; int qsum = qsuma[pair];
+#pragma unroll
+        for (int f = 0; f < NA; f++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                int row0 = rowblk + f * 32 + g * 8 + G2 * 4;
+                float4 sd = *(const float4 *)(ex.ds + row0);
+                float sdv[4] = {sd.x, sd.y, sd.z, sd.w};
+                int ad[4]; float o[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) { ad[i] = acc[f][j][g * 4 + i]; o[i] = (float)(ad[i] - qsum) * qs * sdv[i]; }
+                *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
+                if (dbg) *(int4 *)(dbg + (size_t)pair * MH + row0) = make_int4(ad[0], ad[1], ad[2], ad[3]);
+            }
     }
 }
 

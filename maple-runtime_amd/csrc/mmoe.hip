@@ -42,6 +42,7 @@ struct Work {
     float *hn = nullptr, *x = nullptr, *rl = nullptr, *tw = nullptr, *uw = nullptr;
     int *top = nullptr, *hist = nullptr, *base = nullptr, *utok = nullptr, *tp = nullptr, *sp = nullptr, *ustart = nullptr;
     Plan *plan = nullptr;
+    Tile *tiles = nullptr;
     ExpPtr *eptr = nullptr;
     int8_t *qx = nullptr, *qa = nullptr;
     float *qsx = nullptr, *qsa = nullptr, *act = nullptr, *down = nullptr;
@@ -57,7 +58,7 @@ static int work_alloc(Work &w, int maxtok) {
     HC(hipMalloc(&w.hn, T * MH * 4)); HC(hipMalloc(&w.x, T * MH * 4)); HC(hipMalloc(&w.rl, T * MNE * 4));
     HC(hipMalloc(&w.top, T * MTOPK * 4)); HC(hipMalloc(&w.tw, T * MTOPK * 4));
     HC(hipMalloc(&w.hist, (size_t)nch * MNE * 4)); HC(hipMalloc(&w.base, (size_t)nch * MNE * 4));
-    HC(hipMalloc(&w.plan, sizeof(Plan))); HC(hipMalloc(&w.eptr, MNE * sizeof(ExpPtr)));
+    HC(hipMalloc(&w.plan, sizeof(Plan))); HC(hipMalloc(&w.tiles, sizeof(Tile) * ((size_t)w.maxp / 16 + MNE + 8))); HC(hipMalloc(&w.eptr, MNE * sizeof(ExpPtr)));
     HC(hipMalloc(&w.utok, P * 4)); HC(hipMalloc(&w.uw, P * 4)); HC(hipMalloc(&w.tp, P * 4)); HC(hipMalloc(&w.sp, P * 4));
     HC(hipMalloc(&w.ustart, (MNE + 1) * 4));
     HC(hipMalloc(&w.qx, T * MH)); HC(hipMalloc(&w.qsx, T * 4)); HC(hipMalloc(&w.qsumx, T * 4));
@@ -155,7 +156,7 @@ static int stage_route_group(Work &w, int L, int nb, int tn) {
     if (launch(MMOE_K_TOPK, [&] { k_topk<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rl, nb, w.top, w.tw); })) return -1;
     if (launch(MMOE_K_GROUP, [&] {
             k_hist<<<nch, 256, 0, S.st>>>(w.top, nb, w.hist);
-            k_plan<<<1, 256, 0, S.st>>>(w.hist, nch, w.base, w.plan, S.layers[L].tab, w.eptr, tn);
+            k_plan<<<1, 256, 0, S.st>>>(w.hist, nch, w.base, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles);
             k_scatter<<<nch, 64, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp);
         })) return -1;
     return 0;
@@ -168,13 +169,14 @@ static int stage_quant_x(Work &w, const float *d_hn, int nb) {
 // gate/up (+SiLU), act quantisation, down for np pairs under w.plan / w.eptr / w.utok
 static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; } LAST;
 
+static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8); }  // xcd_item needs a multiple of 8
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
-    if (tn == 64) return launch(MMOE_K_GATEUP, [&] { k_gateup<64, 4, 2><<<dim3(maxtiles, MFF / 128), 256, 0, S.st>>>(w.plan, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
-    return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<dim3(maxtiles, MFF / 16), 64, 0, S.st>>>(w.plan, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
+    if (tn == 64) return launch(MMOE_K_GATEUP, [&] { k_gateup32<0><<<grid8(maxtiles * (MFF / 128)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
+    return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<grid8(maxtiles * (MFF / 16)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
 static int launch_down(Work &w, int maxtiles, int tn, int *dd) {
-    if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down<64, 4, 4><<<dim3(maxtiles, MH / 256), 256, 0, S.st>>>(w.plan, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
-    return launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<dim3(maxtiles, MH / 64), 64, 0, S.st>>>(w.plan, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
+    if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down32<<<grid8(maxtiles * (MH / 256)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
+    return launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<grid8(maxtiles * (MH / 64)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
 }
 
 static int stage_experts(Work &w, int np, int nu_max, int tn) {
@@ -222,7 +224,7 @@ static int experts_host_grouping(Work &w, int nb, int nu, const ExpPtr *eptr_h, 
     HC(hipMemcpyAsync(w.utok, ptok, sizeof(int) * np, hipMemcpyHostToDevice, S.st));
     if (pw) HC(hipMemcpyAsync(w.uw, pw, sizeof(float) * np, hipMemcpyHostToDevice, S.st));
     if (tp) HC(hipMemcpyAsync(w.tp, tp, sizeof(int) * nb * MTOPK, hipMemcpyHostToDevice, S.st));
-    if (launch(MMOE_K_GROUP, [&] { k_plan_from_ustart<<<1, 64, 0, S.st>>>(w.ustart, nu, w.plan, tn); })) return -1;
+    if (launch(MMOE_K_GROUP, [&] { k_plan_from_ustart<<<1, 64, 0, S.st>>>(w.ustart, nu, w.plan, tn, w.tiles); })) return -1;
     if (stage_quant_x(w, w.hn, nb)) return -1;
     return stage_experts(w, np, nu, tn);
 }

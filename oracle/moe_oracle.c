@@ -104,34 +104,28 @@ void mo_router_step(const float *hn, const uint16_t *w, const float *bias, float
     }
 }
 
-/* exp(x) for fp32 x: k = rint(x / ln2), r = x - k ln2 (two FMAs, split ln2), Taylor series to r^13
- * (|r| <= 0.35, truncation < 1e-17 relative) by Horner with FMA, times 2^k, rounded once to fp32.
- * The GPU kernels run the identical operation sequence, so both sides produce the same bits. */
-float mo_exp(float xf) {
-    double x = (double)xf;
-    if (x > 100.0) return (float)INFINITY;
-    if (x < -110.0) return 0.0f;
-    const double LOG2E = 1.4426950408889634, LN2_HI = 6.93147180369123816490e-01, LN2_LO = 1.90821492927058770002e-10;
-    double k = rint(x * LOG2E);
-    double r = fma(-k, LN2_HI, x);
-    r = fma(-k, LN2_LO, r);
-    double p = 1.0 / 6227020800.0;
-    p = fma(p, r, 1.0 / 479001600.0);
-    p = fma(p, r, 1.0 / 39916800.0);
-    p = fma(p, r, 1.0 / 3628800.0);
-    p = fma(p, r, 1.0 / 362880.0);
-    p = fma(p, r, 1.0 / 40320.0);
-    p = fma(p, r, 1.0 / 5040.0);
-    p = fma(p, r, 1.0 / 720.0);
-    p = fma(p, r, 1.0 / 120.0);
-    p = fma(p, r, 1.0 / 24.0);
-    p = fma(p, r, 1.0 / 6.0);
-    p = fma(p, r, 0.5);
-    p = fma(p, r, 1.0);
-    p = fma(p, r, 1.0);
-    union { uint64_t u; double d; } sc;
-    sc.u = (uint64_t)((int64_t)k + 1023) << 52;
-    return (float)(p * sc.d);
+/* exp(x) in fp32 arithmetic: k = rint(x * log2(e)), r = x - k ln2 with ln2 split in two (two FMAs, exact
+ * for |k| < 2^12), exp(r) by its Taylor series to r^7 (|r| <= 0.347: truncation 6e-9 relative) by Horner with
+ * FMA, then times 2^k as exponent-field arithmetic in two steps (2^(k/2) * 2^(k - k/2)) so that results in
+ * the subnormal range are rounded once more like any product. Overflow gives inf, x < -104 gives 0.
+ * The HIP kernels run the identical operation sequence, so both sides produce the same bits. */
+static inline float pow2i(int k) { union { uint32_t u; float f; } c; c.u = (uint32_t)(k + 127) << 23; return c.f; }
+float mo_exp(float x) {
+    if (x > 88.8f) return (float)INFINITY;
+    if (x < -104.0f) return 0.0f;
+    float k = rintf(x * 1.44269504f);
+    float r = fmaf(-k, 0.693145752f, x);
+    r = fmaf(-k, 1.42860677e-06f, r);
+    float p = 1.98412698e-04f;
+    p = fmaf(p, r, 1.38888889e-03f);
+    p = fmaf(p, r, 8.33333333e-03f);
+    p = fmaf(p, r, 4.16666667e-02f);
+    p = fmaf(p, r, 1.66666667e-01f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int ki = (int)k, k1 = ki / 2, k2 = ki - k1;
+    return p * pow2i(k1) * pow2i(k2);
 }
 
 /* maple.c:910-923 */

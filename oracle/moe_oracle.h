@@ -14,7 +14,7 @@
  *   mo_prep                maple.c built here (oracle/_ref) on 10^5 vectors, bit-exact; x=0 special case
  *   mo_dot_i32             brute force sum (c-1)*q on unpacked codes; maple.c tdot_multi with qs=s=1, bit-exact
  *   mo_router_*            maple.c job_route_multi / bf_row, bit-exact; fp64 dot within 1e-6
- *   mo_exp                 |rel err| < 2^-50 against libm exp over a sweep (the function the GPU repeats)
+ *   mo_exp                 within 2 ulp of libm exp over a sweep, mostly exact (the function the GPU repeats)
  *   mo_topk                maple.c job_topk indices identical; weights within 2 ulp; permutation invariants
  *   mo_group               maple.c group_pairs identical; counting-sort invariants
  *   mo_act                 maple.c's act loop (fast-math expf/rcp) within 4 ulp
@@ -66,8 +66,8 @@ void mo_router_batch(const float *hn, int nb, const uint16_t *w_bf16, const floa
 /* maple.c:146-157 bf_row order (decode step(), maple.c:609): two 8-lane accumulators with stride 16. */
 void mo_router_step(const float *hn, const uint16_t *w_bf16, const float *bias, float *rl);
 
-/* exp used by softmax and SiLU: a fixed fp64 evaluation (range reduction + degree-13 Taylor, explicit FMA)
- * rounded to fp32. The HIP kernels evaluate the same sequence of IEEE operations. */
+/* exp used by softmax and SiLU: a fixed fp32 evaluation (range reduction with split ln2, degree-7 Taylor by
+ * Horner with FMA, exponent scaling). The HIP kernels evaluate the same sequence of IEEE operations. */
 float mo_exp(float x);
 
 /* maple.c:910-923 job_topk (== the inline block maple.c:735-748 and step's 608-617): softmax with
