@@ -143,6 +143,8 @@ int mmoe_gfull_post_norm(int L, float *rl);
 #define MMOE_R_HN 19      /* float [nb][2048] work input */
 int mmoe_read(int what, void *dst, size_t bytes);
 int mmoe_set_debug(int on);
+/* Batches of <= 8 tokens use three fused decode kernels (default on); off = the grouped-GEMM path. */
+int mmoe_set_decode_path(int on);
 const char *mmoe_last_error(void);
 
 /* Device memory on the library's device, and the library stream */

@@ -1,0 +1,374 @@
+// decode.h -- the MoE layer for small batches (decode: 1..8 tokens) in three kernels per layer.
+//
+// Decode reads each used expert's codes once per token step and is bound by memory latency, not by MFMA
+// throughput: 8 experts of one token are 6.4 MB of codes, less than what the GPU keeps in flight. What costs
+// time is the number of dependent steps, so the layer is three launches and no block waits for another
+// inside a launch (device-scope fences that would publish data between blocks flush L2 on this part):
+//   k_dec_route   rmsnorm (optional) + router logits in maple.c's FMA-chain order, from a chain-major copy
+//                 of the router so every thread issues all its loads at once
+//   k_dec_gateup  every block first repeats the small routing step (softmax/top-8 and the grouping of
+//                 maple.c:924-938 for <= 8 tokens, the int8 quantisation of its tokens), then computes its
+//                 gate/up rows as a GEMV (codes decoded in registers, v_dot4 on int8) and SiLU * up.
+//                 Block (0, 0) also publishes the routing for the next kernel and for checks.
+//   k_dec_down    every block re-quantises the act vectors (maple.c:832), then a wave computes 8 down rows
+//                 over all used experts and runs the combine chain in maple.c's order into the hidden state.
+// Results are bit-identical to the grouped-GEMM path and the oracle: same integer sums, same fp32 sequence.
+#pragma once
+#include "kernels.h"
+
+#ifdef DEC_TIMING   // development instrumentation: per-phase timestamps of one block per kernel
+#define DEC_TS(i, cond) do { if ((cond) && threadIdx.x == 0) dec_ts[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#define DEC_SPAN(i) do { if (threadIdx.x == 0) { unsigned long long ts_ = __builtin_amdgcn_s_memrealtime(); atomicMin(&dec_ts[i], ts_); atomicMax(&dec_ts[i + 1], ts_); } } while (0)
+#else
+#define DEC_TS(i, cond) do {} while (0)
+#define DEC_SPAN(i) do {} while (0)
+#endif
+
+#define DEC_MAXTOK 8
+#define DEC_MAXP (DEC_MAXTOK * MTOPK)  // 64 pairs
+#define DEC_GS 144                      // LDS bytes per 128-column group of int8 vectors (16 bytes padding)
+#define DEC_HP 4                        // LDS floats of padding per router chain
+
+__device__ __forceinline__ int dot16(const uint32_t *c, const uint32_t *q, int acc) {
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc = __builtin_amdgcn_sdot4((int)c[i], (int)q[i], acc, false);
+    return acc;
+}
+__device__ __forceinline__ void decode4(uint32_t w, uint32_t *o) {
+    const uint32_t M = 0x03030303u;
+    o[0] = w & M; o[1] = (w >> 2) & M; o[2] = (w >> 4) & M; o[3] = (w >> 6) & M;
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Router logits. One wave per block, 64/NCH experts per block (grid = MNE*NCH/64), lane = (expert, chain j):
+// chain j of expert e runs over columns j, j+NCH, ... (NCH = 16: maple.c:146-157, step; NCH = 8:
+// maple.c:853-889, batch). wc is the router in chain-major order, wc[e][j][m] = w[e][j + NCH*m]; a lane
+// issues all loads of its chain at kernel start and keeps them in registers for every token. hn sits in
+// LDS in the same chain-major order (padded against bank conflicts). do_norm: hn = rmsnorm(x, post_ln)
+// (maple.c:398-402, as k_rmsnorm), else hn = x. Block 0 writes hn.
+// ---------------------------------------------------------------------------------------------------------
+template <int NCH>
+__global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, int nb, const uint16_t *__restrict__ post_ln, int do_norm,
+                                                  const uint16_t *__restrict__ wc, const float *__restrict__ bias,
+                                                  float *__restrict__ hn, float *__restrict__ rl) {
+    constexpr int LEN = MH / NCH;                     // chain length
+    __shared__ __attribute__((aligned(16))) float hs[NCH * (LEN + DEC_HP)];
+    int l = threadIdx.x, j = l % NCH, e = blockIdx.x * (64 / NCH) + l / NCH;
+    DEC_SPAN(0);
+    DEC_TS(2, blockIdx.x == 5);
+    const gptr_u4 *wp = (const gptr_u4 *)(wc + ((size_t)e * NCH + j) * LEN);
+    v4i wv[LEN / 8];
+#pragma unroll
+    for (int i = 0; i < LEN / 8; i++) wv[i] = wp[i];
+    float lw[32];                                     // post_ln at columns 4l + 256i + 0..3
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        uint2 pv = (do_norm && post_ln) ? *(const uint2 *)(post_ln + 4 * l + 256 * i) : make_uint2(0x3f803f80u, 0x3f803f80u);
+        lw[4 * i] = bf16f(pv.x & 0xffff); lw[4 * i + 1] = bf16f(pv.x >> 16); lw[4 * i + 2] = bf16f(pv.y & 0xffff); lw[4 * i + 3] = bf16f(pv.y >> 16);
+    }
+    float bv = bias && j == 0 ? bias[e] : 0.0f;
+    for (int b = 0; b < nb; b++) {
+        const float *xb = x + (size_t)b * MH;
+        float v[32]; double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 f = *(const float4 *)(xb + 4 * l + 256 * i);
+            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+        }
+        if (do_norm) {
+#pragma unroll
+            for (int i = 0; i < 32; i++) ss += (double)v[i] * (double)v[i];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            float k = 1.0f / sqrtf((float)(ss / (double)MH) + 1e-6f);
+#pragma unroll
+            for (int i = 0; i < 32; i++) v[i] = v[i] * k * lw[i];
+        }
+        DEC_TS(3, blockIdx.x == 5);
+        __syncthreads();                              // previous token's chains are done with hs
+#pragma unroll
+        for (int i = 0; i < 32; i++) { int c = 4 * l + 256 * (i >> 2) + (i & 3); hs[(c % NCH) * (LEN + DEC_HP) + c / NCH] = v[i]; }
+        if (blockIdx.x == 0)
+#pragma unroll
+            for (int i = 0; i < 8; i++) *(float4 *)(hn + (size_t)b * MH + 4 * l + 256 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+        __syncthreads();
+        const float *hc = hs + j * (LEN + DEC_HP);
+        DEC_TS(4, blockIdx.x == 5);
+        float acc = 0.0f;
+#pragma unroll
+        for (int i = 0; i < LEN / 8; i++) {
+            float4 h0 = *(const float4 *)(hc + 8 * i), h1 = *(const float4 *)(hc + 8 * i + 4);
+            uint32_t q0 = (uint32_t)wv[i].x, q1 = (uint32_t)wv[i].y, q2 = (uint32_t)wv[i].z, q3 = (uint32_t)wv[i].w;
+            acc = __builtin_fmaf(__uint_as_float(q0 << 16), h0.x, acc); acc = __builtin_fmaf(__uint_as_float(q0 & 0xffff0000u), h0.y, acc);
+            acc = __builtin_fmaf(__uint_as_float(q1 << 16), h0.z, acc); acc = __builtin_fmaf(__uint_as_float(q1 & 0xffff0000u), h0.w, acc);
+            acc = __builtin_fmaf(__uint_as_float(q2 << 16), h1.x, acc); acc = __builtin_fmaf(__uint_as_float(q2 & 0xffff0000u), h1.y, acc);
+            acc = __builtin_fmaf(__uint_as_float(q3 << 16), h1.z, acc); acc = __builtin_fmaf(__uint_as_float(q3 & 0xffff0000u), h1.w, acc);
+        }
+        float vv[NCH];
+        int base = l & ~(NCH - 1);
+#pragma unroll
+        for (int i = 0; i < NCH; i++) vv[i] = __shfl(acc, base + i, 64);
+        if (j == 0) {
+            float s8[8];
+            if (NCH == 16) { for (int i = 0; i < 8; i++) s8[i] = vv[i] + vv[i + 8]; }
+            else { for (int i = 0; i < 8; i++) s8[i] = vv[i]; }
+            float r = hsum8(s8);
+            if (bias) r = r + bv;
+            rl[(size_t)b * MNE + e] = r;
+        }
+    }
+    DEC_TS(5, blockIdx.x == 5);
+    DEC_SPAN(0);
+}
+
+// wc[e][j][m] = w[e][j + NCH*m]
+template <int NCH>
+__global__ void k_router_chainmajor(const uint16_t *__restrict__ w, uint16_t *__restrict__ wc) {
+    int i = blockIdx.x * 256 + threadIdx.x;      // over 256 * 2048 elements of wc
+    int e = i / MH, r = i % MH, j = r / (MH / NCH), m = r % (MH / NCH);
+    wc[i] = w[(size_t)e * MH + j + NCH * m];
+}
+
+// Grouping of the nb <= 8 tokens' top-8 (R.top) by one wave of the block, the counting sort of
+// maple.c:924-938 (experts ascending, stable in token order) computed per pair from counts. Results in LDS: nu, ue, ustart, utok, uw, sp (slot -> pair), tp (pair ids of a token ascending).
+struct DecRoute {
+    int top[DEC_MAXP]; float tw[DEC_MAXP];
+    int nu, ue[DEC_MAXP], ustart[DEC_MAXP + 1];
+    int utok[DEC_MAXP]; float uw[DEC_MAXP]; int sp[DEC_MAXP], tp[DEC_MAXP];
+};
+__device__ void dec_group_block(int nb, DecRoute &R) {
+    int t = threadIdx.x, P = nb * MTOPK;
+    if (t < 64) {                                     // one wave, lane i = pair i (P <= 64)
+        int i = t, e = i < P ? R.top[i] : -1, cl = 0, ce = 0;
+        for (int j = 0; j < P; j++) { int ej = R.top[j]; cl += ej < e; ce += (j < i) & (ej == e); }
+        bool first = i < P && ce == 0;
+        unsigned long long fm = __ballot(first);
+        int du = 0;
+        for (int j = 0; j < P; j++) du += (int)((fm >> j) & 1) & (R.top[j] < e);
+        int slot = cl + ce;                           // experts ascending, tokens ascending within one
+        if (first) { R.ue[du] = e; R.ustart[du] = cl; }
+        if (i == 0) { R.nu = popc64(fm); R.ustart[popc64(fm)] = P; }
+        if (i < P) { R.utok[slot] = i / MTOPK; R.uw[slot] = R.tw[i]; R.sp[i] = slot; }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (i < P) {                                  // tp: a token's slots ascending (maple.c:1018-1019)
+            int g = i & ~(MTOPK - 1), rank = 0;
+            for (int k = 0; k < MTOPK; k++) rank += R.sp[g + k] < slot;
+            R.tp[g + rank] = slot;
+        }
+    }
+    __syncthreads();
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Gate/up GEMV. grid (64 row blocks of 8 rows, 8*nb expert slots); block 256. Every block routes (above);
+// slot u >= nu exits. Waves 0-1: gate rows, 2-3: up rows; 16 lanes per row, a lane = one 128-column group
+// (8 code words). Block (0, 0) publishes the routing (top, tw, plan, utok, uw, tp, sp, eptr, qx, qsx, qsumx).
+// ---------------------------------------------------------------------------------------------------------
+__global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl, const float *__restrict__ hn, int nb,
+                                                    const ExpPtr *__restrict__ layer_tab, int *__restrict__ top,
+                                                    float *__restrict__ tw, Plan *__restrict__ plan, int *__restrict__ utok,
+                                                    float *__restrict__ uw, int *__restrict__ tp, int *__restrict__ sp,
+                                                    ExpPtr *__restrict__ eptr, int8_t *__restrict__ qx, float *__restrict__ qsx,
+                                                    int *__restrict__ qsumx, float *__restrict__ act, int *__restrict__ dbg) {
+    __shared__ DecRoute R;
+    __shared__ float E[4][MNE];
+    __shared__ __attribute__((aligned(16))) int8_t qs_l[DEC_MAXTOK][MH / 128 * DEC_GS];
+    __shared__ float qsv_l[DEC_MAXTOK];
+    __shared__ int qsum_l[DEC_MAXTOK];
+    __shared__ int sums[2][8][DEC_MAXTOK];
+    __shared__ float sgu[2][8];
+    __shared__ ExpPtr tab[MNE];
+    int t = threadIdx.x, wv = t >> 6, l = t & 63;
+    DEC_TS(18, blockIdx.x == 3 && blockIdx.y == 1);
+    tab[t] = layer_tab[t];                            // the layer's expert table, loaded before it is needed
+
+    // top-8 of every token and the int8 quantisation (maple.c:908-909 prep) of every token, spread over waves
+    for (int it = wv; it < 2 * nb; it += 4) {
+        if (it < nb) topk_wave(rl + (size_t)it * MNE, E[wv], l, R.top + it * MTOPK, R.tw + it * MTOPK);
+        else quant_wave<MH, DEC_GS - 128>(hn + (size_t)(it - nb) * MH, l, qs_l[it - nb], &qsv_l[it - nb], &qsum_l[it - nb]);
+    }
+    __syncthreads();
+    DEC_TS(19, blockIdx.x == 3 && blockIdx.y == 1);
+    dec_group_block(nb, R);
+    DEC_TS(20, blockIdx.x == 3 && blockIdx.y == 1);
+    int u = blockIdx.y;
+    bool pub = blockIdx.x == 0 && blockIdx.y == 0;
+    if (u >= R.nu && !pub) return;                    // whole block
+    if (pub) {
+        int P = nb * MTOPK;
+        if (t < P) { top[t] = R.top[t]; tw[t] = R.tw[t]; utok[t] = R.utok[t]; uw[t] = R.uw[t]; tp[t] = R.tp[t]; sp[t] = R.sp[t]; }
+        if (t < R.nu) { plan->ue[t] = R.ue[t]; plan->ustart[t] = R.ustart[t]; eptr[t] = tab[R.ue[t]]; }
+        if (t == 0) { plan->nu = R.nu; plan->np = P; plan->ustart[R.nu] = P; plan->tn = 16; }
+        for (int bb = 0; bb < nb; bb++) {
+            for (int i = t; i < MH / 16; i += 256) *(uint4 *)(qx + (size_t)bb * MH + i * 16) = *(const uint4 *)(&qs_l[bb][(i >> 3) * DEC_GS + (i & 7) * 16]);
+            if (t == 0) { qsx[bb] = qsv_l[bb]; qsumx[bb] = qsum_l[bb]; }
+        }
+        if (u >= R.nu) return;
+    }
+    int kind = wv >> 1, rr = (wv & 1) * 4 + (l >> 4), grp = l & 15;
+    int r0 = blockIdx.x * 8, row = r0 + rr;
+    ExpPtr ex = tab[R.ue[u]];
+    const gptr_u4 *cp = (const gptr_u4 *)((kind ? ex.uc : ex.gc) + (size_t)row * (MH / 4) + grp * 32);
+    v4i c0 = cp[0], c1 = cp[1];
+    float srow = t < 16 ? (t < 8 ? ex.gs[r0 + t] : ex.us[r0 + t - 8]) : 0.0f;   // row scales, loaded with the codes
+    uint32_t cd[32];
+    uint32_t cwd[8] = {(uint32_t)c0.x, (uint32_t)c0.y, (uint32_t)c0.z, (uint32_t)c0.w, (uint32_t)c1.x, (uint32_t)c1.y, (uint32_t)c1.z, (uint32_t)c1.w};
+#pragma unroll
+    for (int k = 0; k < 8; k++) decode4(cwd[k], cd + 4 * k);
+#ifdef DEC_TIMING
+    if (cd[31] == 0xffffffffu) dec_ts[63] = 1;      // forces the code loads before the next stamp
+#endif
+    DEC_TS(21, blockIdx.x == 3 && blockIdx.y == 1);
+    int a0 = R.ustart[u], n = R.ustart[u + 1] - a0;
+    for (int i = 0; i < n; i++) {
+        int tok = R.utok[a0 + i];
+        const uint32_t *qd = (const uint32_t *)(&qs_l[tok][grp * DEC_GS]);
+        int acc = 0;
+#pragma unroll
+        for (int k = 0; k < 32; k++) acc = __builtin_amdgcn_sdot4((int)cd[k], (int)qd[k], acc, false);
+#pragma unroll
+        for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        if (grp == 0) sums[kind][rr][i] = acc;
+    }
+    if (t < 16) sgu[t >> 3][t & 7] = srow;
+    __syncthreads();
+    DEC_TS(22, blockIdx.x == 3 && blockIdx.y == 1);
+    if (t < n * 8) {
+        int i = t >> 3, r8 = t & 7, a = a0 + i, tok = R.utok[a];
+        float qs = qsv_l[tok]; int qsum = qsum_l[tok];
+        int ag = sums[0][r8][i], au = sums[1][r8][i];
+        float gv = (float)(ag - qsum) * qs * sgu[0][r8];
+        float uv = (float)(au - qsum) * qs * sgu[1][r8];
+        float g = gv < 7.0f ? gv : 7.0f;
+        float uu = uv < -7.0f ? -7.0f : (uv > 7.0f ? 7.0f : uv);
+        act[(size_t)a * MFF + r0 + r8] = g / (1.0f + dexp(-g)) * uu;
+        if (dbg) { dbg[(size_t)a * 2 * MFF + r0 + r8] = ag; dbg[(size_t)a * 2 * MFF + MFF + r0 + r8] = au; }
+    }
+    DEC_TS(23, blockIdx.x == 3 && blockIdx.y == 1);
+}
+
+// Quantisation of two FF-long act vectors by one wave (maple.c:832 prep, as quant_wave): lanes 0-31 take
+// vector a0, lanes 32-63 vector a1; lane = one 16-column chunk (mfma order within each 128-column group).
+struct ActChunk { float v[16]; };
+__device__ __forceinline__ void act_load(const float *__restrict__ act, int a, int l, ActChunk &c) {
+    int o = l & 31, g = o >> 3, h = (o >> 2) & 1, tq = o & 3;
+    const float *xr = act + (size_t)a * MFF;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        float4 f = *(const float4 *)(xr + g * 128 + s * 32 + h * 16 + tq * 4);
+        c.v[s * 4] = f.x; c.v[s * 4 + 1] = f.y; c.v[s * 4 + 2] = f.z; c.v[s * 4 + 3] = f.w;
+    }
+}
+__device__ __forceinline__ void act_quant(const ActChunk &c, int l, int8_t *q, float *qs, int *qsum) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(c.v[i]));
+    mx = fmaxf(mx, __int_as_float(dpp<0xB1>(__float_as_int(mx))));
+    mx = fmaxf(mx, __int_as_float(dpp<0x4E>(__float_as_int(mx))));
+    mx = fmaxf(mx, __int_as_float(dpp<0x141>(__float_as_int(mx))));
+    mx = fmaxf(mx, __int_as_float(dpp<0x140>(__float_as_int(mx))));
+    int mb = __float_as_int(mx);
+    float m0 = fmaxf(__int_as_float(__builtin_amdgcn_readlane(mb, 0)), __int_as_float(__builtin_amdgcn_readlane(mb, 16)));
+    float m1 = fmaxf(__int_as_float(__builtin_amdgcn_readlane(mb, 32)), __int_as_float(__builtin_amdgcn_readlane(mb, 48)));
+    mx = l < 32 ? m0 : m1;
+    float qsv = 1.0f, inv = 1.0f;
+    if (mx > 0.0f) { qsv = mx * (1.0f / 127.0f); inv = 127.0f / mx; }
+    int sum = 0; uint32_t wds[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        uint32_t wd = 0;
+#pragma unroll
+        for (int bb = 0; bb < 4; bb++) {
+            int qi = (int)__builtin_rintf(c.v[d * 4 + bb] * inv);
+            sum += qi;
+            wd |= (uint32_t)(qi & 0xff) << (8 * bb);
+        }
+        wds[d] = wd;
+    }
+    int o = l & 31;
+    *(uint4 *)(q + (o >> 3) * DEC_GS + (o & 7) * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+    sum += dpp<0xB1>(sum); sum += dpp<0x4E>(sum); sum += dpp<0x141>(sum); sum += dpp<0x140>(sum);
+    int s0 = __builtin_amdgcn_readlane(sum, 0) + __builtin_amdgcn_readlane(sum, 16);
+    int s1 = __builtin_amdgcn_readlane(sum, 32) + __builtin_amdgcn_readlane(sum, 48);
+    if ((l & 31) == 0) { *qs = qsv; *qsum = l < 32 ? s0 : s1; }
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Down GEMV + combine. grid = 2048 / 8 row blocks of 256 threads. Every block quantises all act vectors into
+// LDS (wave w takes pairs 8k + 2w, 8k + 2w + 1; block 0 also publishes them). Wave w computes the 8 rows for
+// the used experts u = w, w+4, ... (lane = row l/8, 64-column slice l%8); its code vectors are loaded while
+// the act vectors are quantised. Last, thread (token, row) runs the combine chain: mode 6 = step
+// (maple.c:664), mode 1 = step_batch (maple.c:834), as k_combine.
+// ---------------------------------------------------------------------------------------------------------
+#define DEC_DU (DEC_MAXP / 4)   // experts per wave
+__global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan, const ExpPtr *__restrict__ eptr,
+                                                  const float *__restrict__ act, int8_t *__restrict__ qa_out, float *__restrict__ qsa_out,
+                                                  int *__restrict__ qsuma_out, const int *__restrict__ tp, const int *__restrict__ sp,
+                                                  const float *__restrict__ uw, const float *__restrict__ tw, int nb,
+                                                  float *__restrict__ x, int mode, float *__restrict__ down, int *__restrict__ dbg) {
+    __shared__ float Dl[DEC_MAXP][8];
+    __shared__ __attribute__((aligned(16))) int8_t qa[DEC_MAXP][MFF / 128 * DEC_GS];
+    __shared__ float qsa[DEC_MAXP];
+    __shared__ int qsuma[DEC_MAXP];
+    int t = threadIdx.x, wv = t >> 6, l = t & 63, rr = l >> 3, sl = l & 7;
+    int r0 = blockIdx.x * 8, row = r0 + rr;
+    DEC_TS(34, blockIdx.x == 7);
+    ActChunk c0;
+    act_load(act, 2 * wv + (l >> 5), l, c0);          // first act vectors, issued before anything else
+    int nu = plan->nu;
+    const uint8_t *dcp[DEC_DU]; const float *dsp[DEC_DU];
+#pragma unroll
+    for (int k = 0; k < DEC_DU; k++) { int u = wv + 4 * k; dcp[k] = eptr[u].dc; dsp[k] = eptr[u].ds; }
+    v4i cv[DEC_DU]; float sd[DEC_DU];
+#pragma unroll
+    for (int k = 0; k < DEC_DU; k++)
+        if (wv + 4 * k < nu) { cv[k] = *(const gptr_u4 *)(dcp[k] + (size_t)row * (MFF / 4) + sl * 16); sd[k] = dsp[k][row]; }
+    for (int k = 0; k < nb; k++) {
+        int a = 8 * k + 2 * wv + (l >> 5);
+        if (k > 0) act_load(act, a, l, c0);
+        act_quant(c0, l, qa[a], &qsa[a], &qsuma[a]);
+    }
+    __syncthreads();
+    DEC_TS(35, blockIdx.x == 7);
+    if (blockIdx.x == 0)
+        for (int a = wv; a < nb * MTOPK; a += 4) {
+            if (l < MFF / 16) *(uint4 *)(qa_out + (size_t)a * MFF + l * 16) = *(const uint4 *)(&qa[a][(l >> 3) * DEC_GS + (l & 7) * 16]);
+            if (l == 0) { qsa_out[a] = qsa[a]; qsuma_out[a] = qsuma[a]; }
+        }
+#pragma unroll
+    for (int k = 0; k < DEC_DU; k++) {
+        int u = wv + 4 * k;
+        if (u >= nu) break;
+        uint32_t cd[16];
+        decode4((uint32_t)cv[k].x, cd); decode4((uint32_t)cv[k].y, cd + 4); decode4((uint32_t)cv[k].z, cd + 8); decode4((uint32_t)cv[k].w, cd + 12);
+        int a0 = plan->ustart[u], a1 = plan->ustart[u + 1];
+        for (int a = a0; a < a1; a++) {
+            const uint32_t *qd = (const uint32_t *)(&qa[a][(sl >> 1) * DEC_GS + (sl & 1) * 64]);
+            int acc = dot16(cd, qd, 0);
+#pragma unroll
+            for (int o = 4; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+            if (sl == 0) {
+                float d = (float)(acc - qsuma[a]) * qsa[a] * sd[k];
+                Dl[a][rr] = d;
+                down[(size_t)a * MH + row] = d;
+                if (dbg) dbg[(size_t)a * MH + row] = acc;
+            }
+        }
+    }
+    __syncthreads();
+    DEC_TS(36, blockIdx.x == 7);
+    if (t < nb * 8) {
+        int b = t >> 3, r8 = t & 7;
+        float *xp = x + (size_t)b * MH + r0 + r8;
+        float acc = (mode & 1) ? *xp : 0.0f;
+        for (int j = 0; j < MTOPK; j++) {
+            int a = (mode & 2) ? sp[b * MTOPK + j] : tp[b * MTOPK + j];
+            float wgt = (mode & 2) ? tw[b * MTOPK + j] : uw[a];
+            acc = __builtin_fmaf(wgt, Dl[a][r8], acc);
+        }
+        if (mode & 4) acc = *xp + acc;
+        *xp = acc;
+    }
+    DEC_TS(37, blockIdx.x == 7);
+}

@@ -70,15 +70,29 @@ __device__ __forceinline__ float dexp(float x) {
     return p * pow2i(k1) * pow2i(k2);
 }
 
-// ---- wave64 reductions (order-free operations only: max, integer sum) ----
+// ---- wave64 reductions (order-free operations only: max, integer sum). DPP inside each 16-lane row
+// (quad swaps, half-row mirror, row mirror), then the four row results are read as scalars. The whole wave
+// must be active.
+template <int CTRL> __device__ __forceinline__ int dpp(int v) { return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false); }
 __device__ __forceinline__ float wave_max(float v) {
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, __int_as_float(dpp<0xB1>(__float_as_int(v))));    // quad_perm [1,0,3,2]
+    v = fmaxf(v, __int_as_float(dpp<0x4E>(__float_as_int(v))));    // quad_perm [2,3,0,1]
+    v = fmaxf(v, __int_as_float(dpp<0x141>(__float_as_int(v))));   // row_half_mirror
+    v = fmaxf(v, __int_as_float(dpp<0x140>(__float_as_int(v))));   // row_mirror
+    int b = __float_as_int(v);
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0)), r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 __device__ __forceinline__ int wave_sum_i(int v) {
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp<0xB1>(v);
+    v += dpp<0x4E>(v);
+    v += dpp<0x141>(v);
+    v += dpp<0x140>(v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+           __builtin_amdgcn_readlane(v, 48);
 }
+__device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
 
 // =====================================================================================================
 // RMSNorm, maple.c:398-402: k = 1 / sqrtf((float)(sum x^2 / n) + 1e-6), out = x * k * w. The sum of squares
@@ -186,12 +200,16 @@ __global__ void __launch_bounds__(256) k_router_tiled(const float *__restrict__ 
 // of argmax on p with the lowest index winning ties (maple.c's strict >), picked entries set to -1; weights
 // p / (sum of picked, in pick order, + 1e-20). Also writes slot -> expert (top) and weight (tw).
 // =====================================================================================================
-__global__ void __launch_bounds__(256) k_topk(const float *__restrict__ rl, int nb, int *__restrict__ top, float *__restrict__ tw) {
-    __shared__ float E[4][MNE];
-    int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    int b = blockIdx.x * 4 + wv;
-    if (b >= nb) return;  // whole wave exits together
-    const float *r = rl + (size_t)b * MNE;
+// One wave, one token: rl_row[256] -> top[8], tw[8] (written by lane 0). E = 256 floats of LDS scratch.
+#ifdef DEC_TIMING
+__device__ unsigned long long dec_ts[64];
+#endif
+// One wave, one token: rl_row[256] -> top[8], tw[8]. E = 256 floats of LDS scratch.
+// Selection without 8 dependent arg-max rounds: p >= 0, so its bit pattern orders like the value. A
+// 31-step binary search on the bits (ballot counts) finds T = the 8th largest p; the picks are every p > T
+// and the lowest-indexed p == T until there are 8. Their pick order (larger first, lower index first among
+// equals, the order of repeated strict-> scans) is their rank among the 8.
+__device__ __forceinline__ void topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
     float lg[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) lg[i] = r[l + 64 * i];
@@ -199,38 +217,82 @@ __global__ void __launch_bounds__(256) k_topk(const float *__restrict__ rl, int 
     mx = wave_max(mx);
     mx = fmaxf(mx, -1e30f);  // maple.c starts its max at -1e30
 #pragma unroll
-    for (int i = 0; i < 4; i++) { lg[i] = dexp(lg[i] - mx); E[wv][l + 64 * i] = lg[i]; }
+    for (int i = 0; i < 4; i++) { lg[i] = dexp(lg[i] - mx); E[l + 64 * i] = lg[i]; }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float part = 0.0f;
-    if (l < 8)
-        for (int e = l; e < MNE; e += 8) part = part + E[wv][e];
+    if (l < 8) {
+        float ev[MNE / 8];
+#pragma unroll
+        for (int m = 0; m < MNE / 8; m++) ev[m] = E[l + 8 * m];
+#pragma unroll
+        for (int m = 0; m < MNE / 8; m++) part = part + ev[m];
+    }
     float pv[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) pv[i] = __shfl(part, i, 64);
+    for (int i = 0; i < 8; i++) pv[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), i));
     float sum = hsum8(pv);
-    float p[4];
+    float p[4]; uint32_t key[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) p[i] = lg[i] / sum;
-    float tsum = 0.0f, pk[MTOPK]; int ek[MTOPK];
+    for (int i = 0; i < 4; i++) { p[i] = lg[i] / sum; key[i] = __float_as_uint(p[i]); }
+    // T: the largest bit pattern with at least 8 keys >= it
+    uint32_t T = 0;
+    for (int bit = 30; bit >= 0; bit--) {
+        uint32_t c = T | (1u << bit);
+        int n = 0;
 #pragma unroll
-    for (int k = 0; k < MTOPK; k++) {
-        // lane-local best (lowest index among equals: i ascending means e ascending)
-        float bp = p[0]; int be = l;
-#pragma unroll
-        for (int i = 1; i < 4; i++) if (p[i] > bp) { bp = p[i]; be = l + 64 * i; }
-        for (int o = 32; o > 0; o >>= 1) {
-            float op = __shfl_xor(bp, o, 64); int oe = __shfl_xor(be, o, 64);
-            if (op > bp || (op == bp && oe < be)) { bp = op; be = oe; }
-        }
-        pk[k] = bp; ek[k] = be;
-        tsum = tsum + bp;
-        if ((be & 63) == l) p[be >> 6] = -1.0f;
+        for (int i = 0; i < 4; i++) n += popc64(__ballot(key[i] >= c));
+        if (n >= MTOPK) T = c;
     }
+    int ngt = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) ngt += popc64(__ballot(key[i] > T));
+    // which keys are picked; index = l + 64 i, so lower index = earlier row i, or same row and lower lane
+    unsigned long long lanemask = (1ull << l) - 1;
+    int eqbefore = 0; bool sel[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned long long eq = __ballot(key[i] == T);
+        bool e = key[i] == T;
+        sel[i] = key[i] > T || (e && ngt + eqbefore + popc64(eq & lanemask) < MTOPK);
+        eqbefore += popc64(eq);
+    }
+    // compact the 8 picks into E (index, p) in ascending index, then order them
+    __builtin_amdgcn_wave_barrier();
+    int *Ei = (int *)E;
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        unsigned long long m = __ballot(sel[i]);
+        if (sel[i]) { int pos = base + popc64(m & lanemask); Ei[pos] = l + 64 * i; E[MTOPK + pos] = p[i]; }
+        base += popc64(m);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (l < MTOPK) {
+        int me = Ei[l]; float mp = E[MTOPK + l];
+        int rank = 0;
+#pragma unroll
+        for (int k = 0; k < MTOPK; k++) { float q = E[MTOPK + k]; rank += q > mp || (q == mp && k < l); }
+        Ei[2 * MTOPK + rank] = me; E[3 * MTOPK + rank] = mp;
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     if (l == 0) {
+        float pk[MTOPK], tsum = 0.0f;
 #pragma unroll
-        for (int k = 0; k < MTOPK; k++) { top[b * MTOPK + k] = ek[k]; tw[b * MTOPK + k] = pk[k] / (tsum + 1e-20f); }
+        for (int k = 0; k < MTOPK; k++) { pk[k] = E[3 * MTOPK + k]; tsum = tsum + pk[k]; }
+#pragma unroll
+        for (int k = 0; k < MTOPK; k++) { top[k] = Ei[2 * MTOPK + k]; tw[k] = pk[k] / (tsum + 1e-20f); }
     }
+}
+
+__global__ void __launch_bounds__(256) k_topk(const float *__restrict__ rl, int nb, int *__restrict__ top, float *__restrict__ tw) {
+    __shared__ float E[4][MNE];
+    int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    int b = blockIdx.x * 4 + wv;
+    if (b >= nb) return;  // whole wave exits together
+    topk_wave(rl + (size_t)b * MNE, E[wv], l, top + b * MTOPK, tw + b * MTOPK);
 }
 
 // =====================================================================================================
@@ -339,15 +401,13 @@ __global__ void k_plan_from_ustart(const int *__restrict__ ustart, int nu, Plan 
 // n = 2048 or 512 values; output in mfma order (see top of file) plus qs and qsum. Optionally the source
 // rows are gathered (src_row = rows ? rows[i] : i) -- not used by the current path.
 // =====================================================================================================
-template <int N>
-__global__ void __launch_bounds__(256) k_quant(const float *__restrict__ x, int nrows, int8_t *__restrict__ q,
-                                               float *__restrict__ qs, int *__restrict__ qsum) {
+// One wave quantises one vector of N (2048 or 512) floats into q (mfma order), *qs, *qsum (lane 0 writes).
+// GPAD: bytes of padding after each 128-column group of q (LDS copies read by lanes one group apart).
+template <int N, int GPAD = 0>
+__device__ __forceinline__ void quant_wave(const float *__restrict__ xr, int l, int8_t *__restrict__ q, float *__restrict__ qs,
+                                           int *__restrict__ qsum) {
     constexpr int NCHK = N / 16;                    // 16-byte output chunks per vector
     constexpr int PER = (NCHK + 63) / 64;           // chunks per lane
-    int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    int row = blockIdx.x * 4 + wv;
-    if (row >= nrows) return;
-    const float *xr = x + (size_t)row * N;
     float v[PER][16];
     float mx = 0.0f;
 #pragma unroll
@@ -384,11 +444,20 @@ __global__ void __launch_bounds__(256) k_quant(const float *__restrict__ x, int 
                 }
                 wds[d] = wd;
             }
-            *(uint4 *)(q + (size_t)row * N + o * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+            *(uint4 *)(q + (o >> 3) * (128 + GPAD) + (o & 7) * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
         }
     }
     sum = wave_sum_i(sum);
-    if (l == 0) { qs[row] = qsv; qsum[row] = sum; }
+    if (l == 0) { *qs = qsv; *qsum = sum; }
+}
+
+template <int N>
+__global__ void __launch_bounds__(256) k_quant(const float *__restrict__ x, int nrows, int8_t *__restrict__ q,
+                                               float *__restrict__ qs, int *__restrict__ qsum) {
+    int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    int row = blockIdx.x * 4 + wv;
+    if (row >= nrows) return;
+    quant_wave<N>(x + (size_t)row * N, l, q + (size_t)row * N, qs + row, qsum + row);
 }
 
 // =====================================================================================================

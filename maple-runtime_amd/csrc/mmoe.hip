@@ -17,6 +17,7 @@
 #include <unistd.h>
 #include <vector>
 #include "kernels.h"
+#include "decode.h"
 
 extern "C" {
 #include "../../include/maplemoe.h"
@@ -48,6 +49,7 @@ struct Work {
     float *qsx = nullptr, *qsa = nullptr, *act = nullptr, *down = nullptr;
     int *qsumx = nullptr, *qsuma = nullptr;
     int *dbg_gu = nullptr, *dbg_dn = nullptr;
+    unsigned *counters = nullptr;   // [0] routing, [64 + u] per used expert: last-block-done counters (self-resetting)
 };
 
 static int work_alloc(Work &w, int maxtok) {
@@ -64,6 +66,8 @@ static int work_alloc(Work &w, int maxtok) {
     HC(hipMalloc(&w.qx, T * MH)); HC(hipMalloc(&w.qsx, T * 4)); HC(hipMalloc(&w.qsumx, T * 4));
     HC(hipMalloc(&w.act, P * MFF * 4)); HC(hipMalloc(&w.qa, P * MFF)); HC(hipMalloc(&w.qsa, P * 4)); HC(hipMalloc(&w.qsuma, P * 4));
     HC(hipMalloc(&w.down, P * MH * 4));
+    HC(hipMalloc(&w.counters, (64 + MNE) * sizeof(unsigned)));
+    HC(hipMemset(w.counters, 0, (64 + MNE) * sizeof(unsigned)));
     return 0;
 }
 
@@ -80,7 +84,7 @@ static int work_debug(Work &w, int on) {
 // Global state
 // ------------------------------------------------------------------------------------------------------
 struct Region { const void *host; size_t len; uint8_t *dev; };
-struct LayerW { ExpPtr *tab = nullptr; uint16_t *router = nullptr; uint16_t *post_ln = nullptr; float *bias = nullptr; };
+struct LayerW { ExpPtr *tab = nullptr; uint16_t *router = nullptr; uint16_t *rc16 = nullptr, *rc8 = nullptr; uint16_t *post_ln = nullptr; float *bias = nullptr; };
 
 static struct {
     bool ready = false;
@@ -167,7 +171,7 @@ static int stage_quant_x(Work &w, const float *d_hn, int nb) {
 }
 
 // gate/up (+SiLU), act quantisation, down for np pairs under w.plan / w.eptr / w.utok
-static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; } LAST;
+static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int dec; float *x; } LAST;
 
 static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8); }  // xcd_item needs a multiple of 8
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
@@ -180,7 +184,7 @@ static int launch_down(Work &w, int maxtiles, int tn, int *dd) {
 }
 
 static int stage_experts(Work &w, int np, int nu_max, int tn) {
-    LAST.w = &w; LAST.np = np; LAST.nu_max = nu_max; LAST.tn = tn;
+    LAST.w = &w; LAST.np = np; LAST.nu_max = nu_max; LAST.tn = tn; LAST.dec = 0;
     int maxtiles = np / tn + (nu_max < np ? nu_max : np);
     int *dg = S.debug ? w.dbg_gu : nullptr, *dd = S.debug ? w.dbg_dn : nullptr;
     if (launch_gateup(w, maxtiles, tn, dg)) return -1;
@@ -194,13 +198,42 @@ static int stage_combine(Work &w, int nb, float *d_x, int mode) {
     return launch(MMOE_K_COMBINE, [&] { k_combine<<<(n + 255) / 256, 256, 0, S.st>>>(w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode); });
 }
 
+// Small batches (decode): three kernels, see decode.h. in = hn (do_norm 0) or the hidden state x whose
+// rmsnorm(post_ln) is the MoE input (do_norm 1); hn is also written to w.hn.
+static bool S_dec_enabled = true;
+static int launch_dec_gateup(Work &w, int nb, int L) {
+    int maxu = nb * MTOPK < MNE ? nb * MTOPK : MNE;
+    int *dg = S.debug ? w.dbg_gu : nullptr;
+    const ExpPtr *tab = S.layers[L].tab;
+    return launch(MMOE_K_GATEUP, [&] { k_dec_gateup<<<dim3(MFF / 8, maxu), 256, 0, S.st>>>(w.rl, w.hn, nb, tab, w.top, w.tw, w.plan, w.utok, w.uw, w.tp, w.sp, w.eptr, w.qx, w.qsx, w.qsumx, w.act, dg); });
+}
+static int launch_dec_down(Work &w, int nb, float *d_x, int order) {
+    int *dd = S.debug ? w.dbg_dn : nullptr;
+    int mode = order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH;
+    return launch(MMOE_K_DOWN, [&] { k_dec_down<<<MH / 8, 256, 0, S.st>>>(w.plan, w.eptr, w.act, w.qa, w.qsa, w.qsuma, w.tp, w.sp, w.uw, w.tw, nb, d_x, mode, w.down, dd); });
+}
+static int moe_dec(int L, const float *in, int do_norm, int nb, float *d_x, int order) {
+    Work &w = S.main;
+    LayerW &lw = S.layers[L];
+    LAST.w = &w; LAST.np = nb * MTOPK; LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = nullptr; LAST.dec = 1; LAST.x = d_x;
+    const uint16_t *pln = do_norm ? lw.post_ln : nullptr;
+    if (order == MMOE_ORDER_STEP) {
+        if (launch(MMOE_K_ROUTER, [&] { k_dec_route<16><<<MNE * 16 / 64, 64, 0, S.st>>>(in, nb, pln, do_norm, lw.rc16, lw.bias, w.hn, w.rl); })) return -1;
+    } else {
+        if (launch(MMOE_K_ROUTER, [&] { k_dec_route<8><<<MNE * 8 / 64, 64, 0, S.st>>>(in, nb, pln, do_norm, lw.rc8, lw.bias, w.hn, w.rl); })) return -1;
+    }
+    if (launch_dec_gateup(w, nb, L)) return -1;
+    return launch_dec_down(w, nb, d_x, order);
+}
+
 // Whole MoE layer on device buffers: x[b] += MoE_L(hn[b])
 static int moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) {
     Work &w = S.main;
     if (nb < 1 || nb > w.maxtok) { seterr("nb %d outside 1..%d (mmoe_init)", nb, w.maxtok); return -1; }
     if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("layer %d not set (mmoe_set_layer)", L); return -1; }
+    if (nb <= DEC_MAXTOK && S_dec_enabled) return moe_dec(L, d_hn, 0, nb, d_x, order);
     int np = nb * MTOPK, tn = tile_tn(np);
-    LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = d_hn;
+    LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = d_hn; LAST.dec = 0;
     if (stage_router(w, L, d_hn, nb, order)) return -1;
     if (stage_route_group(w, L, nb, tn)) return -1;
     if (stage_quant_x(w, d_hn, nb)) return -1;
@@ -438,6 +471,9 @@ int mmoe_init(int maxtok) {
     return work_debug(S.main, S.debug);
 }
 
+// Small batches take the three-kernel decode path unless switched off (tests compare both paths).
+int mmoe_set_decode_path(int on) { S_dec_enabled = on != 0; return 0; }
+
 int mmoe_set_debug(int on) {
     S.debug = on != 0;
     if (S.main.maxtok && work_debug(S.main, S.debug)) return -1;
@@ -455,6 +491,12 @@ int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *
     if (!lw.router) HC(hipMalloc(&lw.router, (size_t)MNE * MH * 2));
     HC(hipMemcpy(lw.tab, ep, sizeof ep, hipMemcpyHostToDevice));
     HC(hipMemcpy(lw.router, router, (size_t)MNE * MH * 2, hipMemcpyHostToDevice));
+    if (!lw.rc16) HC(hipMalloc(&lw.rc16, (size_t)MNE * MH * 2));
+    if (!lw.rc8) HC(hipMalloc(&lw.rc8, (size_t)MNE * MH * 2));
+    k_router_chainmajor<16><<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rc16);
+    k_router_chainmajor<8><<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rc8);
+    HC(hipGetLastError());
+    HC(hipStreamSynchronize(S.st));
     if (post_ln) {
         if (!lw.post_ln) HC(hipMalloc(&lw.post_ln, MH * 2));
         HC(hipMemcpy(lw.post_ln, post_ln, MH * 2, hipMemcpyHostToDevice));
@@ -496,6 +538,7 @@ int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order) {
     if (!w.maxtok || nb < 1 || nb > w.maxtok) { seterr("mmoe_stack_dev: nb %d outside capacity %d", nb, w.maxtok); return -1; }
     for (int L = L0; L < L0 + nl; L++) {
         if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("mmoe_stack_dev: layer %d not set", L); return -1; }
+        if (nb <= DEC_MAXTOK && S_dec_enabled) { if (moe_dec(L, d_x, 1, nb, d_x, order)) return -1; continue; }
         const uint16_t *pw = S.layers[L].post_ln;
         if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(d_x, pw, w.hn, nb); })) return -1;
         if (moe_dev(L, w.hn, nb, d_x, order)) return -1;
@@ -592,10 +635,17 @@ double mmoe_event_elapsed_ms(void) {
 double mmoe_bench_stage(int kid, int reps) {
     if (!LAST.w || reps < 1 || S.prof) { seterr("mmoe_bench_stage: nothing to repeat"); return -1.0; }
     Work &w = *LAST.w;
-    int maxtiles = LAST.np / LAST.tn + (LAST.nu_max < LAST.np ? LAST.nu_max : LAST.np);
+    int maxtiles = LAST.dec || LAST.tn < 1 ? 0 : LAST.np / LAST.tn + (LAST.nu_max < LAST.np ? LAST.nu_max : LAST.np);
     if (hipEventRecord(S.pe[0], S.st) != hipSuccess) return -1.0;
     for (int i = 0; i < reps; i++) {
         int rc = 0;
+        if (LAST.dec) {   // decode kernels (k_dec_down adds into x again: timing only)
+            if (kid == MMOE_K_GATEUP) rc = launch_dec_gateup(w, LAST.nb, LAST.L);
+            else if (kid == MMOE_K_DOWN) rc = launch_dec_down(w, LAST.nb, LAST.x, LAST.order);
+            else { seterr("mmoe_bench_stage: kernel %d not repeatable on the decode path", kid); return -1.0; }
+            if (rc) return -1.0;
+            continue;
+        }
         switch (kid) {
             case MMOE_K_GATEUP: rc = launch_gateup(w, maxtiles, LAST.tn, nullptr); break;
             case MMOE_K_DOWN: rc = launch_down(w, maxtiles, LAST.tn, nullptr); break;
@@ -626,3 +676,14 @@ int mmoe_device_info(char *name, int len, int *cus, int *clock_khz) {
 }
 
 }  // extern "C"
+
+#ifdef DEC_TIMING
+extern "C" int mmoe_dec_ts(unsigned long long *out, int reset) {
+    if (reset) {
+        unsigned long long h[64];
+        for (int i = 0; i < 64; i++) h[i] = (i % 16 == 0) ? ~0ull : 0ull;
+        return hipMemcpyToSymbol(HIP_SYMBOL(dec_ts), h, sizeof h) == hipSuccess ? 0 : -1;
+    }
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(dec_ts), 64 * 8) == hipSuccess ? 0 : -1;
+}
+#endif

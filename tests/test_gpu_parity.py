@@ -146,3 +146,49 @@ def test_gpux(layer0):
         qa, qsa, qsuma = O.prep(act)
         d = np.array([np.float32(np.float32(o.mo_dot_i32(O._p(dc[r]), O._p(qa), 512) - qsuma) * qsa) * ds[r] for r in range(2048)], np.float32)
         assert relmax(out[k], d) <= TOL
+
+
+@pytest.mark.parametrize("nb", [1, 5, 8])
+def test_moe_grouped_path_small_batches(layer0, nb):
+    """the grouped-GEMM kernels at decode sizes (the default there is the three-kernel decode path)"""
+    M.check(M.lib().mmoe_set_decode_path(0), "decode off")
+    try:
+        compare_layer(layer0, nb, M.ORDER_BATCH)
+        if nb == 1:
+            compare_layer(layer0, 1, M.ORDER_STEP)
+    finally:
+        M.lib().mmoe_set_decode_path(1)
+
+
+def test_stack_decode(layer0):
+    """3 stacked layers (rmsnorm with a bf16 post-norm weight, then the MoE block of step()) on device memory,
+    against the oracle applied layer by layer"""
+    lib = M.lib()
+    layers = [layer0]
+    rng = np.random.default_rng(5)
+    pln = (np.float32(1.0) + rng.standard_normal((3, 2048)).astype(np.float32) * 0.1).view(np.uint32)
+    pln = ((pln + 0x7FFF + ((pln >> 16) & 1)) >> 16).astype(np.uint16)       # bf16 weights
+    for L in (1, 2):
+        hl = HostLayer(SEED, L)
+        hl.rid = M.register_layer(L, hl.blk, hl.router, pln[L])
+        layers.append(hl)
+    M.register_layer(0, layer0.blk, layer0.router, pln[0])  # layer 0 again, now with its norm weight
+    for nb, order in [(1, M.ORDER_STEP), (4, M.ORDER_BATCH)]:
+        x0 = M.synth_hidden(SEED, 300 + nb, nb)
+        d_x = lib.mmoe_dev_alloc(x0.nbytes)
+        M.check(lib.mmoe_h2d(d_x, M.ptr(x0), x0.nbytes), "h2d")
+        M.check(lib.mmoe_stack_dev(0, 3, d_x, nb, order), "stack")
+        xg = np.empty_like(x0)
+        M.check(lib.mmoe_d2h(M.ptr(xg), d_x, x0.nbytes), "d2h")
+        lib.mmoe_dev_free(d_x)
+        xo = x0.copy()
+        for L in range(3):
+            hn = np.empty_like(xo)
+            for b in range(nb):
+                O.oracle().mo_rmsnorm(O._p(xo[b]), O._p(pln[L]), 2048, O._p(hn[b]))
+            if order == M.ORDER_STEP:
+                O.moe_step(hn[0], layers[L].router, layers[L].table, xo[0])
+            else:
+                O.moe_batch(hn, layers[L].router, layers[L].table, xo)
+        print(f"\n  stack nb={nb}: bit-exact {np.array_equal(xg, xo)}, rel {relmax(xg - x0, xo - x0):.2e}")
+        assert relmax(xg - x0, xo - x0) <= TOL
