@@ -76,10 +76,11 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
             v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
         }
         if (do_norm) {
+            double s4[4] = {0.0, 0.0, 0.0, 0.0};     // squares are exact in fp64; only the additions round
 #pragma unroll
-            for (int i = 0; i < 32; i++) ss += (double)v[i] * (double)v[i];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+            for (int i = 0; i < 32; i++) s4[i & 3] += (double)v[i] * (double)v[i];
+            ss = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+            ss = wave_sum_d(ss);
             float k = 1.0f / sqrtf((float)(ss / (double)MH) + 1e-6f);
 #pragma unroll
             for (int i = 0; i < 32; i++) v[i] = v[i] * k * lw[i];
@@ -139,7 +140,7 @@ struct DecRoute {
 __device__ void dec_group_block(int nb, DecRoute &R) {
     int t = threadIdx.x, P = nb * MTOPK;
     if (t < 64) {                                     // one wave, lane i = pair i (P <= 64)
-        int i = t, e = i < P ? R.top[i] : -1, cl = 0, ce = 0;
+        int i = t, e = i < P ? R.top[i] : 0x7fffffff, cl = 0, ce = 0;
         for (int j = 0; j < P; j++) { int ej = R.top[j]; cl += ej < e; ce += (j < i) & (ej == e); }
         bool first = i < P && ce == 0;
         unsigned long long fm = __ballot(first);
@@ -149,13 +150,11 @@ __device__ void dec_group_block(int nb, DecRoute &R) {
         if (first) { R.ue[du] = e; R.ustart[du] = cl; }
         if (i == 0) { R.nu = popc64(fm); R.ustart[popc64(fm)] = P; }
         if (i < P) { R.utok[slot] = i / MTOPK; R.uw[slot] = R.tw[i]; R.sp[i] = slot; }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        if (i < P) {                                  // tp: a token's slots ascending (maple.c:1018-1019)
-            int g = i & ~(MTOPK - 1), rank = 0;
-            for (int k = 0; k < MTOPK; k++) rank += R.sp[g + k] < slot;
-            R.tp[g + rank] = slot;
-        }
+        // tp: a token's slots ascending (maple.c:1018-1019); the 8 pairs of a token are lanes 8b..8b+7
+        int rank = 0;
+#pragma unroll
+        for (int k = 0; k < MTOPK; k++) rank += __shfl(slot, (i & ~(MTOPK - 1)) + k, 64) < slot;
+        if (i < P) R.tp[(i & ~(MTOPK - 1)) + rank] = slot;
     }
     __syncthreads();
 }
@@ -181,13 +180,14 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     __shared__ ExpPtr tab[MNE];
     int t = threadIdx.x, wv = t >> 6, l = t & 63;
     DEC_TS(18, blockIdx.x == 3 && blockIdx.y == 1);
-    tab[t] = layer_tab[t];                            // the layer's expert table, loaded before it is needed
+    ExpPtr my = layer_tab[t];                         // the layer's expert table, stored to LDS after top-8
 
     // top-8 of every token and the int8 quantisation (maple.c:908-909 prep) of every token, spread over waves
     for (int it = wv; it < 2 * nb; it += 4) {
         if (it < nb) topk_wave(rl + (size_t)it * MNE, E[wv], l, R.top + it * MTOPK, R.tw + it * MTOPK);
         else quant_wave<MH, DEC_GS - 128>(hn + (size_t)(it - nb) * MH, l, qs_l[it - nb], &qsv_l[it - nb], &qsum_l[it - nb]);
     }
+    tab[t] = my;
     __syncthreads();
     DEC_TS(19, blockIdx.x == 3 && blockIdx.y == 1);
     dec_group_block(nb, R);
@@ -227,8 +227,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
         int acc = 0;
 #pragma unroll
         for (int k = 0; k < 32; k++) acc = __builtin_amdgcn_sdot4((int)cd[k], (int)qd[k], acc, false);
-#pragma unroll
-        for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+        acc += dpp<0xB1>(acc); acc += dpp<0x4E>(acc); acc += dpp<0x141>(acc); acc += dpp<0x140>(acc);   // 16-lane row sum
         if (grp == 0) sums[kind][rr][i] = acc;
     }
     if (t < 16) sgu[t >> 3][t & 7] = srow;

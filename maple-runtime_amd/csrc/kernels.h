@@ -93,6 +93,23 @@ __device__ __forceinline__ int wave_sum_i(int v) {
            __builtin_amdgcn_readlane(v, 48);
 }
 __device__ __forceinline__ int popc64(unsigned long long m) { return __popcll(m); }
+// fp64 sum over the wave (DPP on both halves of each double; the order is fixed, not maple.c's)
+template <int CTRL> __device__ __forceinline__ double dpp_d(double v) {
+    unsigned long long b = __double_as_longlong(v);
+    int hi = dpp<CTRL>((int)(b >> 32)), lo = dpp<CTRL>((int)(uint32_t)b);
+    return __longlong_as_double((long long)(((unsigned long long)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+    v += dpp_d<0xB1>(v); v += dpp_d<0x4E>(v); v += dpp_d<0x141>(v); v += dpp_d<0x140>(v);
+    unsigned long long b = __double_as_longlong(v);
+    double r[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t hi = __builtin_amdgcn_readlane((int)(b >> 32), 16 * i), lo = __builtin_amdgcn_readlane((int)(uint32_t)b, 16 * i);
+        r[i] = __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+    }
+    return (r[0] + r[1]) + (r[2] + r[3]);
+}
 
 // =====================================================================================================
 // RMSNorm, maple.c:398-402: k = 1 / sqrtf((float)(sum x^2 / n) + 1e-6), out = x * k * w. The sum of squares
@@ -203,19 +220,24 @@ __global__ void __launch_bounds__(256) k_router_tiled(const float *__restrict__ 
 // One wave, one token: rl_row[256] -> top[8], tw[8] (written by lane 0). E = 256 floats of LDS scratch.
 #ifdef DEC_TIMING
 __device__ unsigned long long dec_ts[64];
+#define TK_TS(i) do { if (blockIdx.x == 3 && blockIdx.y == 1 && l == 0) dec_ts[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
+#else
+#define TK_TS(i) do {} while (0)
 #endif
 // One wave, one token: rl_row[256] -> top[8], tw[8]. E = 256 floats of LDS scratch.
-// Selection without 8 dependent arg-max rounds: p >= 0, so its bit pattern orders like the value. A
-// 31-step binary search on the bits (ballot counts) finds T = the 8th largest p; the picks are every p > T
-// and the lowest-indexed p == T until there are 8. Their pick order (larger first, lower index first among
-// equals, the order of repeated strict-> scans) is their rank among the 8.
+// Selection: p >= 0, so key = p_bits + 1 orders like p, and 0 marks a picked expert. Each of the 8 rounds
+// takes the largest key (lane-local over 4, DPP within 16-lane rows, the 4 row results as scalars), then the
+// lowest expert index holding it (ballots in index order: e = l + 64 i), which is the pick order of maple.c's
+// repeated strict-> scans, ties included.
 __device__ __forceinline__ void topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
+    TK_TS(40); TK_TS(41);
     float lg[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) lg[i] = r[l + 64 * i];
     float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
     mx = wave_max(mx);
     mx = fmaxf(mx, -1e30f);  // maple.c starts its max at -1e30
+    TK_TS(42);
 #pragma unroll
     for (int i = 0; i < 4; i++) { lg[i] = dexp(lg[i] - mx); E[l + 64 * i] = lg[i]; }
     __builtin_amdgcn_wave_barrier();
@@ -232,58 +254,34 @@ __device__ __forceinline__ void topk_wave(const float *__restrict__ r, float *E,
 #pragma unroll
     for (int i = 0; i < 8; i++) pv[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), i));
     float sum = hsum8(pv);
-    float p[4]; uint32_t key[4];
+    TK_TS(43);
+    uint32_t key[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) { p[i] = lg[i] / sum; key[i] = __float_as_uint(p[i]); }
-    // T: the largest bit pattern with at least 8 keys >= it
-    uint32_t T = 0;
-    for (int bit = 30; bit >= 0; bit--) {
-        uint32_t c = T | (1u << bit);
-        int n = 0;
+    for (int i = 0; i < 4; i++) key[i] = __float_as_uint(lg[i] / sum) + 1u;
+    float pk[MTOPK]; int ek[MTOPK];
+    float tsum = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) n += popc64(__ballot(key[i] >= c));
-        if (n >= MTOPK) T = c;
+    for (int k = 0; k < MTOPK; k++) {
+        uint32_t b = max(max(key[0], key[1]), max(key[2], key[3]));
+        b = max(b, (uint32_t)dpp<0xB1>((int)b));
+        b = max(b, (uint32_t)dpp<0x4E>((int)b));
+        b = max(b, (uint32_t)dpp<0x141>((int)b));
+        b = max(b, (uint32_t)dpp<0x140>((int)b));
+        uint32_t m = max(max((uint32_t)__builtin_amdgcn_readlane((int)b, 0), (uint32_t)__builtin_amdgcn_readlane((int)b, 16)),
+                         max((uint32_t)__builtin_amdgcn_readlane((int)b, 32), (uint32_t)__builtin_amdgcn_readlane((int)b, 48)));
+        unsigned long long m0 = __ballot(key[0] == m), m1 = __ballot(key[1] == m), m2 = __ballot(key[2] == m), m3 = __ballot(key[3] == m);
+        int e = m0 ? __ffsll((long long)m0) - 1 : m1 ? 64 + __ffsll((long long)m1) - 1 : m2 ? 128 + __ffsll((long long)m2) - 1 : 192 + __ffsll((long long)m3) - 1;
+        pk[k] = __uint_as_float(m - 1u); ek[k] = e;
+        tsum = tsum + pk[k];
+        if (l == (e & 63)) {
+            int i = e >> 6;
+            key[0] = i == 0 ? 0u : key[0]; key[1] = i == 1 ? 0u : key[1]; key[2] = i == 2 ? 0u : key[2]; key[3] = i == 3 ? 0u : key[3];
+        }
     }
-    int ngt = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) ngt += popc64(__ballot(key[i] > T));
-    // which keys are picked; index = l + 64 i, so lower index = earlier row i, or same row and lower lane
-    unsigned long long lanemask = (1ull << l) - 1;
-    int eqbefore = 0; bool sel[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        unsigned long long eq = __ballot(key[i] == T);
-        bool e = key[i] == T;
-        sel[i] = key[i] > T || (e && ngt + eqbefore + popc64(eq & lanemask) < MTOPK);
-        eqbefore += popc64(eq);
-    }
-    // compact the 8 picks into E (index, p) in ascending index, then order them
-    __builtin_amdgcn_wave_barrier();
-    int *Ei = (int *)E;
-    int base = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        unsigned long long m = __ballot(sel[i]);
-        if (sel[i]) { int pos = base + popc64(m & lanemask); Ei[pos] = l + 64 * i; E[MTOPK + pos] = p[i]; }
-        base += popc64(m);
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    if (l < MTOPK) {
-        int me = Ei[l]; float mp = E[MTOPK + l];
-        int rank = 0;
-#pragma unroll
-        for (int k = 0; k < MTOPK; k++) { float q = E[MTOPK + k]; rank += q > mp || (q == mp && k < l); }
-        Ei[2 * MTOPK + rank] = me; E[3 * MTOPK + rank] = mp;
-    }
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    TK_TS(44); TK_TS(45);
     if (l == 0) {
-        float pk[MTOPK], tsum = 0.0f;
 #pragma unroll
-        for (int k = 0; k < MTOPK; k++) { pk[k] = E[3 * MTOPK + k]; tsum = tsum + pk[k]; }
-#pragma unroll
-        for (int k = 0; k < MTOPK; k++) { top[k] = Ei[2 * MTOPK + k]; tw[k] = pk[k] / (tsum + 1e-20f); }
+        for (int k = 0; k < MTOPK; k++) { top[k] = ek[k]; tw[k] = pk[k] / (tsum + 1e-20f); }
     }
 }
 
