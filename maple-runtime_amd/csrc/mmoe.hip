@@ -84,7 +84,7 @@ static int work_debug(Work &w, int on) {
 // Global state
 // ------------------------------------------------------------------------------------------------------
 struct Region { const void *host; size_t len; uint8_t *dev; };
-struct LayerW { ExpPtr *tab = nullptr; uint16_t *router = nullptr; uint16_t *rc16 = nullptr, *rc8 = nullptr; uint16_t *post_ln = nullptr; float *bias = nullptr; };
+struct LayerW { ExpPtr *tab = nullptr; uint16_t *router = nullptr; uint16_t *rc16 = nullptr, *rc8 = nullptr; float *rf8 = nullptr; uint16_t *post_ln = nullptr; float *bias = nullptr; };
 
 static struct {
     bool ready = false;
@@ -151,7 +151,9 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
         int n = nb * MNE * 8;
         return launch(MMOE_K_ROUTER, [&] { k_router_lanes<8><<<(n + 255) / 256, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
     }
-    return launch(MMOE_K_ROUTER, [&] { k_router_tiled<4><<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
+    if (nb < 128)
+        return launch(MMOE_K_ROUTER, [&] { k_router_tiled<4><<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
+    return launch(MMOE_K_ROUTER, [&] { k_router_gemm<<<dim3((nb + RG_BT - 1) / RG_BT, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
 }
 
 // softmax/top-8 and grouping of nb tokens; eptr filled from layer L's table
@@ -495,6 +497,8 @@ int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *
     if (!lw.rc8) HC(hipMalloc(&lw.rc8, (size_t)MNE * MH * 2));
     k_router_chainmajor<16><<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rc16);
     k_router_chainmajor<8><<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rc8);
+    if (!lw.rf8) HC(hipMalloc(&lw.rf8, (size_t)MNE * MH * 4));
+    k_router_chain8_f32<<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rf8);
     HC(hipGetLastError());
     HC(hipStreamSynchronize(S.st));
     if (post_ln) {
