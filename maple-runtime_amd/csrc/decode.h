@@ -247,9 +247,16 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     DEC_TS(23, blockIdx.x == 3 && blockIdx.y == 1);
 }
 
-// Quantisation of two FF-long act vectors by one wave (maple.c:832 prep, as quant_wave): lanes 0-31 take
-// vector a0, lanes 32-63 vector a1; lane = one 16-column chunk (mfma order within each 128-column group).
+// ---------------------------------------------------------------------------------------------------------
+// Down GEMV + combine. grid = 2048 / 8 row blocks of 256 threads. Every block quantises all act vectors into
+// LDS (wave w takes pairs 8k + 2w, 8k + 2w + 1; block 0 also publishes them). Wave w computes the 8 rows for
+// the used experts u = w, w+4, ... (lane = row l/8, 64-column slice l%8); its code vectors are loaded while
+// the act vectors are quantised. Last, thread (token, row) runs the combine chain: mode 6 = step
+// (maple.c:664), mode 1 = step_batch (maple.c:834), as k_combine.
+// ---------------------------------------------------------------------------------------------------------
+#define DEC_DU (DEC_MAXP / 4)   // experts per wave
 struct ActChunk { float v[16]; };
+// lanes 0-31 load vector a0 = a, lanes 32-63 the vector the caller passes for them; lane = 16-column chunk
 __device__ __forceinline__ void act_load(const float *__restrict__ act, int a, int l, ActChunk &c) {
     int o = l & 31, g = o >> 3, h = (o >> 2) & 1, tq = o & 3;
     const float *xr = act + (size_t)a * MFF;
@@ -259,48 +266,6 @@ __device__ __forceinline__ void act_load(const float *__restrict__ act, int a, i
         c.v[s * 4] = f.x; c.v[s * 4 + 1] = f.y; c.v[s * 4 + 2] = f.z; c.v[s * 4 + 3] = f.w;
     }
 }
-__device__ __forceinline__ void act_quant(const ActChunk &c, int l, int8_t *q, float *qs, int *qsum) {
-    float mx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(c.v[i]));
-    mx = fmaxf(mx, __int_as_float(dpp<0xB1>(__float_as_int(mx))));
-    mx = fmaxf(mx, __int_as_float(dpp<0x4E>(__float_as_int(mx))));
-    mx = fmaxf(mx, __int_as_float(dpp<0x141>(__float_as_int(mx))));
-    mx = fmaxf(mx, __int_as_float(dpp<0x140>(__float_as_int(mx))));
-    int mb = __float_as_int(mx);
-    float m0 = fmaxf(__int_as_float(__builtin_amdgcn_readlane(mb, 0)), __int_as_float(__builtin_amdgcn_readlane(mb, 16)));
-    float m1 = fmaxf(__int_as_float(__builtin_amdgcn_readlane(mb, 32)), __int_as_float(__builtin_amdgcn_readlane(mb, 48)));
-    mx = l < 32 ? m0 : m1;
-    float qsv = 1.0f, inv = 1.0f;
-    if (mx > 0.0f) { qsv = mx * (1.0f / 127.0f); inv = 127.0f / mx; }
-    int sum = 0; uint32_t wds[4];
-#pragma unroll
-    for (int d = 0; d < 4; d++) {
-        uint32_t wd = 0;
-#pragma unroll
-        for (int bb = 0; bb < 4; bb++) {
-            int qi = (int)__builtin_rintf(c.v[d * 4 + bb] * inv);
-            sum += qi;
-            wd |= (uint32_t)(qi & 0xff) << (8 * bb);
-        }
-        wds[d] = wd;
-    }
-    int o = l & 31;
-    *(uint4 *)(q + (o >> 3) * DEC_GS + (o & 7) * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
-    sum += dpp<0xB1>(sum); sum += dpp<0x4E>(sum); sum += dpp<0x141>(sum); sum += dpp<0x140>(sum);
-    int s0 = __builtin_amdgcn_readlane(sum, 0) + __builtin_amdgcn_readlane(sum, 16);
-    int s1 = __builtin_amdgcn_readlane(sum, 32) + __builtin_amdgcn_readlane(sum, 48);
-    if ((l & 31) == 0) { *qs = qsv; *qsum = l < 32 ? s0 : s1; }
-}
-
-// ---------------------------------------------------------------------------------------------------------
-// Down GEMV + combine. grid = 2048 / 8 row blocks of 256 threads. Every block quantises all act vectors into
-// LDS (wave w takes pairs 8k + 2w, 8k + 2w + 1; block 0 also publishes them). Wave w computes the 8 rows for
-// the used experts u = w, w+4, ... (lane = row l/8, 64-column slice l%8); its code vectors are loaded while
-// the act vectors are quantised. Last, thread (token, row) runs the combine chain: mode 6 = step
-// (maple.c:664), mode 1 = step_batch (maple.c:834), as k_combine.
-// ---------------------------------------------------------------------------------------------------------
-#define DEC_DU (DEC_MAXP / 4)   // experts per wave
 __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan, const ExpPtr *__restrict__ eptr,
                                                   const float *__restrict__ act, int8_t *__restrict__ qa_out, float *__restrict__ qsa_out,
                                                   int *__restrict__ qsuma_out, const int *__restrict__ tp, const int *__restrict__ sp,
@@ -326,7 +291,7 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
     for (int k = 0; k < nb; k++) {
         int a = 8 * k + 2 * wv + (l >> 5);
         if (k > 0) act_load(act, a, l, c0);
-        act_quant(c0, l, qa[a], &qsa[a], &qsuma[a]);
+        quant_half<DEC_GS>(c0.v, l, qa[a], &qsa[a], &qsuma[a]);
     }
     __syncthreads();
     DEC_TS(35, blockIdx.x == 7);

@@ -428,7 +428,7 @@ __global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int 
 #pragma unroll
     for (int c = 0; c < MAXCH; c++) hv[c] = c < nchunk ? hist[c * MNE + e] : 0;   // independent loads
 #pragma unroll
-    for (int c = 0; c < MAXCH; c++) if (c < nchunk) { base[c * MNE + e] = run; run += hv[c]; }
+    for (int c = 0; c < MAXCH; c++) { int h = hv[c]; hv[c] = run; run += h; }   // hv: exclusive prefix over chunks
     int used = run > 0, nt = (run + tn - 1) / tn;
     sc[e] = run; su[e] = used; st[e] = nt;
     __syncthreads();
@@ -447,7 +447,8 @@ __global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int 
         if (layer_tab) eptr_u[uidx] = layer_tab[e];
         for (int i = 0; i < nt; i++) tiles[tstart + i] = Tile{uidx, pstart + i * tn, min(tn, run - i * tn), 0};
     }
-    for (int c = 0; c < nchunk; c++) base[c * MNE + e] += pstart;
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) if (c < nchunk) base[c * MNE + e] = hv[c] + pstart;
     if (e == MNE - 1) {
         int nu = su[e];
         plan->nu = nu; plan->np = sc[e]; plan->ntile_gu = st[e]; plan->tn = tn;
@@ -455,33 +456,37 @@ __global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int 
     }
 }
 
-// Block = one chunk of 64 tokens, thread = token. Pair slot of (b, s) = base[chunk][e] + number of earlier
-// tokens of the chunk that picked e, counted as popcount of a per-expert 64-bit token mask of the chunk.
-// Writes utok/uw (maple.c:934-936), tp (pair ids of token b ascending) and sp (pair id of slot s, for the
-// decode combine order).
-__global__ void __launch_bounds__(64) k_scatter(const int *__restrict__ top, const float *__restrict__ tw, int nb,
-                                                const int *__restrict__ base, int *__restrict__ utok, float *__restrict__ uw,
-                                                int *__restrict__ tp, int *__restrict__ sp) {
+// Block = one chunk of 64 tokens, 512 threads, thread = one (token, slot) pair. Pair slot of (b, s) =
+// base[chunk][e] + number of earlier tokens of the chunk that picked e, counted as the popcount of a
+// per-expert 64-bit token mask of the chunk. Writes utok/uw (maple.c:934-936), tp (pair ids of token b
+// ascending) and sp (pair id of slot s, for the decode combine order).
+__global__ void __launch_bounds__(512) k_scatter(const int *__restrict__ top, const float *__restrict__ tw, int nb,
+                                                 const int *__restrict__ base, int *__restrict__ utok, float *__restrict__ uw,
+                                                 int *__restrict__ tp, int *__restrict__ sp) {
     __shared__ unsigned long long msk[MNE];
-    int c = blockIdx.x, t = threadIdx.x, b = c * 64 + t;
-    for (int e = t; e < MNE; e += 64) msk[e] = 0ull;
+    __shared__ int slots[64][MTOPK];
+    int c = blockIdx.x, t = threadIdx.x, tk = t >> 3, s = t & 7, b = c * 64 + tk;
+    if (t < MNE) msk[t] = 0ull;
     __syncthreads();
-    int ex[MTOPK];
-    if (b < nb)
-        for (int s = 0; s < MTOPK; s++) { ex[s] = top[b * MTOPK + s]; atomicOr(&msk[ex[s]], 1ull << t); }
+    bool live = b < nb;
+    int e = live ? top[b * MTOPK + s] : 0;
+    float wv = live ? tw[b * MTOPK + s] : 0.0f;
+    int bs = live ? base[c * MNE + e] : 0;
+    if (live) atomicOr(&msk[e], 1ull << tk);
     __syncthreads();
-    if (b >= nb) return;
-    unsigned long long below = (1ull << t) - 1ull;
-    int a[MTOPK];
-    for (int s = 0; s < MTOPK; s++) {
-        int e = ex[s];
-        int slot = base[c * MNE + e] + __popcll(msk[e] & below);
-        utok[slot] = b; uw[slot] = tw[b * MTOPK + s];
-        a[s] = slot;
+    int slot = bs + __popcll(msk[e] & ((1ull << tk) - 1ull));
+    if (live) {
+        utok[slot] = b; uw[slot] = wv;
         if (sp) sp[b * MTOPK + s] = slot;
     }
-    for (int i = 1; i < MTOPK; i++) { int v = a[i], j = i - 1; while (j >= 0 && a[j] > v) { a[j + 1] = a[j]; j--; } a[j + 1] = v; }
-    for (int s = 0; s < MTOPK; s++) tp[b * MTOPK + s] = a[s];
+    slots[tk][s] = slot;
+    __syncthreads();
+    if (live) {
+        int rank = 0;
+#pragma unroll
+        for (int k = 0; k < MTOPK; k++) rank += slots[tk][k] < slot;
+        tp[b * MTOPK + rank] = slot;
+    }
 }
 
 // Host-given grouping (gpre_moe / gfull_moe / gpux): plan from ustart; one thread.
@@ -562,6 +567,95 @@ __global__ void __launch_bounds__(256) k_quant(const float *__restrict__ x, int 
     quant_wave<N>(x + (size_t)row * N, l, q + (size_t)row * N, qs + row, qsum + row);
 }
 
+// Quantisation of two FF-long (512) vectors by one wave, as quant_wave: lanes 0-31 hold one vector, lanes
+// 32-63 the other, lane = one 16-column chunk o (values v[s*4+b] = columns (o>>3)*128 + s*32 +
+// ((o>>2)&1)*16 + (o&3)*4 + b). Output in mfma order with GS bytes per 128-column group (128 in global
+// memory, more in padded LDS copies); lane 0 of each half writes qs and qsum. store = false: the half takes
+// part in the wave-wide reductions but writes nothing.
+template <int GS>
+__device__ __forceinline__ void quant_half(const float *v, int l, int8_t *q, float *qs, int *qsum, bool store = true) {
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+    mx = fmaxf(mx, __int_as_float(dpp<0xB1>(__float_as_int(mx))));
+    mx = fmaxf(mx, __int_as_float(dpp<0x4E>(__float_as_int(mx))));
+    mx = fmaxf(mx, __int_as_float(dpp<0x141>(__float_as_int(mx))));
+    mx = fmaxf(mx, __int_as_float(dpp<0x140>(__float_as_int(mx))));
+    int mb = __float_as_int(mx);
+    float m0 = fmaxf(__int_as_float(__builtin_amdgcn_readlane(mb, 0)), __int_as_float(__builtin_amdgcn_readlane(mb, 16)));
+    float m1 = fmaxf(__int_as_float(__builtin_amdgcn_readlane(mb, 32)), __int_as_float(__builtin_amdgcn_readlane(mb, 48)));
+    mx = l < 32 ? m0 : m1;
+    float qsv = 1.0f, inv = 1.0f;
+    if (mx > 0.0f) { qsv = mx * (1.0f / 127.0f); inv = 127.0f / mx; }
+    int sum = 0; uint32_t wds[4];
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        uint32_t wd = 0;
+#pragma unroll
+        for (int bb = 0; bb < 4; bb++) {
+            int qi = (int)__builtin_rintf(v[d * 4 + bb] * inv);
+            sum += qi;
+            wd |= (uint32_t)(qi & 0xff) << (8 * bb);
+        }
+        wds[d] = wd;
+    }
+    int o = l & 31;
+    if (store) *(uint4 *)(q + (o >> 3) * GS + (o & 7) * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
+    sum += dpp<0xB1>(sum); sum += dpp<0x4E>(sum); sum += dpp<0x141>(sum); sum += dpp<0x140>(sum);
+    int s0 = __builtin_amdgcn_readlane(sum, 0) + __builtin_amdgcn_readlane(sum, 16);
+    int s1 = __builtin_amdgcn_readlane(sum, 32) + __builtin_amdgcn_readlane(sum, 48);
+    if (store && (l & 31) == 0) { *qs = qsv; *qsum = l < 32 ? s0 : s1; }
+}
+
+// SiLU(min(g,7)) * clamp(u,-7,7) from the gate/up int32 sums, then the int8 quantisation of act
+// (maple.c:825-832). gu[pair][0..511] gate sums, [512..1023] up sums (sum of code * q, as written by
+// k_gateup32<SUMS>): G = (float)(sum - qsum) * qs * s_gate[row], likewise U. grid = tiles x 8 blocks of 8 pairs;
+// a wave takes 2 pairs (half-wave each). act (fp32, for checks) is written only when act != NULL.
+__global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
+                                                   const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
+                                                   const float *__restrict__ qsx, const int *__restrict__ qsumx,
+                                                   const int *__restrict__ gu, float *__restrict__ act, int8_t *__restrict__ qa,
+                                                   float *__restrict__ qsa, int *__restrict__ qsuma) {
+    int tile = blockIdx.x >> 3, part = blockIdx.x & 7;
+    if (tile >= plan->ntile_gu) return;
+    Tile tl = tiles[tile];
+    if (part * 8 >= tl.n) return;
+    int t = threadIdx.x, wv = t >> 6, l = t & 63;
+    int tk = part * 8 + wv * 2 + (l >> 5);
+    bool live = tk < tl.n;
+    int pair = tl.p0 + (live ? tk : 0);
+    ExpPtr ex = eptr[tl.u];
+    int tok = utok[pair];
+    int o = l & 31, g = o >> 3, h = (o >> 2) & 1, tq = o & 3;
+    int4 ag[4], au[4]; float4 sg[4], su[4];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        int col = g * 128 + s * 32 + h * 16 + tq * 4;
+        ag[s] = *(const int4 *)(gu + (size_t)pair * 2 * MFF + col);
+        au[s] = *(const int4 *)(gu + (size_t)pair * 2 * MFF + MFF + col);
+        sg[s] = *(const float4 *)(ex.gs + col);
+        su[s] = *(const float4 *)(ex.us + col);
+    }
+    float qs = qsx[tok]; int qsum = qsumx[tok];
+    float v[16];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        int agv[4] = {ag[s].x, ag[s].y, ag[s].z, ag[s].w}, auv[4] = {au[s].x, au[s].y, au[s].z, au[s].w};
+        float sgv[4] = {sg[s].x, sg[s].y, sg[s].z, sg[s].w}, suv[4] = {su[s].x, su[s].y, su[s].z, su[s].w};
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            float gv = (float)(agv[b] - qsum) * qs * sgv[b];
+            float uv = (float)(auv[b] - qsum) * qs * suv[b];
+            float gg = gv < 7.0f ? gv : 7.0f;
+            float uu = uv < -7.0f ? -7.0f : (uv > 7.0f ? 7.0f : uv);
+            v[s * 4 + b] = gg / (1.0f + dexp(-gg)) * uu;
+        }
+        if (act && live)
+            *(float4 *)(act + (size_t)pair * MFF + g * 128 + s * 32 + h * 16 + tq * 4) = make_float4(v[s * 4], v[s * 4 + 1], v[s * 4 + 2], v[s * 4 + 3]);
+    }
+    quant_half<128>(v, l, qa + (size_t)pair * MFF, qsa + pair, qsuma + pair, live);
+}
+
 // =====================================================================================================
 // Grouped ternary x int8 GEMM on CDNA4 int8 MFMA (v_mfma_i32_16x16x64_i8), shared by gate/up and down.
 //
@@ -584,11 +678,15 @@ __device__ __forceinline__ v4i decode_word(uint32_t w) {
 }
 
 // Work-item order for the 8 XCDs: the hardware hands consecutive workgroup ids to XCDs round robin, so
-// workgroup id b is mapped to logical item (b % 8) * (n / 8) + b / 8 (n padded to a multiple of 8). Each XCD
-// then walks a contiguous run of logical items; items are ordered (token tile, row block) with the row block
-// fastest, so the tiles of one expert -- sharing its codes -- and the row blocks of one tile -- sharing its
-// activations -- meet in the same XCD's L2.
-__device__ __forceinline__ int xcd_item(int b, int n) { return (b & 7) * (n >> 3) + (b >> 3); }
+// workgroup id b runs on XCD b % 8. The n real items (known on the device only; the grid is sized for the
+// worst case) are split into 8 contiguous runs of ceil(n / 8), and workgroup b takes item b / 8 of run b % 8
+// (-1: nothing to do). Items are ordered (token tile, row block) with the row block fastest, so the tiles of
+// one expert -- sharing its codes -- and the row blocks of one tile -- sharing its activations -- meet in the
+// same XCD's L2, and all 8 XCDs get the same number of items whatever the grid size.
+__device__ __forceinline__ int xcd_item(int b, int n) {
+    int per = (n + 7) >> 3, j = b >> 3, item = (b & 7) * per + j;
+    return j < per && item < n ? item : -1;
+}
 
 // Gate+up with fused SiLU*up (maple.c:471-479, 825-830). Block = WAVES waves; wave w owns RF 16-row
 // fragments of gate rows and the same RF fragments of up rows; the block covers WAVES*RF*16 rows of both.
@@ -616,9 +714,9 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
     constexpr int NPC = (TN * 16 + NT - 1) / NT;  // 16-byte activation pieces per thread per chunk
     __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
     __shared__ int toks[TN];
-    int item = xcd_item(blockIdx.x, gridDim.x);
+    int item = xcd_item(blockIdx.x, plan->ntile_gu * RB);
+    if (item < 0) return;
     int tile = item / RB, rb = item % RB;
-    if (tile >= plan->ntile_gu) return;
     Tile tl = tiles[tile];
     int p0 = tl.p0, ntok = tl.n;
     ExpPtr ex = eptr[tl.u];
@@ -734,7 +832,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
 // Block = 4 waves; wave w owns 32 gate rows and the same 32 up rows; the block covers 128 of each and TN = 64
 // tokens (2 token fragments of 32). Pipeline as k_gateup: codes two chunks ahead in registers, activations
 // two chunks ahead in registers then LDS (2 stages, slot p ^ (tk & 15) swizzle).
-template <int MODE = 0>
+template <int MODE = 0, bool SUMS = false>
 __global__ void __launch_bounds__(256) k_gateup32(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                   const ExpPtr *__restrict__ eptr,
                                                   const int *__restrict__ utok, const int8_t *__restrict__ qx,
@@ -747,9 +845,9 @@ __global__ void __launch_bounds__(256) k_gateup32(const Plan *__restrict__ plan,
     constexpr int NPC = TN * 16 / NT;          // 4 activation pieces of 16 bytes per thread per chunk
     __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
     __shared__ int toks[TN];
-    int item = xcd_item(blockIdx.x, gridDim.x);
+    int item = xcd_item(blockIdx.x, plan->ntile_gu * RB);
+    if (item < 0) return;
     int tile = item / RB, rb = item % RB;
-    if (tile >= plan->ntile_gu) return;
     Tile tl = tiles[tile];
     int p0 = tl.p0, ntok = tl.n;
     ExpPtr ex = eptr[tl.u];
@@ -824,7 +922,24 @@ __global__ void __launch_bounds__(256) k_gateup32(const Plan *__restrict__ plan,
             for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst[k]]) = br[(ch + 1) % 2][k];
         }
     }
-    // epilogue: G, U -> act. Lane holds token r32 of each token fragment; rows (i/4)*8 + G2*4 + i%4.
+    // epilogue. Lane holds token r32 of each token fragment; rows (i/4)*8 + G2*4 + i%4.
+    if (SUMS) {                                  // int32 sums to gu = (int *)act; SiLU and quantisation in k_act_quant
+        int *gu = (int *)act;
+#pragma unroll
+        for (int j = 0; j < NF; j++) {
+            int tk = j * 32 + r32;
+            if (tk >= ntok) continue;
+            int pair = p0 + tk;
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                int row0 = rowblk + g * 8 + G2 * 4;
+                *(v4i *)(gu + (size_t)pair * 2 * MFF + row0) = v4i{acc[0][j][g * 4], acc[0][j][g * 4 + 1], acc[0][j][g * 4 + 2], acc[0][j][g * 4 + 3]};
+                *(v4i *)(gu + (size_t)pair * 2 * MFF + MFF + row0) = v4i{acc[1][j][g * 4], acc[1][j][g * 4 + 1], acc[1][j][g * 4 + 2], acc[1][j][g * 4 + 3]};
+            }
+        }
+        return;
+    }
+    // G, U -> act
 #pragma unroll
     for (int j = 0; j < NF; j++) {
         int tk = j * 32 + r32;
@@ -869,9 +984,9 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
     constexpr int LDSW = MFF + 16;
     constexpr int RB = MH / (WAVES * RF * 16);
     __shared__ __attribute__((aligned(16))) int8_t bs[TN * LDSW];
-    int item = xcd_item(blockIdx.x, gridDim.x);
+    int item = xcd_item(blockIdx.x, plan->ntile_gu * RB);
+    if (item < 0) return;
     int tile = item / RB, rb = item % RB;
-    if (tile >= plan->ntile_gu) return;
     Tile tl = tiles[tile];
     int p0 = tl.p0, ntok = tl.n;
     ExpPtr ex = eptr[tl.u];
@@ -947,9 +1062,9 @@ __global__ void __launch_bounds__(256) k_down32(const Plan *__restrict__ plan, c
     constexpr int TN = 64, NT = 256, NF = 2, NA = 2, RB = MH / 256;
     constexpr int NPC = TN * (MFF / 16) / NT;   // 8 pieces of 16 bytes per thread
     __shared__ __attribute__((aligned(16))) int8_t bs[TN * MFF];
-    int item = xcd_item(blockIdx.x, gridDim.x);
+    int item = xcd_item(blockIdx.x, plan->ntile_gu * RB);
+    if (item < 0) return;
     int tile = item / RB, rb = item % RB;
-    if (tile >= plan->ntile_gu) return;
     Tile tl = tiles[tile];
     int p0 = tl.p0, ntok = tl.n;
     ExpPtr ex = eptr[tl.u];

@@ -49,6 +49,7 @@ struct Work {
     float *qsx = nullptr, *qsa = nullptr, *act = nullptr, *down = nullptr;
     int *qsumx = nullptr, *qsuma = nullptr;
     int *dbg_gu = nullptr, *dbg_dn = nullptr;
+    int *gu = nullptr;              // gate/up int32 sums [P][1024] of the 64-token-tile path
     unsigned *counters = nullptr;   // [0] routing, [64 + u] per used expert: last-block-done counters (self-resetting)
 };
 
@@ -66,6 +67,7 @@ static int work_alloc(Work &w, int maxtok) {
     HC(hipMalloc(&w.qx, T * MH)); HC(hipMalloc(&w.qsx, T * 4)); HC(hipMalloc(&w.qsumx, T * 4));
     HC(hipMalloc(&w.act, P * MFF * 4)); HC(hipMalloc(&w.qa, P * MFF)); HC(hipMalloc(&w.qsa, P * 4)); HC(hipMalloc(&w.qsuma, P * 4));
     HC(hipMalloc(&w.down, P * MH * 4));
+    HC(hipMalloc(&w.gu, P * 2 * MFF * 4));
     HC(hipMalloc(&w.counters, (64 + MNE) * sizeof(unsigned)));
     HC(hipMemset(w.counters, 0, (64 + MNE) * sizeof(unsigned)));
     return 0;
@@ -163,7 +165,7 @@ static int stage_route_group(Work &w, int L, int nb, int tn) {
     if (launch(MMOE_K_GROUP, [&] {
             k_hist<<<nch, 256, 0, S.st>>>(w.top, nb, w.hist);
             k_plan<<<1, 256, 0, S.st>>>(w.hist, nch, w.base, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles);
-            k_scatter<<<nch, 64, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp);
+            k_scatter<<<nch, 512, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp);
         })) return -1;
     return 0;
 }
@@ -177,7 +179,10 @@ static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int 
 
 static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8); }  // xcd_item needs a multiple of 8
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
-    if (tn == 64) return launch(MMOE_K_GATEUP, [&] { k_gateup32<0><<<grid8(maxtiles * (MFF / 128)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
+    if (tn == 64) {   // int32 sums into gu (the debug buffer when checks are on: it has the same layout)
+        float *gu = (float *)(dg ? dg : w.gu);
+        return launch(MMOE_K_GATEUP, [&] { k_gateup32<0, true><<<grid8(maxtiles * (MFF / 128)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, gu, nullptr); });
+    }
     return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<grid8(maxtiles * (MFF / 16)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
 static int launch_down(Work &w, int maxtiles, int tn, int *dd) {
@@ -185,12 +190,20 @@ static int launch_down(Work &w, int maxtiles, int tn, int *dd) {
     return launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<grid8(maxtiles * (MH / 64)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
 }
 
+static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
+    if (tn == 64) {
+        const int *gu = dg ? dg : w.gu;
+        float *act = S.debug ? w.act : nullptr;
+        return launch(MMOE_K_QUANT_ACT, [&] { k_act_quant<<<maxtiles * 8, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, gu, act, w.qa, w.qsa, w.qsuma); });
+    }
+    return launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(np + 3) / 4, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); });
+}
 static int stage_experts(Work &w, int np, int nu_max, int tn) {
     LAST.w = &w; LAST.np = np; LAST.nu_max = nu_max; LAST.tn = tn; LAST.dec = 0;
     int maxtiles = np / tn + (nu_max < np ? nu_max : np);
     int *dg = S.debug ? w.dbg_gu : nullptr, *dd = S.debug ? w.dbg_dn : nullptr;
     if (launch_gateup(w, maxtiles, tn, dg)) return -1;
-    if (launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(np + 3) / 4, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); })) return -1;
+    if (launch_quant_act(w, maxtiles, tn, np, dg)) return -1;
     if (launch_down(w, maxtiles, tn, dd)) return -1;
     return 0;
 }
@@ -653,7 +666,7 @@ double mmoe_bench_stage(int kid, int reps) {
         switch (kid) {
             case MMOE_K_GATEUP: rc = launch_gateup(w, maxtiles, LAST.tn, nullptr); break;
             case MMOE_K_DOWN: rc = launch_down(w, maxtiles, LAST.tn, nullptr); break;
-            case MMOE_K_QUANT_ACT: rc = launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(LAST.np + 3) / 4, 256, 0, S.st>>>(w.act, LAST.np, w.qa, w.qsa, w.qsuma); }); break;
+            case MMOE_K_QUANT_ACT: rc = launch_quant_act(w, maxtiles, LAST.tn, LAST.np, nullptr); break;
             case MMOE_K_ROUTER: rc = LAST.hn ? stage_router(w, LAST.L, LAST.hn, LAST.nb, LAST.order) : -1; break;
             default: seterr("mmoe_bench_stage: kernel %d not repeatable", kid); return -1.0;
         }
