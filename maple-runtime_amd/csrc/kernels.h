@@ -972,6 +972,166 @@ __global__ void __launch_bounds__(256) k_gateup32(const Plan *__restrict__ plan,
     }
 }
 
+// One 256-column chunk of a gate/up tile for one wave: 8 steps of 32 columns; at each step the gate and up code
+// words (NA = 2 fragments) are decoded once and multiplied with NFU token fragments of 32 (NFU = 1 when the
+// tile has <= 32 tokens). Activation operands come from the LDS stage sp one
+// step ahead of their use; the body is branch-free so the scheduler can overlap LDS reads, decode and MFMA.
+// LDS stage layout: token tk's 256 bytes at tk * GU_LROW (16 bytes of padding per row: the 16 lanes of a
+// 16-byte read pass fall in 16 different bank groups, and a step is a constant offset).
+#define GU_LROW 272
+template <int NFU>
+__device__ __forceinline__ void gu_chunk(v16i (&acc)[2][2], const v4i (&cwc)[2][2], const int8_t *sp, int G2, int r32) {
+    v4i bv[2][NFU];
+#pragma unroll
+    for (int j = 0; j < NFU; j++) bv[0][j] = *(const v4i *)(sp + (j * 32 + r32) * GU_LROW + G2 * 128);
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+        if (t + 1 < 8) {
+#pragma unroll
+            for (int j = 0; j < NFU; j++) bv[(t + 1) & 1][j] = *(const v4i *)(sp + (j * 32 + r32) * GU_LROW + G2 * 128 + (t + 1) * 16);
+        }
+#pragma unroll
+        for (int f = 0; f < 2; f++) {
+            v4i c4 = cwc[f][t >> 2];
+            int tt = t & 3;
+            v4i av = decode_word((uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w));
+#pragma unroll
+            for (int j = 0; j < NFU; j++) acc[f][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[t & 1][j], acc[f][j], 0, 0, 0);
+        }
+        // issue order of one step: next step's LDS reads, gate decode, gate MFMAs, up decode, up MFMAs
+        if (t + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, NFU, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NFU, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 7, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, NFU, 0);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+}
+
+// Persistent gate+up on the 32x32x32 int8 MFMA, int32 sums out (operand mapping, tile shape and LDS
+// layout as k_gateup32). grid = 8 * NB workgroups; the ones on XCD x = blockIdx % 8 walk that XCD's
+// contiguous run of items (as xcd_item) with stride NB, so an XCD's L2 sees the tiles of few experts at a
+// time. The chunk pipeline runs on across items: while the last three chunks of one item are multiplied, the
+// first three of the next are loaded (codes and activations PD = 3 chunks ahead in 4-slot register rings,
+// activations then through two LDS stages), so no item starts with an empty pipeline.
+__global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
+                                                      const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
+                                                      const int8_t *__restrict__ qx, int *__restrict__ gu) {
+    constexpr int TN = 64, NT = 256, NF = 2, NA = 2, RB = MFF / 128, NCH = MH / 256, BB = TN * GU_LROW;
+    constexpr int NPC = TN * 16 / NT;          // 4 activation pieces of 16 bytes per thread per chunk
+    constexpr int PD = 3;                      // prefetch distance of the codes in chunks (ring of 4)
+    constexpr int PA = 2;                      // prefetch distance of the activations (ring of 2 + 2 LDS stages)
+    __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
+    __shared__ int toks[2][TN];
+    int nitems = plan->ntile_gu * RB;
+    int per = (nitems + 7) >> 3, xcd = blockIdx.x & 7, nbx = gridDim.x >> 3;
+    int last = min(nitems, (xcd + 1) * per);
+    int cur = xcd * per + (blockIdx.x >> 3);
+    if (cur >= last) return;
+    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G2 = l >> 5, r32 = l & 31;
+    // a thread's activation pieces k: token tk = (tid >> 4) + 16 k, 16-byte part tid & 15 of the chunk
+    int part = tid & 15, bdst = (tid >> 4) * GU_LROW + part * 16;
+
+    // current item: uniform bases (scalar registers) + 32-bit per-lane offsets
+    Tile tl = tiles[cur / RB];
+    int p0 = tl.p0, ntok = tl.n, rowblk = (cur % RB) * 128 + wv * 32;
+    const uint8_t *gcb = eptr[tl.u].gc, *ucb = eptr[tl.u].uc;
+    if (tid < TN) toks[0][tid] = utok[p0 + (tid < ntok ? tid : 0)];
+    __syncthreads();
+    int slot = 0;
+    uint32_t aoff = (uint32_t)(rowblk + r32) * (MH / 4) + G2 * 32, boff[NPC];
+#pragma unroll
+    for (int k = 0; k < NPC; k++) boff[k] = (uint32_t)toks[0][(tid >> 4) + 16 * k] * MH + part * 16;
+    v16i acc[NA][NF];
+#pragma unroll
+    for (int f = 0; f < NA; f++)
+#pragma unroll
+        for (int j = 0; j < NF; j++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
+    v4i cw[4][NA][2];   // codes of chunk c of any item in slot c % 4
+    v4i br[2][NPC];     // activations of chunk c in slot c % 2 until stored to LDS stage c % 2
+#define GU_LOADC(slot_, gb_, ub_, off_, c_)                                                                     \
+    {                                                                                                           \
+        cw[slot_][0][0] = *(const gptr_u4 *)((gb_) + (off_) + (c_) * 64);                                      \
+        cw[slot_][0][1] = *(const gptr_u4 *)((gb_) + (off_) + (c_) * 64 + 16);                                 \
+        cw[slot_][1][0] = *(const gptr_u4 *)((ub_) + (off_) + (c_) * 64);                                      \
+        cw[slot_][1][1] = *(const gptr_u4 *)((ub_) + (off_) + (c_) * 64 + 16);                                 \
+    }
+#pragma unroll
+    for (int c = 0; c < PD; c++) GU_LOADC(c, gcb, ucb, aoff, c);
+#pragma unroll
+    for (int c = 0; c < PA; c++)
+#pragma unroll
+        for (int k = 0; k < NPC; k++) br[c][k] = *(const gptr_u4 *)(qx + boff[k] + c * 256);
+#pragma unroll
+    for (int k = 0; k < NPC; k++) *(v4i *)(&bs[0][bdst + k * 16 * GU_LROW]) = br[0][k];
+
+    while (true) {
+        int nxt = cur + nbx;
+        bool has_next = nxt < last;
+        // next item: tile and expert now (scalar loads), its token ids into registers now and LDS at chunk 2
+        Tile ntl = tiles[(has_next ? nxt : cur) / RB];
+        int nrowblk = ((has_next ? nxt : cur) % RB) * 128 + wv * 32;
+        const uint8_t *ngcb = eptr[ntl.u].gc, *nucb = eptr[ntl.u].uc;
+        uint32_t naoff = (uint32_t)(nrowblk + r32) * (MH / 4) + G2 * 32, nboff[NPC];
+        int ntk = 0;
+        if (has_next && tid < TN) ntk = utok[ntl.p0 + (tid < ntl.n ? tid : 0)];
+#pragma unroll
+        for (int ch = 0; ch < NCH; ch++) {
+            __syncthreads();
+            if (ch == 2 && tid < TN) toks[slot ^ 1][tid] = ntk;     // read after the barrier of chunk 3
+            if (ch == NCH - PA && has_next) {
+#pragma unroll
+                for (int k = 0; k < NPC; k++) nboff[k] = (uint32_t)toks[slot ^ 1][(tid >> 4) + 16 * k] * MH + part * 16;
+            }
+            // prefetch codes of chunk ch + PD and activations of chunk ch + PA (of this item, or of the next one)
+            if (ch + PD < NCH) GU_LOADC((ch + PD) % 4, gcb, ucb, aoff, ch + PD)
+            else if (has_next) GU_LOADC((ch + PD) % 4, ngcb, nucb, naoff, (ch + PD) % NCH)
+            if (ch + PA < NCH) {
+#pragma unroll
+                for (int k = 0; k < NPC; k++) br[ch % 2][k] = *(const gptr_u4 *)(qx + boff[k] + (ch + PA) * 256);
+            } else if (has_next) {
+#pragma unroll
+                for (int k = 0; k < NPC; k++) br[ch % 2][k] = *(const gptr_u4 *)(qx + nboff[k] + ((ch + PA) % NCH) * 256);
+            }
+            gu_chunk<2>(acc, cw[ch % 4], &bs[ch % 2][0], G2, r32);
+            __builtin_amdgcn_sched_barrier(0);
+            if (ch + 1 < NCH || has_next) {
+#pragma unroll
+                for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst + k * 16 * GU_LROW]) = br[(ch + 1) % 2][k];
+            }
+        }
+        // epilogue: int32 gate and up sums of this item; token r32 of each fragment, rows (i/4)*8 + G2*4 + i%4
+#pragma unroll
+        for (int j = 0; j < NF; j++) {
+            int tk = j * 32 + r32;
+            if (tk < ntok) {
+                int pair = p0 + tk;
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    int row0 = rowblk + g * 8 + G2 * 4;
+                    *(v4i *)(gu + (size_t)pair * 2 * MFF + row0) = v4i{acc[0][j][g * 4], acc[0][j][g * 4 + 1], acc[0][j][g * 4 + 2], acc[0][j][g * 4 + 3]};
+                    *(v4i *)(gu + (size_t)pair * 2 * MFF + MFF + row0) = v4i{acc[1][j][g * 4], acc[1][j][g * 4 + 1], acc[1][j][g * 4 + 2], acc[1][j][g * 4 + 3]};
+                }
+            }
+        }
+        if (!has_next) break;
+#pragma unroll
+        for (int f = 0; f < NA; f++)
+#pragma unroll
+            for (int j = 0; j < NF; j++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
+        cur = nxt; slot ^= 1;
+        p0 = ntl.p0; ntok = ntl.n; rowblk = nrowblk;
+        gcb = ngcb; ucb = nucb; aoff = naoff;
+#pragma unroll
+        for (int k = 0; k < NPC; k++) boff[k] = nboff[k];
+    }
+#undef GU_LOADC
+}
+
 // Down (maple.c:498-505): D[pair][row] = (float)(sum c*qa - qsuma) * qsa * s_down[row]. Block = WAVES waves
 // of RF 16-row fragments; K = 512 staged in LDS at once. Pairs of a tile are contiguous (no gather).
 // 1-D grid of (token tile x row block) items in XCD order, as k_gateup.
@@ -1129,6 +1289,104 @@ __global__ void __launch_bounds__(256) k_down32(const Plan *__restrict__ plan, c
                 if (dbg) *(int4 *)(dbg + (size_t)pair * MH + row0) = make_int4(ad[0], ad[1], ad[2], ad[3]);
             }
     }
+}
+
+// Down per tile (operand mapping as k_down32): one workgroup takes a tile of up to 64 pairs of one expert
+// and RPB row blocks of 256 down rows. The tile's activations (64 x 512 int8) are staged in LDS once (rows
+// padded to DN_LROW bytes); the row blocks then run back to back, the codes of the next row block loaded
+// while the current one is multiplied. Wave w owns rows w*64 .. +64 of each row block (two 32-row
+// fragments) and both 32-pair fragments. grid = tiles x 8 / RPB items (XCD order as xcd_item).
+#define DN_LROW (MFF + 16)
+template <int RPB>
+__global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
+                                                      const ExpPtr *__restrict__ eptr, const int8_t *__restrict__ qa,
+                                                      const float *__restrict__ qsa, const int *__restrict__ qsuma,
+                                                      float *__restrict__ down, int *__restrict__ dbg) {
+    constexpr int TN = 64, NT = 256, NF = 2, NA = 2, NSPLIT = MH / 256 / RPB;
+    constexpr int NPC = TN * (MFF / 16) / NT;   // 8 pieces of 16 bytes per thread
+    __shared__ __attribute__((aligned(16))) int8_t bs[TN * DN_LROW];
+    __shared__ __attribute__((aligned(16))) float sds[MH];          // the expert's down scales
+    int item = xcd_item(blockIdx.x, plan->ntile_gu * NSPLIT);
+    if (item < 0) return;
+    int tile = item / NSPLIT, rb0 = (item % NSPLIT) * RPB;
+    Tile tl = tiles[tile];
+    int p0 = tl.p0, ntok = tl.n;
+    const uint8_t *dcb = eptr[tl.u].dc;
+    const float *dsb = eptr[tl.u].ds;
+    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G2 = l >> 5, r32 = l & 31;
+    uint32_t aoff = (uint32_t)(wv * 64 + r32) * (MFF / 4) + G2 * 32;   // row block 0, fragment 0
+    v4i cw[2][NA][2][2];   // [row block parity][fragment][chunk][16 bytes]
+#define DN_LOADC(slot_, rb_)                                                                                   \
+    {                                                                                                          \
+        _Pragma("unroll") for (int f = 0; f < NA; f++)                                                         \
+        _Pragma("unroll") for (int c = 0; c < 2; c++) {                                                        \
+            const uint8_t *ap = dcb + aoff + (uint32_t)((rb_) * 256 + f * 32) * (MFF / 4) + c * 64;            \
+            cw[slot_][f][c][0] = *(const gptr_u4 *)ap;                                                         \
+            cw[slot_][f][c][1] = *(const gptr_u4 *)(ap + 16);                                                  \
+        }                                                                                                      \
+    }
+    DN_LOADC(0, rb0);
+    float qs[NF]; int qsm[NF];
+#pragma unroll
+    for (int j = 0; j < NF; j++) { int pr = p0 + min(j * 32 + r32, ntok - 1); qs[j] = qsa[pr]; qsm[j] = qsuma[pr]; }
+#pragma unroll
+    for (int k = 0; k < NPC; k++) {
+        int i = tid + k * NT, tk = i >> 5, part = i & 31;
+        int pr = p0 + (tk < ntok ? tk : 0);
+        *(v4i *)(&bs[tk * DN_LROW + part * 16]) = *(const gptr_u4 *)(qa + (size_t)pr * MFF + part * 16);
+    }
+    if (tid < RPB * 64) *(float4 *)(&sds[rb0 * 256 + tid * 4]) = *(const float4 *)(dsb + rb0 * 256 + tid * 4);
+    __syncthreads();
+#pragma unroll
+    for (int rr = 0; rr < RPB; rr++) {
+        int rb = rb0 + rr;
+        if (rr + 1 < RPB) DN_LOADC((rr + 1) & 1, rb + 1);
+        v16i acc[NA][NF];
+#pragma unroll
+        for (int f = 0; f < NA; f++)
+#pragma unroll
+            for (int j = 0; j < NF; j++)
+#pragma unroll
+                for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
+#pragma unroll
+        for (int c = 0; c < 2; c++)
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                int part = c * 16 + G2 * 8 + t;
+                v4i bv[NF];
+#pragma unroll
+                for (int j = 0; j < NF; j++) bv[j] = *(const v4i *)(bs + (j * 32 + r32) * DN_LROW + part * 16);
+#pragma unroll
+                for (int f = 0; f < NA; f++) {
+                    v4i c4 = cw[rr & 1][f][c][t >> 2];
+                    int tt = t & 3;
+                    v4i av = decode_word((uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w));
+#pragma unroll
+                    for (int j = 0; j < NF; j++) acc[f][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], acc[f][j], 0, 0, 0);
+                }
+            }
+        // D[pair][row] = (float)(sum - qsum) * qs * s_down[row]; lane: pair j*32 + r32, rows (i/4)*8 + G2*4 + i%4
+#pragma unroll
+        for (int j = 0; j < NF; j++) {
+            int tk = j * 32 + r32;
+            if (tk >= ntok) continue;
+            int pair = p0 + tk;
+#pragma unroll
+            for (int f = 0; f < NA; f++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    int row0 = rb * 256 + wv * 64 + f * 32 + g * 8 + G2 * 4;
+                    float4 sd = *(const float4 *)(&sds[row0]);
+                    float sdv[4] = {sd.x, sd.y, sd.z, sd.w};
+                    int ad[4]; float o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) { ad[i] = acc[f][j][g * 4 + i]; o[i] = (float)(ad[i] - qsm[j]) * qs[j] * sdv[i]; }
+                    *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
+                    if (dbg) *(int4 *)(dbg + (size_t)pair * MH + row0) = make_int4(ad[0], ad[1], ad[2], ad[3]);
+                }
+        }
+    }
+#undef DN_LOADC
 }
 
 // =====================================================================================================

@@ -18,6 +18,9 @@
 #include <vector>
 #include "kernels.h"
 #include "decode.h"
+#ifndef DN_RPB
+#define DN_RPB 2   // down row blocks of 256 per workgroup
+#endif
 
 extern "C" {
 #include "../../include/maplemoe.h"
@@ -108,6 +111,7 @@ static struct {
     hipEvent_t pe[2];
     double prof_ms[MMOE_PROF_NKERNELS]; long prof_n[MMOE_PROF_NKERNELS];
     hipGraphExec_t graph = nullptr;
+    int ncu = 256;             // compute units of the device (persistent grids)
 } S;
 
 static int ctx_ready() {
@@ -117,6 +121,8 @@ static int ctx_ready() {
     HC(hipStreamCreateWithFlags(&S.st, hipStreamNonBlocking));
     HC(hipEventCreate(&S.pe[0])); HC(hipEventCreate(&S.pe[1]));
     HC(hipEventCreate(&S.gx_ev));
+    int dev = 0; HC(hipGetDevice(&dev));
+    HC(hipDeviceGetAttribute(&S.ncu, hipDeviceAttributeMultiprocessorCount, dev));
     S.ready = true;
     return 0;
 }
@@ -181,12 +187,14 @@ static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8)
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
     if (tn == 64) {   // int32 sums into gu (the debug buffer when checks are on: it has the same layout)
         float *gu = (float *)(dg ? dg : w.gu);
-        return launch(MMOE_K_GATEUP, [&] { k_gateup32<0, true><<<grid8(maxtiles * (MFF / 128)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, gu, nullptr); });
+        int *gi = (int *)gu;
+        int nblk = (int)grid8(S.ncu < maxtiles * (MFF / 128) ? S.ncu : maxtiles * (MFF / 128));   // one persistent block per CU
+        return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, gi); });
     }
     return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<grid8(maxtiles * (MFF / 16)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
 static int launch_down(Work &w, int maxtiles, int tn, int *dd) {
-    if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down32<<<grid8(maxtiles * (MH / 256)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
+    if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
     return launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<grid8(maxtiles * (MH / 64)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
 }
 
