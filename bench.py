@@ -34,6 +34,18 @@ OPS_GU_PER_PAIR = 2 * 1024 * 2048
 OPS_DN_PER_PAIR = 2 * 2048 * 512
 
 
+def pmc_traffic(kernel):
+    """HBM bytes per dispatch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary, or None."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cols = [c.strip() for c in line.split("|")]
+        if len(cols) > 6 and cols[1] == kernel:
+            return int(cols[6])
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -94,7 +106,7 @@ def cpu_baseline_decode(blocks, routers, seconds):
     n, t0 = 0, time.perf_counter()
     while True:
         token(); n += 1
-        if time.perf_counter() - t0 >= seconds or n >= 2000:
+        if time.perf_counter() - t0 >= seconds:
             break
     dt = time.perf_counter() - t0
     return dict(value=n / dt, unit="tokens/s", cores=nt, kind="reference",
@@ -111,6 +123,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--graph", type=int, default=1, help="replay the 24-layer decode as a HIP graph")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="also run 3 plain device copies of MIB MiB (scale reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only: the MoE path of one MI355X; "
@@ -118,6 +132,12 @@ def main():
         sys.exit(2)
     lib = M.lib()
     M.check(lib.mmoe_init(2048), "mmoe_init")
+    if args.calib_copy:
+        nbytes = args.calib_copy << 20
+        a, b = lib.mmoe_dev_alloc(nbytes), lib.mmoe_dev_alloc(nbytes)
+        for _ in range(3):
+            M.check(lib.mmoe_d2d(b, a, nbytes), "calibration copy")
+        lib.mmoe_sync(); lib.mmoe_dev_free(a); lib.mmoe_dev_free(b)
     name, cus, clk = M.device_info()
     log(f"device {name}, {cus} CUs, {clk / 1e3:.0f} MHz")
 
@@ -162,8 +182,9 @@ def main():
     dn_ms = lib.mmoe_bench_stage(7, 200)
     log(f"  back-to-back: gateup {gu_ms * 1e3:.2f} us, down {dn_ms * 1e3:.2f} us per launch")
     gu_bytes = 8 * GU_BYTES_PER_EXPERT
-    roof = dict(bound="hbm", kernel="k_gateup (decode, 8 experts x 1024 rows)", achieved=round(gu_bytes / gu_ms / 1e6, 1),
-                peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gu_bytes / gu_ms / 1e6 / HBM_PEAK_GBS, 4), traffic=None,
+    roof = dict(bound="hbm", kernel="k_dec_gateup (decode, 8 experts x 1024 rows)", achieved=round(gu_bytes / gu_ms / 1e6, 1),
+                peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gu_bytes / gu_ms / 1e6 / HBM_PEAK_GBS, 4),
+                traffic=pmc_traffic("k_dec_gateup"),
                 algorithmic_bytes_per_launch=gu_bytes, avg_launch_us=round(gu_ms * 1e3, 2),
                 step_gbs=round(bytes_tok / ms / 1e6, 1), step_frac=round(bytes_tok / ms / 1e6 / HBM_PEAK_GBS, 4))
 
@@ -205,9 +226,9 @@ def main():
                        value=round(T / pms * 1e3, 1), unit="tokens/s", ms_per_layer=round(pms, 4),
                        layer_tops=round(ops / pms / 1e9, 1), layer_frac_int8_peak=round(ops / pms / 1e9 / INT8_PEAK_TOPS, 4),
                        experts_used=plan["nu"], max_expert_load=int(cnt.max()),
-                       roofline=dict(bound="mfma", kernel="k_gateup (grouped int8 MFMA)", achieved=round(g_ops / g_ms / 1e9, 1),
+                       roofline=dict(bound="mfma", kernel="k_gateup_pk (grouped int8 MFMA)", achieved=round(g_ops / g_ms / 1e9, 1),
                                      peak=INT8_PEAK_TOPS, unit="TOPS", frac=round(g_ops / g_ms / 1e9 / INT8_PEAK_TOPS, 4),
-                                     traffic=None, avg_launch_us=round(g_ms * 1e3, 2)),
+                                     traffic=pmc_traffic("k_gateup_pk"), avg_launch_us=round(g_ms * 1e3, 2)),
                        kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()})
 
     cpu = None
