@@ -123,6 +123,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--graph", type=int, default=1, help="replay the 24-layer decode as a HIP graph")
+    ap.add_argument("--router", choices=["exact", "mfma"], default="exact",
+                    help="router of the 2048-token prefill: fp32 FMA chains for every logit, or bf16 MFMA logits "
+                         "with each token's near-top-8 experts recomputed exactly")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
                     help="also run 3 plain device copies of MIB MiB (scale reference for rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
@@ -204,6 +207,8 @@ def main():
         hn = hn.astype(np.float32)
         d_hn = lib.mmoe_dev_alloc(hn.nbytes); d_xp = lib.mmoe_dev_alloc(hn.nbytes)
         lib.mmoe_h2d(d_hn, M.ptr(hn), hn.nbytes); lib.mmoe_h2d(d_xp, M.ptr(xs), xs.nbytes)
+
+        M.check(lib.mmoe_set_router_mode(1 if args.router == "exact" else 0), "router mode")
 
         def pstep():
             M.check(lib.mmoe_moe_dev(LP, d_hn, T, d_xp, M.ORDER_BATCH), "moe_dev")

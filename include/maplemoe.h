@@ -145,6 +145,10 @@ int mmoe_read(int what, void *dst, size_t bytes);
 int mmoe_set_debug(int on);
 /* Batches of <= 8 tokens use three fused decode kernels (default on); off = the grouped-GEMM path. */
 int mmoe_set_decode_path(int on);
+/* Router of batches of >= 128 tokens in batch order: 1 (default) = exact fp32 FMA chains for every logit;
+ * 0 = bf16 MFMA logits with the experts near each token's top 8 recomputed exactly (top-8 indices and their
+ * logits stay maple.c's; the other logits and the softmax weights are within 1e-5). */
+int mmoe_set_router_mode(int exact);
 const char *mmoe_last_error(void);
 
 /* Device memory on the library's device, and the library stream */

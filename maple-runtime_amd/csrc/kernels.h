@@ -314,6 +314,120 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ h
     }
 }
 
+// Large batches, approximate logits on the bf16 MFMA + exact refinement (k_cand, k_chain).
+// hn is split into two bf16 parts, h = h1 + h2 + r (h1 the top 8 significant bits by truncation, h2 the top 8
+// of what is left; both subtractions are exact and |r| <= 2^-15 |h|). The router is bf16 already, so every
+// product w * h_i is exact in fp32 and only the fp32 accumulation of the MFMA and the dropped r contribute
+// to the difference from maple.c's chain result L, bounded in k_cand.
+__global__ void __launch_bounds__(256) k_split2(const float *__restrict__ hn, int nb, uint16_t *__restrict__ hs,
+                                                float *__restrict__ hmax) {
+    int wv = threadIdx.x >> 6, l = threadIdx.x & 63, b = blockIdx.x * 4 + wv;
+    if (b >= nb) return;
+    const float *xr = hn + (size_t)b * MH;
+    float4 f[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) f[i] = *(const float4 *)(xr + (l + 64 * i) * 4);
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        float v[4] = {f[i].x, f[i].y, f[i].z, f[i].w};
+        uint32_t h1[4], h2[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            mx = fmaxf(mx, fabsf(v[u]));
+            uint32_t b1 = __float_as_uint(v[u]) & 0xffff0000u;
+            float r1 = v[u] - __uint_as_float(b1);
+            h1[u] = b1 >> 16; h2[u] = __float_as_uint(r1) >> 16;
+        }
+        int c = (l + 64 * i) * 4;
+        *(uint2 *)(hs + (size_t)b * MH + c) = make_uint2(h1[0] | (h1[1] << 16), h1[2] | (h1[3] << 16));
+        *(uint2 *)(hs + ((size_t)nb + b) * MH + c) = make_uint2(h2[0] | (h2[1] << 16), h2[2] | (h2[3] << 16));
+    }
+    mx = wave_max(mx);
+    if (l == 0) hmax[b] = mx;
+}
+
+// Partial logits on v_mfma_f32_32x32x16_bf16: P[q][b][e] = sum over columns [512 q, 512 q + 512) of
+// w[e][c] * (h1 + h2)[b][c]. Block: 64 experts x 64 tokens x one column quarter q (grid.z), 4 waves, wave
+// (we, wt) owns the 32 x 32 output fragment (we, wt). Columns advance in chunks of 64: the router chunk
+// (64 x 64 bf16) and the two input parts (2 x 64 x 64 bf16) are read with coalesced 16-byte loads into
+// registers two chunks ahead, then stored to LDS (rows padded to 72 bf16). k_cand adds the 4 partials.
+#define RM_KC 64
+#define RM_LR 72
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+__global__ void __launch_bounds__(256) k_router_mfma(const uint16_t *__restrict__ w, const uint16_t *__restrict__ hs, int nb,
+                                                     float *__restrict__ P) {
+    __shared__ __attribute__((aligned(16))) uint16_t ws[64 * RM_LR];
+    __shared__ __attribute__((aligned(16))) uint16_t hsl[2][64 * RM_LR];
+    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, r = l & 31, kg = l >> 5;
+    int we = wv >> 1, wt = wv & 1;
+    int e0 = blockIdx.y * 64, t0 = blockIdx.x * 64, kq = blockIdx.z * (MH / 4);
+    int srow = tid >> 3, spc = tid & 7;          // staging: row srow + 32 i, 16-byte piece spc of the chunk
+    const uint16_t *wsrc[2], *hsrc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        wsrc[i] = w + (size_t)(e0 + srow + 32 * i) * MH + kq + spc * 8;
+#pragma unroll
+        for (int sp = 0; sp < 2; sp++) hsrc[sp][i] = hs + ((size_t)sp * nb + min(t0 + srow + 32 * i, nb - 1)) * MH + kq + spc * 8;
+    }
+    v4i rw[2][2], rh[2][2][2];                   // [ring][row half] / [ring][part][row half]
+#define RM_LOAD(q_, k_)                                                                              \
+    {                                                                                                \
+        _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
+            rw[q_][i] = *(const gptr_u4 *)(wsrc[i] + (k_));                                          \
+            _Pragma("unroll") for (int sp = 0; sp < 2; sp++) rh[q_][sp][i] = *(const gptr_u4 *)(hsrc[sp][i] + (k_)); \
+        }                                                                                            \
+    }
+    RM_LOAD(0, 0);
+    RM_LOAD(1, RM_KC);
+    f32x16 acc;
+#pragma unroll
+    for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+#pragma unroll
+    for (int ck = 0; ck < MH / 4 / RM_KC; ck++) {
+        const int q = ck & 1;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            *(v4i *)(&ws[(srow + 32 * i) * RM_LR + spc * 8]) = rw[q][i];
+#pragma unroll
+            for (int sp = 0; sp < 2; sp++) *(v4i *)(&hsl[sp][(srow + 32 * i) * RM_LR + spc * 8]) = rh[q][sp][i];
+        }
+        __syncthreads();
+        if (ck + 2 < MH / 4 / RM_KC) RM_LOAD(q, (ck + 2) * RM_KC);
+#pragma unroll
+        for (int kk = 0; kk < RM_KC; kk += 16) {
+            bf16x8 av = *(const bf16x8 *)(&ws[(we * 32 + r) * RM_LR + kk + kg * 8]);
+#pragma unroll
+            for (int sp = 0; sp < 2; sp++) {
+                bf16x8 bv = *(const bf16x8 *)(&hsl[sp][(wt * 32 + r) * RM_LR + kk + kg * 8]);
+                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+            }
+        }
+    }
+#undef RM_LOAD
+    // D: register i -> expert row (i/4)*8 + kg*4 + i%4 of the fragment, token column r
+    float *Pq = P + (size_t)blockIdx.z * nb * MNE;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        int e = e0 + we * 32 + (i >> 2) * 8 + kg * 4 + (i & 3), tk = t0 + wt * 32 + r;
+        if (tk < nb) Pq[(size_t)tk * MNE + e] = acc[i];
+    }
+}
+
+// max over experts of sum_c |w_ec| (one block)
+__global__ void __launch_bounds__(256) k_router_l1max(const uint16_t *__restrict__ w, float *__restrict__ out) {
+    __shared__ float red[256];
+    int e = threadIdx.x;
+    float s = 0.0f;
+    for (int c = 0; c < MH; c++) s += fabsf(bf16f(w[(size_t)e * MH + c]));
+    red[e] = s;
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) { if (e < o) red[e] = fmaxf(red[e], red[e + o]); __syncthreads(); }
+    if (e == 0) out[0] = red[0] * 1.001f;   // margin for the float sum's own rounding
+}
+
 // =====================================================================================================
 // Softmax + top-8 + renormalisation, maple.c:910-923. One wave per token; lane l holds experts l, l+64,
 // l+128, l+192. Probabilities: p_e = exp(l_e - max) / sum, the sum taken as 8 interleaved partial sums
@@ -328,12 +442,12 @@ __device__ unsigned long long dec_ts[64];
 #else
 #define TK_TS(i) do {} while (0)
 #endif
-// One wave, one token: rl_row[256] -> top[8], tw[8]. E = 256 floats of LDS scratch.
-// Selection: p >= 0, so key = p_bits + 1 orders like p, and 0 marks a picked expert. Each of the 8 rounds
+// One wave, one token: rl_row[256] -> top[8], tw[8] (and lane l returns the expert of slot l % 8).
+// E = 256 floats of LDS scratch. Selection: p >= 0, so key = p_bits + 1 orders like p, and 0 marks a picked expert. Each of the 8 rounds
 // takes the largest key (lane-local over 4, DPP within 16-lane rows, the 4 row results as scalars), then the
 // lowest expert index holding it (ballots in index order: e = l + 64 i), which is the pick order of maple.c's
 // repeated strict-> scans, ties included.
-__device__ __forceinline__ void topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
+__device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
     TK_TS(40); TK_TS(41);
     float lg[4];
 #pragma unroll
@@ -387,8 +501,17 @@ __device__ __forceinline__ void topk_wave(const float *__restrict__ r, float *E,
 #pragma unroll
         for (int k = 0; k < MTOPK; k++) { top[k] = ek[k]; tw[k] = pk[k] / (tsum + 1e-20f); }
     }
+    int mine = 0;   // lane l returns the expert of slot l % 8
+#pragma unroll
+    for (int k = 0; k < MTOPK; k++) mine = (l & (MTOPK - 1)) == k ? ek[k] : mine;
+    return mine;
 }
 
+// Top-8 and the int8 quantisation of the MoE input (maple.c:909-923 and 908 prep) of 4 tokens per block,
+// one wave per token; adds each token's 8 experts to hist (per chunk of 64 tokens) when hist is given.
+__global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl, const float *__restrict__ hn, int nb,
+                                                    int *__restrict__ top, float *__restrict__ tw, int8_t *__restrict__ qx,
+                                                    float *__restrict__ qsx, int *__restrict__ qsumx, int *__restrict__ hist);
 __global__ void __launch_bounds__(256) k_topk(const float *__restrict__ rl, int nb, int *__restrict__ top, float *__restrict__ tw) {
     __shared__ float E[4][MNE];
     int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
@@ -433,6 +556,48 @@ __global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int 
     sc[e] = run; su[e] = used; st[e] = nt;
     __syncthreads();
     // inclusive Hillis-Steele scans over 256 entries (integer, exact)
+    for (int o = 1; o < MNE; o <<= 1) {
+        int a = e >= o ? sc[e - o] : 0, bq = e >= o ? su[e - o] : 0, cq = e >= o ? st[e - o] : 0;
+        __syncthreads();
+        sc[e] += a; su[e] += bq; st[e] += cq;
+        __syncthreads();
+    }
+    int pstart = sc[e] - run, uidx = su[e] - used, tstart = st[e] - nt;
+    if (used) {
+        plan->ue[uidx] = e;
+        plan->ustart[uidx] = pstart;
+        plan->tstart[uidx] = tstart;
+        if (layer_tab) eptr_u[uidx] = layer_tab[e];
+        for (int i = 0; i < nt; i++) tiles[tstart + i] = Tile{uidx, pstart + i * tn, min(tn, run - i * tn), 0};
+    }
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) if (c < nchunk) base[c * MNE + e] = hv[c] + pstart;
+    if (e == MNE - 1) {
+        int nu = su[e];
+        plan->nu = nu; plan->np = sc[e]; plan->ntile_gu = st[e]; plan->tn = tn;
+        plan->ustart[nu] = sc[e]; plan->tstart[nu] = st[e];
+    }
+}
+
+// The plan for the device-side routing of a large batch, in one block, from the per-chunk expert counts
+// hist[chunk of 64 tokens][expert] that k_topk_quant accumulated (read, then cleared for the next call).
+__global__ void __launch_bounds__(256) k_plan_top(int *__restrict__ hist, int nb, int *__restrict__ base, Plan *__restrict__ plan,
+                                                  const ExpPtr *__restrict__ layer_tab, ExpPtr *__restrict__ eptr_u, int tn,
+                                                  Tile *__restrict__ tiles) {
+    constexpr int MAXCH = (2048 + 63) / 64;
+    __shared__ int sc[MNE], su[MNE], st[MNE];
+    int e = threadIdx.x, nchunk = (nb + 63) / 64;
+    int cnt[MAXCH];
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) cnt[c] = c < nchunk ? hist[c * MNE + e] : 0;   // independent loads
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) if (c < nchunk) hist[c * MNE + e] = 0;        // ready for the next call
+    int run = 0, hv[MAXCH];
+#pragma unroll
+    for (int c = 0; c < MAXCH; c++) { hv[c] = run; run += cnt[c]; }   // hv: exclusive prefix over chunks
+    int used = run > 0, nt = (run + tn - 1) / tn;
+    sc[e] = run; su[e] = used; st[e] = nt;
+    __syncthreads();
     for (int o = 1; o < MNE; o <<= 1) {
         int a = e >= o ? sc[e - o] : 0, bq = e >= o ? su[e - o] : 0, cq = e >= o ? st[e - o] : 0;
         __syncthreads();
@@ -565,6 +730,127 @@ __global__ void __launch_bounds__(256) k_quant(const float *__restrict__ x, int 
     int row = blockIdx.x * 4 + wv;
     if (row >= nrows) return;
     quant_wave<N>(x + (size_t)row * N, l, q + (size_t)row * N, qs + row, qsum + row);
+}
+
+__global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl, const float *__restrict__ hn, int nb,
+                                                    int *__restrict__ top, float *__restrict__ tw, int8_t *__restrict__ qx,
+                                                    float *__restrict__ qsx, int *__restrict__ qsumx, int *__restrict__ hist) {
+    __shared__ float E[4][MNE];
+    int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
+    int b = blockIdx.x * 4 + wv;
+    if (b >= nb) return;  // whole wave exits together
+    int ek = topk_wave(rl + (size_t)b * MNE, E[wv], l, top + b * MTOPK, tw + b * MTOPK);
+    if (hist && l < MTOPK) atomicAdd(&hist[(b >> 6) * MNE + ek], 1);   // per-chunk expert counts for k_plan_top
+    quant_wave<MH>(hn + (size_t)b * MH, l, qx + (size_t)b * MH, qsx + b, qsumx + b);
+}
+
+// Exact top-8 from approximate logits (k_router_mfma), in two kernels before k_topk_quant.
+// |A - L| <= RG_ERRK * max|h_b| * max_e sum_c |w_ec| = err_b bounds the gap between the MFMA logit A and
+// maple.c's chain logit L: 2 * 2048 fp32 accumulations on the MFMA side and 256 + 3 on the chain side, each
+// at most one rounding of 2^-24 times the running magnitude (at most sum |w h|), plus the dropped input
+// remainder (2^-15 = 512 x 2^-24 of |h|), 4867 x 2^-24 x sum |w h| in all; times 1.01 for the bf16 parts and
+// 2 for safety. Every expert with A >= a8 - 2 err_b (a8 = the 8th largest A) is a candidate and gets its exact
+// chain logit in maple.c's batch order; no other expert can reach the top 8 of the exact logits, because the 8
+// experts with A >= a8 have L >= a8 - err_b while the rest have L < a8 - err_b. The softmax/top-8 of
+// k_topk_quant then runs on the row of exact (candidates) and approximate (the rest) logits, so the picks and
+// their order are maple.c's; p, and so tw, differ only through the softmax sum's approximate small terms.
+#define RG_ERRK (2.0f * 4867.0f * 1.01f / 16777216.0f)
+#define RG_MAXC 32   // candidates per token resolved by the chain kernel; more than that: all 256 experts
+// k_cand: one wave per token: candidate list cand[b][0..nc) (ascending expert), nc in ncand[b]
+// A = (P0 + P1) + (P2 + P3) + bias is written to rl; k_chain then overwrites the candidates' entries.
+__global__ void __launch_bounds__(256) k_cand(const float *__restrict__ P, int nb, const float *__restrict__ bias,
+                                              const float *__restrict__ hmax, const float *__restrict__ w1max,
+                                              float *__restrict__ rl, int *__restrict__ cand, int *__restrict__ ncand) {
+    int wv = threadIdx.x >> 6, l = threadIdx.x & 63, b = blockIdx.x * 4 + wv;
+    if (b >= nb) return;
+    float a[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        size_t o = (size_t)b * MNE + l + 64 * i, qs = (size_t)nb * MNE;
+        float v = (P[o] + P[o + qs]) + (P[o + 2 * qs] + P[o + 3 * qs]);
+        if (bias) v = v + bias[l + 64 * i];
+        a[i] = v; rl[o] = v;
+    }
+    float err = RG_ERRK * hmax[b] * w1max[0];
+    float rem[4] = {a[0], a[1], a[2], a[3]}, a8 = 0.0f;
+    for (int k = 0; k < MTOPK; k++) {
+        float m = wave_max(fmaxf(fmaxf(rem[0], rem[1]), fmaxf(rem[2], rem[3])));
+        a8 = m;
+        unsigned long long m0 = __ballot(rem[0] == m), m1 = __ballot(rem[1] == m), m2 = __ballot(rem[2] == m), m3 = __ballot(rem[3] == m);
+        int e = m0 ? __ffsll((long long)m0) - 1 : m1 ? 64 + __ffsll((long long)m1) - 1 : m2 ? 128 + __ffsll((long long)m2) - 1 : 192 + __ffsll((long long)m3) - 1;
+        if (l == (e & 63)) { int i = e >> 6; rem[0] = i == 0 ? -INFINITY : rem[0]; rem[1] = i == 1 ? -INFINITY : rem[1]; rem[2] = i == 2 ? -INFINITY : rem[2]; rem[3] = i == 3 ? -INFINITY : rem[3]; }
+    }
+    float thr = a8 - 2.0f * err;
+    int nc = 0;
+    unsigned long long lanemask = (1ull << l) - 1ull;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        bool c = a[i] >= thr;
+        unsigned long long m = __ballot(c);
+        int pos = nc + popc64(m & lanemask);
+        if (c && pos < RG_MAXC) cand[(size_t)b * RG_MAXC + pos] = l + 64 * i;
+        nc += popc64(m);
+    }
+    if (l == 0) ncand[b] = nc;
+}
+// k_chain: exact chain logits (maple.c:870-889 order, 8 chains over columns j + 8m, hsum8, + bias) of the
+// candidates, written over the approximate logits. Block = 4 tokens x 8 candidate slots x 8 chains; grid.y
+// = RG_MAXC / 8 groups of candidate slots (tokens with more than RG_MAXC candidates: every expert, all groups
+// striding over 256). wc8 = router chain-major (wc8[e][j][m] = w[e][j + 8 m]).
+__global__ void __launch_bounds__(256) k_chain(const float *__restrict__ hn, int nb, const uint16_t *__restrict__ wc8,
+                                               const float *__restrict__ bias, const int *__restrict__ cand,
+                                               const int *__restrict__ ncand, float *__restrict__ rl) {
+    __shared__ __attribute__((aligned(16))) float hsc[4][8][260];
+    int tid = threadIdx.x, tk = tid >> 6, l = tid & 63, j = l & 7, slot = l >> 3;
+    int b = blockIdx.x * 4 + tk;
+    bool live = b < nb;
+    int bb = live ? b : nb - 1;
+    const float *xr = hn + (size_t)bb * MH;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int c = (l + 64 * i) * 4;
+        float4 f = *(const float4 *)(xr + c);
+        hsc[tk][(c & 7) + 0][c >> 3] = f.x; hsc[tk][(c & 7) + 1][c >> 3] = f.y;
+        hsc[tk][(c & 7) + 2][c >> 3] = f.z; hsc[tk][(c & 7) + 3][c >> 3] = f.w;
+    }
+    __syncthreads();
+    if (!live) return;
+    int nc = ncand[b];
+    bool all = nc > RG_MAXC;
+    int n = all ? MNE : nc;
+    // slots of this block: blockIdx.y * 8 + slot, + gridDim.y * 8, ... (one round unless every expert is needed)
+    for (int c0 = blockIdx.y * 8; c0 < n; c0 += gridDim.y * 8) {   // c0 is uniform over the wave
+        int ci = c0 + slot;
+        bool on = ci < n;
+        int e = all ? (on ? ci : 0) : cand[(size_t)b * RG_MAXC + (on ? ci : 0)];
+        const gptr_u4 *wp = (const gptr_u4 *)(wc8 + ((size_t)e * 8 + j) * 256);
+        const float *hc = &hsc[tk][j][0];
+        float acc = 0.0f;
+#pragma unroll 1
+        for (int mb = 0; mb < 4; mb++) {
+            v4i wq[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) wq[q] = wp[mb * 8 + q];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                float4 h0 = *(const float4 *)(hc + mb * 64 + q * 8), h1 = *(const float4 *)(hc + mb * 64 + q * 8 + 4);
+                v4i wv = wq[q];
+                uint32_t q0 = (uint32_t)wv.x, q1 = (uint32_t)wv.y, q2 = (uint32_t)wv.z, q3 = (uint32_t)wv.w;
+                acc = __builtin_fmaf(__uint_as_float(q0 << 16), h0.x, acc); acc = __builtin_fmaf(__uint_as_float(q0 & 0xffff0000u), h0.y, acc);
+                acc = __builtin_fmaf(__uint_as_float(q1 << 16), h0.z, acc); acc = __builtin_fmaf(__uint_as_float(q1 & 0xffff0000u), h0.w, acc);
+                acc = __builtin_fmaf(__uint_as_float(q2 << 16), h1.x, acc); acc = __builtin_fmaf(__uint_as_float(q2 & 0xffff0000u), h1.y, acc);
+                acc = __builtin_fmaf(__uint_as_float(q3 << 16), h1.z, acc); acc = __builtin_fmaf(__uint_as_float(q3 & 0xffff0000u), h1.w, acc);
+            }
+        }
+        float s8[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) s8[i] = __shfl(acc, (l & ~7) + i, 64);
+        if (j == 0 && on) {
+            float r = hsum8(s8);
+            if (bias) r = r + bias[e];
+            rl[(size_t)b * MNE + e] = r;
+        }
+    }
 }
 
 // Quantisation of two FF-long (512) vectors by one wave, as quant_wave: lanes 0-31 hold one vector, lanes

@@ -53,6 +53,11 @@ struct Work {
     int *qsumx = nullptr, *qsuma = nullptr;
     int *dbg_gu = nullptr, *dbg_dn = nullptr;
     int *gu = nullptr;              // gate/up int32 sums [P][1024] of the 64-token-tile path
+    uint16_t *hs = nullptr;         // MoE input split into 2 bf16 parts [2][T][2048] (approximate router)
+    float *rpart = nullptr;         // partial router logits [4][T][256]
+    float *hmax = nullptr;          // max |hn| per token
+    int *cand = nullptr, *ncand = nullptr;   // refinement candidates [T][RG_MAXC], counts [T]
+    bool refine = false;            // the last router call left approximate logits for k_cand / k_chain
     unsigned *counters = nullptr;   // [0] routing, [64 + u] per used expert: last-block-done counters (self-resetting)
 };
 
@@ -64,6 +69,7 @@ static int work_alloc(Work &w, int maxtok) {
     HC(hipMalloc(&w.hn, T * MH * 4)); HC(hipMalloc(&w.x, T * MH * 4)); HC(hipMalloc(&w.rl, T * MNE * 4));
     HC(hipMalloc(&w.top, T * MTOPK * 4)); HC(hipMalloc(&w.tw, T * MTOPK * 4));
     HC(hipMalloc(&w.hist, (size_t)nch * MNE * 4)); HC(hipMalloc(&w.base, (size_t)nch * MNE * 4));
+    HC(hipMemset(w.hist, 0, (size_t)nch * MNE * 4));   // k_plan_top clears what it used
     HC(hipMalloc(&w.plan, sizeof(Plan))); HC(hipMalloc(&w.tiles, sizeof(Tile) * ((size_t)w.maxp / 16 + MNE + 8))); HC(hipMalloc(&w.eptr, MNE * sizeof(ExpPtr)));
     HC(hipMalloc(&w.utok, P * 4)); HC(hipMalloc(&w.uw, P * 4)); HC(hipMalloc(&w.tp, P * 4)); HC(hipMalloc(&w.sp, P * 4));
     HC(hipMalloc(&w.ustart, (MNE + 1) * 4));
@@ -71,6 +77,8 @@ static int work_alloc(Work &w, int maxtok) {
     HC(hipMalloc(&w.act, P * MFF * 4)); HC(hipMalloc(&w.qa, P * MFF)); HC(hipMalloc(&w.qsa, P * 4)); HC(hipMalloc(&w.qsuma, P * 4));
     HC(hipMalloc(&w.down, P * MH * 4));
     HC(hipMalloc(&w.gu, P * 2 * MFF * 4));
+    HC(hipMalloc(&w.hs, 2 * T * MH * 2)); HC(hipMalloc(&w.hmax, T * 4)); HC(hipMalloc(&w.rpart, 4 * T * MNE * 4));
+    HC(hipMalloc(&w.cand, T * RG_MAXC * 4)); HC(hipMalloc(&w.ncand, T * 4));
     HC(hipMalloc(&w.counters, (64 + MNE) * sizeof(unsigned)));
     HC(hipMemset(w.counters, 0, (64 + MNE) * sizeof(unsigned)));
     return 0;
@@ -89,7 +97,7 @@ static int work_debug(Work &w, int on) {
 // Global state
 // ------------------------------------------------------------------------------------------------------
 struct Region { const void *host; size_t len; uint8_t *dev; };
-struct LayerW { ExpPtr *tab = nullptr; uint16_t *router = nullptr; uint16_t *rc16 = nullptr, *rc8 = nullptr; float *rf8 = nullptr; uint16_t *post_ln = nullptr; float *bias = nullptr; };
+struct LayerW { ExpPtr *tab = nullptr; uint16_t *router = nullptr; uint16_t *rc16 = nullptr, *rc8 = nullptr; float *rf8 = nullptr, *w1max = nullptr; uint16_t *post_ln = nullptr; float *bias = nullptr; };
 
 static struct {
     bool ready = false;
@@ -148,8 +156,10 @@ static int launch(int kid, F &&f) {
 static int tile_tn(int np) { return np >= 2048 ? 64 : 16; }
 
 // Router logits of nb tokens (d_hn) with layer L's router; order 0 = batch (maple.c:853-889), 1 = step (bf_row)
+static bool S_router_exact = true;    // large batches: exact chain GEMM (else MFMA logits + exact refinement)
 static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
     LayerW &lw = S.layers[L];
+    w.refine = false;
     if (!lw.router) { seterr("layer %d has no router (mmoe_set_layer)", L); return -1; }
     if (order == MMOE_ORDER_STEP) {
         int n = nb * MNE * 16;
@@ -161,19 +171,31 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
     }
     if (nb < 128)
         return launch(MMOE_K_ROUTER, [&] { k_router_tiled<4><<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
-    return launch(MMOE_K_ROUTER, [&] { k_router_gemm<<<dim3((nb + RG_BT - 1) / RG_BT, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
+    if (S_router_exact)
+        return launch(MMOE_K_ROUTER, [&] { k_router_gemm<<<dim3((nb + RG_BT - 1) / RG_BT, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
+    // approximate logits on the bf16 MFMA; k_cand + k_chain make the top-8 exact
+    w.refine = true;
+    return launch(MMOE_K_ROUTER, [&] {
+        k_split2<<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, w.hs, w.hmax);
+        k_router_mfma<<<dim3((nb + 63) / 64, MNE / 64, 4), 256, 0, S.st>>>(lw.router, w.hs, nb, w.rpart);
+    });
 }
 
-// softmax/top-8 and grouping of nb tokens; eptr filled from layer L's table
-static int stage_route_group(Work &w, int L, int nb, int tn) {
+// softmax/top-8, the int8 quantisation of hn and the grouping of nb tokens; eptr filled from layer L's table
+static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) {
     int nch = (nb + 63) / 64;
-    if (launch(MMOE_K_TOPK, [&] { k_topk<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rl, nb, w.top, w.tw); })) return -1;
-    if (launch(MMOE_K_GROUP, [&] {
-            k_hist<<<nch, 256, 0, S.st>>>(w.top, nb, w.hist);
-            k_plan<<<1, 256, 0, S.st>>>(w.hist, nch, w.base, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles);
-            k_scatter<<<nch, 512, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp);
-        })) return -1;
-    return 0;
+    if (w.refine) {
+        const LayerW &lw = S.layers[L];
+        if (launch(MMOE_K_ROUTER, [&] {
+                k_cand<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rpart, nb, lw.bias, w.hmax, lw.w1max, w.rl, w.cand, w.ncand);
+                k_chain<<<dim3((nb + 3) / 4, 2), 256, 0, S.st>>>(d_hn, nb, lw.rc8, lw.bias, w.cand, w.ncand, w.rl);
+            })) return -1;
+    }
+    if (launch(MMOE_K_TOPK, [&] { k_topk_quant<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
+    return launch(MMOE_K_GROUP, [&] {
+        k_plan_top<<<1, 256, 0, S.st>>>(w.hist, nb, w.base, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles);
+        k_scatter<<<nch, 512, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp);
+    });
 }
 
 static int stage_quant_x(Work &w, const float *d_hn, int nb) {
@@ -258,8 +280,7 @@ static int moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) {
     int np = nb * MTOPK, tn = tile_tn(np);
     LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = d_hn; LAST.dec = 0;
     if (stage_router(w, L, d_hn, nb, order)) return -1;
-    if (stage_route_group(w, L, nb, tn)) return -1;
-    if (stage_quant_x(w, d_hn, nb)) return -1;
+    if (stage_route_group(w, L, nb, tn, d_hn)) return -1;
     if (stage_experts(w, np, MNE, tn)) return -1;
     return stage_combine(w, nb, d_x, order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH);
 }
@@ -495,6 +516,7 @@ int mmoe_init(int maxtok) {
 }
 
 // Small batches take the three-kernel decode path unless switched off (tests compare both paths).
+int mmoe_set_router_mode(int exact) { S_router_exact = exact != 0; return 0; }
 int mmoe_set_decode_path(int on) { S_dec_enabled = on != 0; return 0; }
 
 int mmoe_set_debug(int on) {
@@ -520,6 +542,8 @@ int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *
     k_router_chainmajor<8><<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rc8);
     if (!lw.rf8) HC(hipMalloc(&lw.rf8, (size_t)MNE * MH * 4));
     k_router_chain8_f32<<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rf8);
+    if (!lw.w1max) HC(hipMalloc(&lw.w1max, sizeof(float)));
+    k_router_l1max<<<1, 256, 0, S.st>>>(lw.router, lw.w1max);
     HC(hipGetLastError());
     HC(hipStreamSynchronize(S.st));
     if (post_ln) {

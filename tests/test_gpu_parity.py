@@ -30,20 +30,31 @@ def run_gpu(L, hn, x, order):
     return x_out
 
 
-def compare_layer(hl, nb, order, bias_note=""):
+def compare_layer(hl, nb, order, bias_note="", refined=False):
     x, hn = normed_hidden(SEED, nb, nb)
     nb = hn.shape[0]; P = nb * 8
     xg = run_gpu(hl.L, hn, x, order)
     xo = x.copy()
     o = O.moe_batch(hn, hl.router, hl.table, xo) if order == M.ORDER_BATCH else O.moe_step(hn[0], hl.router, hl.table, xo[0])
     print(f"\n[nb={nb} order={order}{bias_note}]", flush=True)
+    # refined: the MFMA router + exact refinement (mmoe_set_router_mode(0)); the logits of every token's
+    # top-8 experts are maple.c's chain results bit for bit, the rest are approximate
     rl = M.read("LOGITS", (nb, 256), np.float32)
-    assert np.array_equal(rl.view(np.int32), o["rl"].view(np.int32).reshape(nb, 256)), "router logits not bit-exact"
+    orl = o["rl"].reshape(nb, 256)
     top = M.read("TOP", (nb, 8), np.int32)
     assert np.array_equal(top, o["top"].reshape(nb, 8)), "top-8 indices differ"
+    if refined:
+        sel = np.take_along_axis(rl, top, 1), np.take_along_axis(orl, top, 1)
+        assert np.array_equal(sel[0].view(np.int32), sel[1].view(np.int32)), "top-8 logits not bit-exact"
+        # the other logits are an intermediate (only their softmax sum reaches tw): two bf16 parts of the input
+        # leave a 2^-15 remainder per term, so they sit ~1e-5 from the chain values; tw and x keep the 1e-5 bar
+        assert relmax(rl, orl) <= 1e-4
+        print("  approximate logits: relmax", relmax(rl, orl), "bit-exact share", float((rl == orl).mean()))
+    else:
+        assert np.array_equal(rl.view(np.int32), orl.view(np.int32)), "router logits not bit-exact"
     tw = M.read("TW", (nb, 8), np.float32)
     assert relmax(tw, o["tw"].reshape(nb, 8)) <= TOL
-    print("  tw bit-exact:", np.array_equal(tw, o["tw"].reshape(nb, 8)))
+    print("  tw bit-exact:", np.array_equal(tw, o["tw"].reshape(nb, 8)), "relmax", relmax(tw, o["tw"].reshape(nb, 8)))
     plan = M.read_plan()
     qx = M.mfma_to_natural(M.read("QX", (nb, 2048), np.int8), 2048)
     assert np.array_equal(qx, o["qx"]), "int8 input quantisation differs"
@@ -53,7 +64,8 @@ def compare_layer(hl, nb, order, bias_note=""):
         nu = int(o["nu"][0])
         assert plan["nu"] == nu and np.array_equal(plan["ue"], o["ue"][:nu]) and np.array_equal(plan["ustart"], o["ustart"][:nu + 1])
         assert np.array_equal(M.read("UTOK", (P,), np.int32), o["utok"])
-        assert np.array_equal(M.read("UW", (P,), np.float32), o["uw"])
+        uw = M.read("UW", (P,), np.float32)
+        assert relmax(uw, o["uw"]) <= TOL if refined else np.array_equal(uw, o["uw"])
         assert np.array_equal(M.read("TP", (nb, 8), np.int32), o["tp"])
         perm = np.arange(P)
     else:
@@ -192,3 +204,14 @@ def test_stack_decode(layer0):
                 O.moe_batch(hn, layers[L].router, layers[L].table, xo)
         print(f"\n  stack nb={nb}: bit-exact {np.array_equal(xg, xo)}, rel {relmax(xg - x0, xo - x0):.2e}")
         assert relmax(xg - x0, xo - x0) <= TOL
+
+
+def test_moe_batch_mfma_router(layer0):
+    """Batches of >= 128 tokens with the bf16-MFMA router and exact refinement of each token's candidates."""
+    lib = M.lib()
+    M.check(lib.mmoe_set_router_mode(0), "router mode")
+    try:
+        compare_layer(layer0, 256, M.ORDER_BATCH, " mfma router", refined=True)
+        compare_layer(layer0, 200, M.ORDER_BATCH, " mfma router", refined=True)
+    finally:
+        M.check(lib.mmoe_set_router_mode(1), "router mode")
