@@ -236,6 +236,37 @@ def main():
                                      traffic=pmc_traffic("k_gateup_pk"), avg_launch_us=round(g_ms * 1e3, 2)),
                        kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()})
 
+    # ---- config 3: batched decode, 64 sequences x 24 layers (batch order), and config 0: a 128-token chunk
+    extra = {}
+    if not args.no_prefill:
+        xb0 = M.synth_hidden(SEED, 3, 64)
+        d_xb = lib.mmoe_dev_alloc(xb0.nbytes); d_xb0 = lib.mmoe_dev_alloc(xb0.nbytes)
+        lib.mmoe_h2d(d_xb0, M.ptr(xb0), xb0.nbytes)
+
+        def bstep():
+            lib.mmoe_d2d(d_xb, d_xb0, xb0.nbytes)
+            M.check(lib.mmoe_stack_graph(0, NL, d_xb, 64, M.ORDER_BATCH, 1) if args.graph else
+                    lib.mmoe_stack_dev(0, NL, d_xb, 64, M.ORDER_BATCH), "batched decode")
+        lib.mmoe_graph_reset()
+        bms, _ = timed(bstep, max(5, args.steps // 5), 2)
+        lib.mmoe_graph_reset()
+        log(f"batched decode 64 x 24 layers: {bms * 1e3:.1f} us/step, {64 / bms * 1e3:.0f} tok/s")
+        extra["batched_decode"] = dict(workload="config 3: 64 sequences x 1 token x 24 MoE layers (batch order)",
+                                       value=round(64 / bms * 1e3, 1), unit="tokens/s", ms_per_step=round(bms, 4))
+        T0 = 128
+        M.check(lib.mmoe_set_bias(LP, None), "bias off")
+        x128 = M.synth_hidden(SEED, 4, T0)
+        h128 = (x128 / np.sqrt((x128.astype(np.float64) ** 2).mean(1, keepdims=True) + 1e-6)).astype(np.float32)
+        d_h128 = lib.mmoe_dev_alloc(h128.nbytes); d_x128 = lib.mmoe_dev_alloc(h128.nbytes)
+        lib.mmoe_h2d(d_h128, M.ptr(h128), h128.nbytes); lib.mmoe_h2d(d_x128, M.ptr(x128), x128.nbytes)
+
+        def cstep():
+            M.check(lib.mmoe_moe_dev(LP, d_h128, T0, d_x128, M.ORDER_BATCH), "moe_dev 128")
+        cms, _ = timed(cstep, max(5, args.steps // 5), 2)
+        log(f"prefill 128 (config 0): {cms * 1e3:.1f} us/layer, {T0 / cms * 1e3:.0f} tok/s")
+        extra["prefill_128"] = dict(workload="config 0: 128-token chunk, 1 MoE layer, unbiased router",
+                                    value=round(T0 / cms * 1e3, 1), unit="tokens/s", ms_per_layer=round(cms, 4))
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_decode(blocks, routers, args.cpu_seconds)
@@ -249,7 +280,7 @@ def main():
            "config": {"workload": "config 1: decode 1 token x 24 stacked MoE layers (d=2048, 256 experts, top-8, FF=512)",
                       "tokens_per_step": 1, "layers": NL, "hip_graph": bool(args.graph), "device": name},
            "roofline": roof, "cpu_baseline": cpu, "prefill": prefill,
-           "decode_kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in kt.items()}}
+           "decode_kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in kt.items()}, **extra}
     print(json.dumps(out), flush=True)
 
 

@@ -90,7 +90,7 @@ def compare_layer(hl, nb, order, bias_note="", refined=False):
     print("  x bit-exact:", np.array_equal(xg, xo), "rel", relmax(xg - x, xo - x))
 
 
-@pytest.mark.parametrize("nb", [1, 3, 32, 64, 100])
+@pytest.mark.parametrize("nb", [1, 3, 32, 64, 100, 128])   # 128: config 0 chunk
 def test_moe_batch(layer0, nb):
     compare_layer(layer0, nb, M.ORDER_BATCH)
 
@@ -185,7 +185,7 @@ def test_stack_decode(layer0):
         hl.rid = M.register_layer(L, hl.blk, hl.router, pln[L])
         layers.append(hl)
     M.register_layer(0, layer0.blk, layer0.router, pln[0])  # layer 0 again, now with its norm weight
-    for nb, order in [(1, M.ORDER_STEP), (4, M.ORDER_BATCH)]:
+    for nb, order in [(1, M.ORDER_STEP), (4, M.ORDER_BATCH), (64, M.ORDER_BATCH)]:   # 64: batched decode (config 3 shape)
         x0 = M.synth_hidden(SEED, 300 + nb, nb)
         d_x = lib.mmoe_dev_alloc(x0.nbytes)
         M.check(lib.mmoe_h2d(d_x, M.ptr(x0), x0.nbytes), "h2d")
