@@ -145,69 +145,60 @@ __device__ __forceinline__ float hsum8(const float *v) {
     return (a0 + a1) + (a2 + a3);
 }
 
-// Small batches: one thread per (token, expert, chain). Block 256 = 256/NCH (token, expert) logits.
+// Mid-size batches: one thread per (expert, chain) of one token, block = 256/NCH experts of token
+// blockIdx.y. The token's row sits in LDS chain-major (hc[j][m] = hn[j + NCH m]) and the router comes from
+// its chain-major copy (wc[e][j][m] = w[e][j + NCH m]), so a chain reads contiguous memory; its loads are
+// issued 16 at a time ahead of the FMAs. Chain j runs over columns j, j + NCH, ... with fma(w, x, acc); the
+// chains are then folded as described above (NCH = 16: chain j + chain j+8 first).
 template <int NCH>
-__global__ void __launch_bounds__(256) k_router_lanes(const float *__restrict__ hn, int nb, const uint16_t *__restrict__ w,
+__global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__ hn, int nb, const uint16_t *__restrict__ wc,
                                                        const float *__restrict__ bias, float *__restrict__ rl) {
-    int gid = blockIdx.x * 256 + threadIdx.x;
-    int j = gid % NCH, te = gid / NCH;
-    int e = te % MNE, b = te / MNE;
-    bool on = b < nb;
-    const uint16_t *wr = w + (size_t)e * MH;
-    const float *xr = hn + (size_t)(on ? b : 0) * MH;
+    constexpr int LEN = MH / NCH, HP = LEN + 4;
+    __shared__ __attribute__((aligned(16))) float hc[NCH * HP];
+    int tid = threadIdx.x, b = blockIdx.y, j = tid % NCH, e = blockIdx.x * (256 / NCH) + tid / NCH;
+    const gptr_u4 *wp = (const gptr_u4 *)(wc + ((size_t)e * NCH + j) * LEN);
+    v4i wv[16];
+#pragma unroll
+    for (int q = 0; q < 16; q++) wv[q] = wp[q];
+    const float *xr = hn + (size_t)b * MH;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        int c = (tid + 256 * i) * 4;
+        float4 f = *(const float4 *)(xr + c);
+        hc[((c + 0) % NCH) * HP + (c + 0) / NCH] = f.x; hc[((c + 1) % NCH) * HP + (c + 1) / NCH] = f.y;
+        hc[((c + 2) % NCH) * HP + (c + 2) / NCH] = f.z; hc[((c + 3) % NCH) * HP + (c + 3) / NCH] = f.w;
+    }
+    __syncthreads();
+    const float *h = hc + j * HP;
     float acc = 0.0f;
-    if (on)
-        for (int c = j; c < MH; c += NCH) acc = __builtin_fmaf(bf16f(wr[c]), xr[c], acc);
+#pragma unroll
+    for (int half = 0; half < LEN / 128; half++) {
+        if (half > 0) {
+#pragma unroll
+            for (int q = 0; q < 16; q++) wv[q] = wp[half * 16 + q];
+        }
+#pragma unroll
+        for (int q = 0; q < 16; q++) {
+            float4 h0 = *(const float4 *)(h + half * 128 + q * 8), h1 = *(const float4 *)(h + half * 128 + q * 8 + 4);
+            uint32_t q0 = (uint32_t)wv[q].x, q1 = (uint32_t)wv[q].y, q2 = (uint32_t)wv[q].z, q3 = (uint32_t)wv[q].w;
+            acc = __builtin_fmaf(__uint_as_float(q0 << 16), h0.x, acc); acc = __builtin_fmaf(__uint_as_float(q0 & 0xffff0000u), h0.y, acc);
+            acc = __builtin_fmaf(__uint_as_float(q1 << 16), h0.z, acc); acc = __builtin_fmaf(__uint_as_float(q1 & 0xffff0000u), h0.w, acc);
+            acc = __builtin_fmaf(__uint_as_float(q2 << 16), h1.x, acc); acc = __builtin_fmaf(__uint_as_float(q2 & 0xffff0000u), h1.y, acc);
+            acc = __builtin_fmaf(__uint_as_float(q3 << 16), h1.z, acc); acc = __builtin_fmaf(__uint_as_float(q3 & 0xffff0000u), h1.w, acc);
+        }
+    }
     float v[NCH];
-    int base = (threadIdx.x & 63) & ~(NCH - 1);  // lanes of one logit are consecutive and inside one wave
+    int base = (tid & 63) & ~(NCH - 1);
 #pragma unroll
     for (int i = 0; i < NCH; i++) v[i] = __shfl(acc, base + i, 64);
-    if (on && j == 0) {
-        float s[8];
-        if (NCH == 16) { for (int i = 0; i < 8; i++) s[i] = v[i] + v[i + 8]; }
-        else { for (int i = 0; i < 8; i++) s[i] = v[i]; }
-        float r = hsum8(s);
+    if (j == 0) {
+        float s8[8];
+        if (NCH == 16) { for (int i = 0; i < 8; i++) s8[i] = v[i] + v[i + 8]; }
+        else { for (int i = 0; i < 8; i++) s8[i] = v[i]; }
+        float r = hsum8(s8);
         if (bias) r = r + bias[e];
         rl[(size_t)b * MNE + e] = r;
     }
-}
-
-// Large batches (batch order only): block = 256 experts (one per thread) x RT tokens; the token's
-// activations are wave-uniform (scalar loads), the expert row streams per lane.
-template <int RT>
-__global__ void __launch_bounds__(256) k_router_tiled(const float *__restrict__ hn, int nb, const uint16_t *__restrict__ w,
-                                                       const float *__restrict__ bias, float *__restrict__ rl) {
-    int e = threadIdx.x, b0 = blockIdx.x * RT;
-    const uint16_t *wr = w + (size_t)e * MH;
-    float acc[RT][8];
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-#pragma unroll
-        for (int j = 0; j < 8; j++) acc[t][j] = 0.0f;
-    const float *xb[RT];
-#pragma unroll
-    for (int t = 0; t < RT; t++) xb[t] = hn + (size_t)min(b0 + t, nb - 1) * MH;
-    for (int c = 0; c < MH; c += 8) {
-        uint4 wv = *(const uint4 *)(wr + c);
-        float wf[8] = {__uint_as_float(wv.x << 16), __uint_as_float(wv.x & 0xffff0000u), __uint_as_float(wv.y << 16), __uint_as_float(wv.y & 0xffff0000u),
-                       __uint_as_float(wv.z << 16), __uint_as_float(wv.z & 0xffff0000u), __uint_as_float(wv.w << 16), __uint_as_float(wv.w & 0xffff0000u)};
-#pragma unroll
-        for (int t = 0; t < RT; t++) {
-            float4 x0 = *(const float4 *)(xb[t] + c), x1 = *(const float4 *)(xb[t] + c + 4);
-            acc[t][0] = __builtin_fmaf(wf[0], x0.x, acc[t][0]); acc[t][1] = __builtin_fmaf(wf[1], x0.y, acc[t][1]);
-            acc[t][2] = __builtin_fmaf(wf[2], x0.z, acc[t][2]); acc[t][3] = __builtin_fmaf(wf[3], x0.w, acc[t][3]);
-            acc[t][4] = __builtin_fmaf(wf[4], x1.x, acc[t][4]); acc[t][5] = __builtin_fmaf(wf[5], x1.y, acc[t][5]);
-            acc[t][6] = __builtin_fmaf(wf[6], x1.z, acc[t][6]); acc[t][7] = __builtin_fmaf(wf[7], x1.w, acc[t][7]);
-        }
-    }
-    float bv = bias ? bias[e] : 0.0f;
-#pragma unroll
-    for (int t = 0; t < RT; t++)
-        if (b0 + t < nb) {
-            float r = hsum8(acc[t]);
-            if (bias) r = r + bv;
-            rl[(size_t)(b0 + t) * MNE + e] = r;
-        }
 }
 
 // Large batches (batch order, NCH = 8) as a register-tiled GEMM that keeps maple.c's chains: one thread
@@ -216,7 +207,7 @@ __global__ void __launch_bounds__(256) k_router_tiled(const float *__restrict__ 
 // ws[j][m][expert] for column j + 8m, so a chain step reads 2 + 2 16-byte words. The router comes
 // pre-converted to fp32 in that order, wT[j][m][e] = w[e][j + 8m] (k_router_chain8_f32). Columns advance
 // in chunks of RG_MC steps, the next chunk loaded into registers while the current one is used.
-// After the last column the 8 chain values meet in LDS and are folded by hsum8, as in k_router_lanes.
+// After the last column the 8 chain values meet in LDS and are folded by hsum8.
 #define RG_BT 32
 #define RG_BE 64
 #define RG_MC 16
@@ -512,73 +503,6 @@ __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, 
 __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl, const float *__restrict__ hn, int nb,
                                                     int *__restrict__ top, float *__restrict__ tw, int8_t *__restrict__ qx,
                                                     float *__restrict__ qsx, int *__restrict__ qsumx, int *__restrict__ hist);
-__global__ void __launch_bounds__(256) k_topk(const float *__restrict__ rl, int nb, int *__restrict__ top, float *__restrict__ tw) {
-    __shared__ float E[4][MNE];
-    int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
-    int b = blockIdx.x * 4 + wv;
-    if (b >= nb) return;  // whole wave exits together
-    topk_wave(rl + (size_t)b * MNE, E[wv], l, top + b * MTOPK, tw + b * MTOPK);
-}
-
-// =====================================================================================================
-// Grouping by expert, maple.c:924-938 (counting sort, stable in token order) + tp (maple.c:1018-1019).
-// Three kernels: per-chunk histograms (64 tokens per chunk), one block scanning them into the plan, and a
-// scatter in which every (token, slot) finds its rank among earlier tokens of its chunk with that expert.
-// =====================================================================================================
-__global__ void __launch_bounds__(256) k_hist(const int *__restrict__ top, int nb, int *__restrict__ hist) {
-    __shared__ int cnt[MNE];
-    int c = blockIdx.x, t = threadIdx.x;
-    cnt[t] = 0;
-    __syncthreads();
-    for (int i = t; i < 64 * MTOPK; i += 256) {
-        int b = c * 64 + i / MTOPK;
-        if (b < nb) atomicAdd(&cnt[top[b * MTOPK + (i % MTOPK)]], 1);
-    }
-    __syncthreads();
-    hist[c * MNE + t] = cnt[t];
-}
-
-// One block of 256 threads (thread = expert). hist[nchunk][256] -> base[nchunk][256] (first pair slot of
-// chunk c's pairs of expert e) and the plan; eptr_u[u] = layer table entry of expert ue[u] if table given.
-__global__ void __launch_bounds__(256) k_plan(const int *__restrict__ hist, int nchunk, int *__restrict__ base, Plan *__restrict__ plan,
-                                              const ExpPtr *__restrict__ layer_tab, ExpPtr *__restrict__ eptr_u, int tn,
-                                              Tile *__restrict__ tiles) {
-    __shared__ int sc[MNE], su[MNE], st[MNE];
-    int e = threadIdx.x;
-    int run = 0;
-    constexpr int MAXCH = (2048 + 63) / 64;          // chunks of 64 tokens at the largest batch
-    int hv[MAXCH];
-#pragma unroll
-    for (int c = 0; c < MAXCH; c++) hv[c] = c < nchunk ? hist[c * MNE + e] : 0;   // independent loads
-#pragma unroll
-    for (int c = 0; c < MAXCH; c++) { int h = hv[c]; hv[c] = run; run += h; }   // hv: exclusive prefix over chunks
-    int used = run > 0, nt = (run + tn - 1) / tn;
-    sc[e] = run; su[e] = used; st[e] = nt;
-    __syncthreads();
-    // inclusive Hillis-Steele scans over 256 entries (integer, exact)
-    for (int o = 1; o < MNE; o <<= 1) {
-        int a = e >= o ? sc[e - o] : 0, bq = e >= o ? su[e - o] : 0, cq = e >= o ? st[e - o] : 0;
-        __syncthreads();
-        sc[e] += a; su[e] += bq; st[e] += cq;
-        __syncthreads();
-    }
-    int pstart = sc[e] - run, uidx = su[e] - used, tstart = st[e] - nt;
-    if (used) {
-        plan->ue[uidx] = e;
-        plan->ustart[uidx] = pstart;
-        plan->tstart[uidx] = tstart;
-        if (layer_tab) eptr_u[uidx] = layer_tab[e];
-        for (int i = 0; i < nt; i++) tiles[tstart + i] = Tile{uidx, pstart + i * tn, min(tn, run - i * tn), 0};
-    }
-#pragma unroll
-    for (int c = 0; c < MAXCH; c++) if (c < nchunk) base[c * MNE + e] = hv[c] + pstart;
-    if (e == MNE - 1) {
-        int nu = su[e];
-        plan->nu = nu; plan->np = sc[e]; plan->ntile_gu = st[e]; plan->tn = tn;
-        plan->ustart[nu] = sc[e]; plan->tstart[nu] = st[e];
-    }
-}
-
 // The plan for the device-side routing of a large batch, in one block, from the per-chunk expert counts
 // hist[chunk of 64 tokens][expert] that k_topk_quant accumulated (read, then cleared for the next call).
 __global__ void __launch_bounds__(256) k_plan_top(int *__restrict__ hist, int nb, int *__restrict__ base, Plan *__restrict__ plan,
@@ -895,7 +819,7 @@ __device__ __forceinline__ void quant_half(const float *v, int l, int8_t *q, flo
 
 // SiLU(min(g,7)) * clamp(u,-7,7) from the gate/up int32 sums, then the int8 quantisation of act
 // (maple.c:825-832). gu[pair][0..511] gate sums, [512..1023] up sums (sum of code * q, as written by
-// k_gateup32<SUMS>): G = (float)(sum - qsum) * qs * s_gate[row], likewise U. grid = tiles x 8 blocks of 8 pairs;
+// k_gateup_pk): G = (float)(sum - qsum) * qs * s_gate[row], likewise U. grid = tiles x 8 blocks of 8 pairs;
 // a wave takes 2 pairs (half-wave each). act (fp32, for checks) is written only when act != NULL.
 __global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                    const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
@@ -1011,11 +935,12 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
     __syncthreads();
 
     // activation pieces of this thread: piece i = tid + k*NT -> token i/16, part i%16 (slot part ^ (tk & 15))
-    const gptr_u4 *bsrc[NPC]; int bdst[NPC];
+    const gptr_u4 *bsrc[NPC]; int bdst[NPC]; bool blive[NPC];   // padding tokens of a short tile: zeros, not loaded
 #pragma unroll
     for (int k = 0; k < NPC; k++) {
         int i = tid + k * NT, tk = (i < TN * 16 ? i : 0) >> 4, part = i & 15;
         bsrc[k] = (const gptr_u4 *)(qx + (size_t)toks[tk] * MH + part * 16);
+        blive[k] = i < TN * 16 && tk < ntok;
         bdst[k] = i < TN * 16 ? tk * 256 + ((part ^ (tk & 15)) * 16) : -1;
     }
     int rowblk = rb * (WAVES * RF * 16) + wv * RF * 16;   // first gate (and up) row of this wave
@@ -1039,7 +964,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
 #pragma unroll
         for (int f = 0; f < NA; f++) cw[c][f] = arow[f][c * 4];
 #pragma unroll
-        for (int k = 0; k < NPC; k++) br[c][k] = bsrc[k][c * 16];
+        for (int k = 0; k < NPC; k++) br[c][k] = blive[k] ? bsrc[k][c * 16] : v4i{0, 0, 0, 0};
     }
 #pragma unroll
     for (int k = 0; k < NPC; k++) if (bdst[k] >= 0) *(v4i *)(&bs[0][bdst[k]]) = br[0][k];
@@ -1051,7 +976,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
             for (int f = 0; f < NA; f++) cw[(ch + 2) % 3][f] = arow[f][(ch + 2) * 4];
             if (MODE != 1) {
 #pragma unroll
-                for (int k = 0; k < NPC; k++) br[ch % 2][k] = bsrc[k][(ch + 2) * 16];
+                for (int k = 0; k < NPC; k++) br[ch % 2][k] = blive[k] ? bsrc[k][(ch + 2) * 16] : v4i{0, 0, 0, 0};
             }
         }
         const int8_t *sp = &bs[ch % 2][0];
@@ -1109,155 +1034,6 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
     }
 }
 
-// Gate+up for large token tiles on the 32x32x32 int8 MFMA (v_mfma_i32_32x32x32_i8, twice the rate of the
-// 16x16x64 form on gfx950). Operand mapping: A lane (G2 = lane/32, r = lane%32) holds 16 int8 of row r, B lane
-// (G2, n) the same 16 k positions of token n. Lane group G2 takes 128-column group G2 of each 256-column
-// chunk; at step t (0..7) its A operand is code word t of that group decoded in registers, and its B operand
-// the 16 contiguous bytes 16t.. of the group in mfma order (see the top of this file). D (16 int32 per lane):
-// register i holds row (i/4)*8 + G2*4 + i%4 of the 32-row block, token lane%32.
-// Block = 4 waves; wave w owns 32 gate rows and the same 32 up rows; the block covers 128 of each and TN = 64
-// tokens (2 token fragments of 32). Pipeline as k_gateup: codes two chunks ahead in registers, activations
-// two chunks ahead in registers then LDS (2 stages, slot p ^ (tk & 15) swizzle).
-template <int MODE = 0, bool SUMS = false>
-__global__ void __launch_bounds__(256) k_gateup32(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
-                                                  const ExpPtr *__restrict__ eptr,
-                                                  const int *__restrict__ utok, const int8_t *__restrict__ qx,
-                                                  const float *__restrict__ qsx, const int *__restrict__ qsumx,
-                                                  float *__restrict__ act, int *__restrict__ dbg) {
-    constexpr int TN = 64, NT = 256, NF = 2, NA = 2;
-    constexpr int RB = MFF / 128;
-    constexpr int NCH = MH / 256;
-    constexpr int BB = TN * 256;
-    constexpr int NPC = TN * 16 / NT;          // 4 activation pieces of 16 bytes per thread per chunk
-    __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
-    __shared__ int toks[TN];
-    int item = xcd_item(blockIdx.x, plan->ntile_gu * RB);
-    if (item < 0) return;
-    int tile = item / RB, rb = item % RB;
-    Tile tl = tiles[tile];
-    int p0 = tl.p0, ntok = tl.n;
-    ExpPtr ex = eptr[tl.u];
-    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G2 = l >> 5, r32 = l & 31;
-    if (tid < TN) toks[tid] = utok[p0 + (tid < ntok ? tid : 0)];
-    __syncthreads();
-
-    const gptr_u4 *bsrc[NPC]; int bdst[NPC];
-#pragma unroll
-    for (int k = 0; k < NPC; k++) {
-        int i = tid + k * NT, tk = i >> 4, part = i & 15;
-        bsrc[k] = (const gptr_u4 *)(qx + (size_t)toks[tk] * MH + part * 16);
-        bdst[k] = tk * 256 + ((part ^ (tk & 15)) * 16);
-    }
-    int rowblk = rb * 128 + wv * 32;           // this wave's first gate (and up) row
-    const gptr_u4 *arow[NA];
-    arow[0] = (const gptr_u4 *)(ex.gc + (size_t)(rowblk + r32) * (MH / 4) + G2 * 32);
-    arow[1] = (const gptr_u4 *)(ex.uc + (size_t)(rowblk + r32) * (MH / 4) + G2 * 32);
-    v16i acc[NA][NF];
-#pragma unroll
-    for (int f = 0; f < NA; f++)
-#pragma unroll
-        for (int j = 0; j < NF; j++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
-
-    v4i cw[3][NA][2];   // 32 code bytes per fragment per chunk: chunks ch, ch+1, ch+2
-    v4i br[2][NPC];
-#pragma unroll
-    for (int c = 0; c < 2; c++) {
-#pragma unroll
-        for (int f = 0; f < NA; f++) { cw[c][f][0] = arow[f][c * 4]; cw[c][f][1] = arow[f][c * 4 + 1]; }
-#pragma unroll
-        for (int k = 0; k < NPC; k++) br[c][k] = bsrc[k][c * 16];
-    }
-#pragma unroll
-    for (int k = 0; k < NPC; k++) *(v4i *)(&bs[0][bdst[k]]) = br[0][k];
-#pragma unroll
-    for (int ch = 0; ch < NCH; ch++) {
-        __syncthreads();
-        if (ch + 2 < NCH && MODE != 6 && MODE != 7) {
-#pragma unroll
-            for (int f = 0; f < NA; f++) { cw[(ch + 2) % 3][f][0] = arow[f][(ch + 2) * 4]; cw[(ch + 2) % 3][f][1] = arow[f][(ch + 2) * 4 + 1]; }
-            if (MODE != 1) {
-#pragma unroll
-                for (int k = 0; k < NPC; k++) br[ch % 2][k] = bsrc[k][(ch + 2) * 16];
-            }
-        }
-        const int8_t *sp = &bs[ch % 2][0];
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            int part = G2 * 8 + t;
-            v4i bv[NF];
-#pragma unroll
-            for (int j = 0; j < NF; j++) {
-                int tk = j * 32 + r32;
-                bv[j] = (MODE == 5 || MODE == 7) ? cw[ch % 3][j][0] : *(const v4i *)(sp + tk * 256 + ((part ^ (tk & 15)) * 16));
-            }
-#pragma unroll
-            for (int f = 0; f < NA; f++) {
-                v4i c4 = cw[ch % 3][f][t >> 2];
-                int tt = t & 3;
-                uint32_t w = (uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w);
-                v4i av = (MODE == 4 || MODE == 7) ? c4 : decode_word(w);
-                acc[f][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[0], acc[f][0], 0, 0, 0);
-                if (ntok > 32) acc[f][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[1], acc[f][1], 0, 0, 0);
-            }
-        }
-        if (ch + 1 < NCH) {
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst[k]]) = br[(ch + 1) % 2][k];
-        }
-    }
-    // epilogue. Lane holds token r32 of each token fragment; rows (i/4)*8 + G2*4 + i%4.
-    if (SUMS) {                                  // int32 sums to gu = (int *)act; SiLU and quantisation in k_act_quant
-        int *gu = (int *)act;
-#pragma unroll
-        for (int j = 0; j < NF; j++) {
-            int tk = j * 32 + r32;
-            if (tk >= ntok) continue;
-            int pair = p0 + tk;
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                int row0 = rowblk + g * 8 + G2 * 4;
-                *(v4i *)(gu + (size_t)pair * 2 * MFF + row0) = v4i{acc[0][j][g * 4], acc[0][j][g * 4 + 1], acc[0][j][g * 4 + 2], acc[0][j][g * 4 + 3]};
-                *(v4i *)(gu + (size_t)pair * 2 * MFF + MFF + row0) = v4i{acc[1][j][g * 4], acc[1][j][g * 4 + 1], acc[1][j][g * 4 + 2], acc[1][j][g * 4 + 3]};
-            }
-        }
-        return;
-    }
-    // G, U -> act
-#pragma unroll
-    for (int j = 0; j < NF; j++) {
-        int tk = j * 32 + r32;
-        if (tk >= ntok) continue;
-        int tok = toks[tk];
-        float qs = qsx[tok]; int qsum = qsumx[tok];
-        int pair = p0 + tk;
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            int row0 = rowblk + g * 8 + G2 * 4;
-            float4 sg = *(const float4 *)(ex.gs + row0), su = *(const float4 *)(ex.us + row0);
-            float sgv[4] = {sg.x, sg.y, sg.z, sg.w}, suv[4] = {su.x, su.y, su.z, su.w};
-            int ag[4], au[4];
-            float o[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                ag[i] = acc[0][j][g * 4 + i]; au[i] = acc[1][j][g * 4 + i];
-                float gv = (float)(ag[i] - qsum) * qs * sgv[i];
-                float uv = (float)(au[i] - qsum) * qs * suv[i];
-                float gg = gv < 7.0f ? gv : 7.0f;
-                float uu = uv < -7.0f ? -7.0f : (uv > 7.0f ? 7.0f : uv);
-                o[i] = (MODE == 3 || MODE == 7) ? gg + uu : gg / (1.0f + dexp(-gg)) * uu;
-            }
-            *(float4 *)(act + (size_t)pair * MFF + row0) = make_float4(o[0], o[1], o[2], o[3]);
-            if (dbg) {
-                *(int4 *)(dbg + (size_t)pair * 2 * MFF + row0) = make_int4(ag[0], ag[1], ag[2], ag[3]);
-                *(int4 *)(dbg + (size_t)pair * 2 * MFF + MFF + row0) = make_int4(au[0], au[1], au[2], au[3]);
-            }
-        }
-    }
-}
-
 // One 256-column chunk of a gate/up tile for one wave: 8 steps of 32 columns; at each step the gate and up code
 // words (NA = 2 fragments) are decoded once and multiplied with NFU token fragments of 32 (NFU = 1 when the
 // tile has <= 32 tokens). Activation operands come from the LDS stage sp one
@@ -1294,8 +1070,13 @@ __device__ __forceinline__ void gu_chunk(v16i (&acc)[2][2], const v4i (&cwc)[2][
     }
 }
 
-// Persistent gate+up on the 32x32x32 int8 MFMA, int32 sums out (operand mapping, tile shape and LDS
-// layout as k_gateup32). grid = 8 * NB workgroups; the ones on XCD x = blockIdx % 8 walk that XCD's
+// Persistent gate+up on v_mfma_i32_32x32x32_i8 (twice the rate of the 16x16x64 form on gfx950), int32 sums
+// out. Operand mapping: A lane (G2 = lane/32, r = lane%32) holds 16 int8 of row r, B lane (G2, n) the same 16
+// k positions of token n. Lane group G2 takes 128-column group G2 of each 256-column chunk; at step t (0..7)
+// its A operand is code word t of that group decoded in registers, and its B operand the 16 contiguous
+// bytes 16t.. of the group in mfma order (see the top of this file). D (16 int32 per lane): register i
+// holds row (i/4)*8 + G2*4 + i%4 of the 32-row block, token lane%32. An item is 128 gate + 128 up rows (wave w:
+// 32 of each) x a tile of 64 tokens (two fragments of 32). grid = 8 * NB workgroups; the ones on XCD x = blockIdx % 8 walk that XCD's
 // contiguous run of items (as xcd_item) with stride NB, so an XCD's L2 sees the tiles of few experts at a
 // time. The chunk pipeline runs on across items: while the last three chunks of one item are multiplied, the
 // first three of the next are loaded (codes and activations PD = 3 chunks ahead in 4-slot register rings,
@@ -1497,87 +1278,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
     }
 }
 
-// Down on the 32x32x32 int8 MFMA (operand mapping as k_gateup32): D[pair][row] = (float)(sum c*qa - qsuma) *
-// qsa * s_down[row]. Block = 4 waves; wave w owns rows w*64 .. +64 of the block's 256 (two 32-row fragments);
-// tile = 64 pairs (contiguous, no gather). K = 512: both chunks' code words are loaded at once, the tile's
-// activations are staged in LDS at once (slot p ^ (tk & 15) swizzle within each 256-byte half).
-__global__ void __launch_bounds__(256) k_down32(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
-                                                const ExpPtr *__restrict__ eptr, const int8_t *__restrict__ qa,
-                                                const float *__restrict__ qsa, const int *__restrict__ qsuma,
-                                                float *__restrict__ down, int *__restrict__ dbg) {
-    constexpr int TN = 64, NT = 256, NF = 2, NA = 2, RB = MH / 256;
-    constexpr int NPC = TN * (MFF / 16) / NT;   // 8 pieces of 16 bytes per thread
-    __shared__ __attribute__((aligned(16))) int8_t bs[TN * MFF];
-    int item = xcd_item(blockIdx.x, plan->ntile_gu * RB);
-    if (item < 0) return;
-    int tile = item / RB, rb = item % RB;
-    Tile tl = tiles[tile];
-    int p0 = tl.p0, ntok = tl.n;
-    ExpPtr ex = eptr[tl.u];
-    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G2 = l >> 5, r32 = l & 31;
-    int rowblk = rb * 256 + wv * 64;
-    v4i cw[NA][2][2];   // [fragment][chunk][16 bytes]
-#pragma unroll
-    for (int f = 0; f < NA; f++) {
-        const gptr_u4 *ar = (const gptr_u4 *)(ex.dc + (size_t)(rowblk + f * 32 + r32) * (MFF / 4) + G2 * 32);
-#pragma unroll
-        for (int c = 0; c < 2; c++) { cw[f][c][0] = ar[c * 4]; cw[f][c][1] = ar[c * 4 + 1]; }
-    }
-#pragma unroll
-    for (int k = 0; k < NPC; k++) {
-        int i = tid + k * NT, tk = i >> 5, part = i & 31;
-        int pr = p0 + (tk < ntok ? tk : 0);
-        v4i v = *(const gptr_u4 *)(qa + (size_t)pr * MFF + part * 16);
-        *(v4i *)(&bs[tk * MFF + ((part ^ (tk & 15)) * 16)]) = v;
-    }
-    __syncthreads();
-    v16i acc[NA][NF];
-#pragma unroll
-    for (int f = 0; f < NA; f++)
-#pragma unroll
-        for (int j = 0; j < NF; j++)
-#pragma unroll
-            for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
-#pragma unroll
-    for (int c = 0; c < 2; c++)
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            int part = c * 16 + G2 * 8 + t;
-            v4i bv[NF];
-#pragma unroll
-            for (int j = 0; j < NF; j++) { int tk = j * 32 + r32; bv[j] = *(const v4i *)(bs + tk * MFF + ((part ^ (tk & 15)) * 16)); }
-#pragma unroll
-            for (int f = 0; f < NA; f++) {
-                v4i c4 = cw[f][c][t >> 2];
-                int tt = t & 3;
-                v4i av = decode_word((uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w));
-                acc[f][0] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[0], acc[f][0], 0, 0, 0);
-                if (ntok > 32) acc[f][1] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[1], acc[f][1], 0, 0, 0);
-            }
-        }
-#pragma unroll
-    for (int j = 0; j < NF; j++) {
-        int tk = j * 32 + r32;
-        if (tk >= ntok) continue;
-        int pair = p0 + tk;
-        float qs = qsa[pair]; int qsum = qsuma[pair];
-#pragma unroll
-        for (int f = 0; f < NA; f++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                int row0 = rowblk + f * 32 + g * 8 + G2 * 4;
-                float4 sd = *(const float4 *)(ex.ds + row0);
-                float sdv[4] = {sd.x, sd.y, sd.z, sd.w};
-                int ad[4]; float o[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) { ad[i] = acc[f][j][g * 4 + i]; o[i] = (float)(ad[i] - qsum) * qs * sdv[i]; }
-                *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
-                if (dbg) *(int4 *)(dbg + (size_t)pair * MH + row0) = make_int4(ad[0], ad[1], ad[2], ad[3]);
-            }
-    }
-}
-
-// Down per tile (operand mapping as k_down32): one workgroup takes a tile of up to 64 pairs of one expert
+// Down per tile (operand mapping as k_gateup_pk, K = 512): one workgroup takes a tile of up to 64 pairs of one expert
 // and RPB row blocks of 256 down rows. The tile's activations (64 x 512 int8) are staged in LDS once (rows
 // padded to DN_LROW bytes); the row blocks then run back to back, the codes of the next row block loaded
 // while the current one is multiplied. Wave w owns rows w*64 .. +64 of each row block (two 32-row

@@ -162,15 +162,10 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
     w.refine = false;
     if (!lw.router) { seterr("layer %d has no router (mmoe_set_layer)", L); return -1; }
     if (order == MMOE_ORDER_STEP) {
-        int n = nb * MNE * 16;
-        return launch(MMOE_K_ROUTER, [&] { k_router_lanes<16><<<(n + 255) / 256, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
+        return launch(MMOE_K_ROUTER, [&] { k_router_chains<16><<<dim3(MNE * 16 / 256, nb), 256, 0, S.st>>>(d_hn, nb, lw.rc16, lw.bias, w.rl); });
     }
-    if (nb <= 16) {
-        int n = nb * MNE * 8;
-        return launch(MMOE_K_ROUTER, [&] { k_router_lanes<8><<<(n + 255) / 256, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
-    }
-    if (nb < 128)
-        return launch(MMOE_K_ROUTER, [&] { k_router_tiled<4><<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, lw.router, lw.bias, w.rl); });
+    if (nb < 512)   // one block per (token, 32 experts): 8 nb blocks, router reread from L2 per token
+        return launch(MMOE_K_ROUTER, [&] { k_router_chains<8><<<dim3(MNE * 8 / 256, nb), 256, 0, S.st>>>(d_hn, nb, lw.rc8, lw.bias, w.rl); });
     if (S_router_exact)
         return launch(MMOE_K_ROUTER, [&] { k_router_gemm<<<dim3((nb + RG_BT - 1) / RG_BT, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
     // approximate logits on the bf16 MFMA; k_cand + k_chain make the top-8 exact
