@@ -507,7 +507,7 @@ __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl
 // hist[chunk of 64 tokens][expert] that k_topk_quant accumulated (read, then cleared for the next call).
 __global__ void __launch_bounds__(256) k_plan_top(int *__restrict__ hist, int nb, int *__restrict__ base, Plan *__restrict__ plan,
                                                   const ExpPtr *__restrict__ layer_tab, ExpPtr *__restrict__ eptr_u, int tn,
-                                                  Tile *__restrict__ tiles) {
+                                                  Tile *__restrict__ tiles, int *__restrict__ eu) {
     constexpr int MAXCH = (2048 + 63) / 64;
     __shared__ int sc[MNE], su[MNE], st[MNE];
     int e = threadIdx.x, nchunk = (nb + 63) / 64;
@@ -529,6 +529,7 @@ __global__ void __launch_bounds__(256) k_plan_top(int *__restrict__ hist, int nb
         __syncthreads();
     }
     int pstart = sc[e] - run, uidx = su[e] - used, tstart = st[e] - nt;
+    eu[e] = used ? uidx : -1;   // expert -> used-expert index (for pu in k_scatter)
     if (used) {
         plan->ue[uidx] = e;
         plan->ustart[uidx] = pstart;
@@ -551,7 +552,8 @@ __global__ void __launch_bounds__(256) k_plan_top(int *__restrict__ hist, int nb
 // ascending) and sp (pair id of slot s, for the decode combine order).
 __global__ void __launch_bounds__(512) k_scatter(const int *__restrict__ top, const float *__restrict__ tw, int nb,
                                                  const int *__restrict__ base, int *__restrict__ utok, float *__restrict__ uw,
-                                                 int *__restrict__ tp, int *__restrict__ sp) {
+                                                 int *__restrict__ tp, int *__restrict__ sp, const int *__restrict__ eu,
+                                                 int *__restrict__ pu) {
     __shared__ unsigned long long msk[MNE];
     __shared__ int slots[64][MTOPK];
     int c = blockIdx.x, t = threadIdx.x, tk = t >> 3, s = t & 7, b = c * 64 + tk;
@@ -567,6 +569,7 @@ __global__ void __launch_bounds__(512) k_scatter(const int *__restrict__ top, co
     if (live) {
         utok[slot] = b; uw[slot] = wv;
         if (sp) sp[b * MTOPK + s] = slot;
+        if (pu) pu[slot] = eu[e];
     }
     slots[tk][s] = slot;
     __syncthreads();
@@ -817,14 +820,17 @@ __device__ __forceinline__ void quant_half(const float *v, int l, int8_t *q, flo
     if (store && (l & 31) == 0) { *qs = qsv; *qsum = l < 32 ? s0 : s1; }
 }
 
-// SiLU(min(g,7)) * clamp(u,-7,7) from the gate/up int32 sums, then the int8 quantisation of act
-// (maple.c:825-832). gu[pair][0..511] gate sums, [512..1023] up sums (sum of code * q, as written by
-// k_gateup_pk): G = (float)(sum - qsum) * qs * s_gate[row], likewise U. grid = tiles x 8 blocks of 8 pairs;
-// a wave takes 2 pairs (half-wave each). act (fp32, for checks) is written only when act != NULL.
+// SiLU(min(g,7)) * clamp(u,-7,7) from the gate/up sums, then the int8 quantisation of act (maple.c:825-832).
+// gu[pair][0..511] gate, [512..1023] up, as written by k_gateup_pk: D16 = false, int32 sums of code * q, and
+// d = sum - qsum here; D16 = true, d itself as int16, or -32768 with d in gov (int32, same index).
+// G = (float)d * qs * s_gate[row], likewise U. grid = tiles x 8 blocks of 8 pairs; a wave takes 2 pairs
+// (half-wave each). act (fp32, for checks) is written only when act != NULL.
+template <bool D16>
 __global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                    const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
                                                    const float *__restrict__ qsx, const int *__restrict__ qsumx,
-                                                   const int *__restrict__ gu, float *__restrict__ act, int8_t *__restrict__ qa,
+                                                   const void *__restrict__ gu, const int *__restrict__ gov,
+                                                   float *__restrict__ act, int8_t *__restrict__ qa,
                                                    float *__restrict__ qsa, int *__restrict__ qsuma) {
     int tile = blockIdx.x >> 3, part = blockIdx.x & 7;
     if (tile >= plan->ntile_gu) return;
@@ -837,25 +843,39 @@ __global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan
     ExpPtr ex = eptr[tl.u];
     int tok = utok[pair];
     int o = l & 31, g = o >> 3, h = (o >> 2) & 1, tq = o & 3;
-    int4 ag[4], au[4]; float4 sg[4], su[4];
+    int ag[4][4], au[4][4]; float4 sg[4], su[4];
+    int qsum = D16 ? 0 : qsumx[tok];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
         int col = g * 128 + s * 32 + h * 16 + tq * 4;
-        ag[s] = *(const int4 *)(gu + (size_t)pair * 2 * MFF + col);
-        au[s] = *(const int4 *)(gu + (size_t)pair * 2 * MFF + MFF + col);
+        size_t o = (size_t)pair * 2 * MFF + col;
+        if (D16) {
+            uint2 a2 = *(const uint2 *)((const int16_t *)gu + o), u2 = *(const uint2 *)((const int16_t *)gu + o + MFF);
+            uint32_t aw[2] = {a2.x, a2.y}, uw2[2] = {u2.x, u2.y};
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                ag[s][b] = (int)(int16_t)(aw[b >> 1] >> (16 * (b & 1)));
+                au[s][b] = (int)(int16_t)(uw2[b >> 1] >> (16 * (b & 1)));
+                if (ag[s][b] == -32768) ag[s][b] = gov[o + b];
+                if (au[s][b] == -32768) au[s][b] = gov[o + MFF + b];
+            }
+        } else {
+            int4 a4 = *(const int4 *)((const int *)gu + o), u4 = *(const int4 *)((const int *)gu + o + MFF);
+            ag[s][0] = a4.x - qsum; ag[s][1] = a4.y - qsum; ag[s][2] = a4.z - qsum; ag[s][3] = a4.w - qsum;
+            au[s][0] = u4.x - qsum; au[s][1] = u4.y - qsum; au[s][2] = u4.z - qsum; au[s][3] = u4.w - qsum;
+        }
         sg[s] = *(const float4 *)(ex.gs + col);
         su[s] = *(const float4 *)(ex.us + col);
     }
-    float qs = qsx[tok]; int qsum = qsumx[tok];
+    float qs = qsx[tok];
     float v[16];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-        int agv[4] = {ag[s].x, ag[s].y, ag[s].z, ag[s].w}, auv[4] = {au[s].x, au[s].y, au[s].z, au[s].w};
         float sgv[4] = {sg[s].x, sg[s].y, sg[s].z, sg[s].w}, suv[4] = {su[s].x, su[s].y, su[s].z, su[s].w};
 #pragma unroll
         for (int b = 0; b < 4; b++) {
-            float gv = (float)(agv[b] - qsum) * qs * sgv[b];
-            float uv = (float)(auv[b] - qsum) * qs * suv[b];
+            float gv = (float)ag[s][b] * qs * sgv[b];
+            float uv = (float)au[s][b] * qs * suv[b];
             float gg = gv < 7.0f ? gv : 7.0f;
             float uu = uv < -7.0f ? -7.0f : (uv > 7.0f ? 7.0f : uv);
             v[s * 4 + b] = gg / (1.0f + dexp(-gg)) * uu;
@@ -1081,9 +1101,11 @@ __device__ __forceinline__ void gu_chunk(v16i (&acc)[2][2], const v4i (&cwc)[2][
 // time. The chunk pipeline runs on across items: while the last three chunks of one item are multiplied, the
 // first three of the next are loaded (codes and activations PD = 3 chunks ahead in 4-slot register rings,
 // activations then through two LDS stages), so no item starts with an empty pipeline.
+template <bool D16>
 __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                       const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
-                                                      const int8_t *__restrict__ qx, int *__restrict__ gu) {
+                                                      const int8_t *__restrict__ qx, const int *__restrict__ qsumx,
+                                                      void *__restrict__ gu, int *__restrict__ gov) {
     constexpr int TN = 64, NT = 256, NF = 2, NA = 2, RB = MFF / 128, NCH = MH / 256, BB = TN * GU_LROW;
     constexpr int NPC = TN * 16 / NT;          // 4 activation pieces of 16 bytes per thread per chunk
     constexpr int PD = 3;                      // prefetch distance of the codes in chunks (ring of 4)
@@ -1169,17 +1191,34 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
                 for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst + k * 16 * GU_LROW]) = br[(ch + 1) % 2][k];
             }
         }
-        // epilogue: int32 gate and up sums of this item; token r32 of each fragment, rows (i/4)*8 + G2*4 + i%4
+        // epilogue: gate and up sums of this item (D16: d = sum - qsum as int16, else the int32 sums); token
+        // r32 of each fragment, rows (i/4)*8 + G2*4 + i%4
 #pragma unroll
         for (int j = 0; j < NF; j++) {
             int tk = j * 32 + r32;
             if (tk < ntok) {
                 int pair = p0 + tk;
+                int qsum = D16 ? qsumx[toks[slot][tk]] : 0;
 #pragma unroll
                 for (int g = 0; g < 4; g++) {
                     int row0 = rowblk + g * 8 + G2 * 4;
-                    *(v4i *)(gu + (size_t)pair * 2 * MFF + row0) = v4i{acc[0][j][g * 4], acc[0][j][g * 4 + 1], acc[0][j][g * 4 + 2], acc[0][j][g * 4 + 3]};
-                    *(v4i *)(gu + (size_t)pair * 2 * MFF + MFF + row0) = v4i{acc[1][j][g * 4], acc[1][j][g * 4 + 1], acc[1][j][g * 4 + 2], acc[1][j][g * 4 + 3]};
+#pragma unroll
+                    for (int f = 0; f < 2; f++) {
+                        size_t o = (size_t)pair * 2 * MFF + f * MFF + row0;
+                        if (D16) {
+                            uint32_t w2[2] = {0, 0};
+#pragma unroll
+                            for (int i = 0; i < 4; i++) {
+                                int d = acc[f][j][g * 4 + i] - qsum;
+                                bool ok = d >= -32767 && d <= 32767;
+                                if (!ok) gov[o + i] = d;
+                                w2[i >> 1] |= (uint32_t)(uint16_t)(ok ? d : -32768) << (16 * (i & 1));
+                            }
+                            *(uint2 *)((int16_t *)gu + o) = make_uint2(w2[0], w2[1]);
+                        } else {
+                            *(v4i *)((int *)gu + o) = v4i{acc[f][j][g * 4], acc[f][j][g * 4 + 1], acc[f][j][g * 4 + 2], acc[f][j][g * 4 + 3]};
+                        }
+                    }
                 }
             }
         }
@@ -1283,12 +1322,14 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
 // padded to DN_LROW bytes); the row blocks then run back to back, the codes of the next row block loaded
 // while the current one is multiplied. Wave w owns rows w*64 .. +64 of each row block (two 32-row
 // fragments) and both 32-pair fragments. grid = tiles x 8 / RPB items (XCD order as xcd_item).
+// Output: D16 = false, D = (float)(sum - qsum) * qs * s_down[row] (fp32); D16 = true, d = sum - qsum as int16
+// (-32768 with d in dov, int32, same index), turned into D by k_combine16 with the same operations.
 #define DN_LROW (MFF + 16)
-template <int RPB>
+template <int RPB, bool D16>
 __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                       const ExpPtr *__restrict__ eptr, const int8_t *__restrict__ qa,
                                                       const float *__restrict__ qsa, const int *__restrict__ qsuma,
-                                                      float *__restrict__ down, int *__restrict__ dbg) {
+                                                      float *__restrict__ down, int *__restrict__ dov, int *__restrict__ dbg) {
     constexpr int TN = 64, NT = 256, NF = 2, NA = 2, NSPLIT = MH / 256 / RPB;
     constexpr int NPC = TN * (MFF / 16) / NT;   // 8 pieces of 16 bytes per thread
     __shared__ __attribute__((aligned(16))) int8_t bs[TN * DN_LROW];
@@ -1368,7 +1409,19 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
                     int ad[4]; float o[4];
 #pragma unroll
                     for (int i = 0; i < 4; i++) { ad[i] = acc[f][j][g * 4 + i]; o[i] = (float)(ad[i] - qsm[j]) * qs[j] * sdv[i]; }
-                    *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
+                    if (D16) {
+                        uint32_t w2[2] = {0, 0};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            int d = ad[i] - qsm[j];
+                            bool ok = d >= -32767 && d <= 32767;
+                            if (!ok) dov[(size_t)pair * MH + row0 + i] = d;
+                            w2[i >> 1] |= (uint32_t)(uint16_t)(ok ? d : -32768) << (16 * (i & 1));
+                        }
+                        *(uint2 *)((int16_t *)down + (size_t)pair * MH + row0) = make_uint2(w2[0], w2[1]);
+                    } else {
+                        *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
+                    }
                     if (dbg) *(int4 *)(dbg + (size_t)pair * MH + row0) = make_int4(ad[0], ad[1], ad[2], ad[3]);
                 }
         }
@@ -1385,6 +1438,61 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
 //   step maple.c:664                  mode 6: y = FMA chain over slots 0..7 from 0, x[b] += y
 // Thread = 4 columns of one token.
 // =====================================================================================================
+// Combine from int16 down results (k_down_tile<., true>): block = one token, 256 threads x 8 columns. The
+// token's 8 pairs (tp/sp order as k_combine), their weights, qs and down-scale rows are looked up once into
+// LDS; then D = (float)d * qs * s_down[row] (k_down_tile's operations) and the same FMA chain as k_combine.
+__global__ void __launch_bounds__(256) k_combine16(const int16_t *__restrict__ down, const float *__restrict__ uw,
+                                                   const int *__restrict__ tp, const int *__restrict__ sp,
+                                                   const float *__restrict__ tw, int nb, float *__restrict__ x, int mode,
+                                                   const int *__restrict__ pu, const ExpPtr *__restrict__ eptr,
+                                                   const float *__restrict__ qsa, const int *__restrict__ dov) {
+    __shared__ int sa[MTOPK];
+    __shared__ float sw[MTOPK], sq[MTOPK];
+    __shared__ const float *sds[MTOPK];
+    int b = blockIdx.x, t = threadIdx.x, c = t * 8;
+    if (t < MTOPK) {
+        int a = (mode & 2) ? sp[b * MTOPK + t] : tp[b * MTOPK + t];
+        sa[t] = a; sw[t] = (mode & 2) ? tw[b * MTOPK + t] : uw[a];
+        sq[t] = qsa[a]; sds[t] = eptr[pu[a]].ds;
+    }
+    float *xp = x + (size_t)b * MH + c;
+    float acc[8];
+    if (mode & 1) {
+        float4 x0 = *(const float4 *)xp, x1 = *(const float4 *)(xp + 4);
+        acc[0] = x0.x; acc[1] = x0.y; acc[2] = x0.z; acc[3] = x0.w; acc[4] = x1.x; acc[5] = x1.y; acc[6] = x1.z; acc[7] = x1.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i] = 0.0f;
+    }
+    __syncthreads();
+    uint4 dv[MTOPK];
+#pragma unroll
+    for (int j = 0; j < MTOPK; j++) dv[j] = *(const uint4 *)(down + (size_t)sa[j] * MH + c);
+#pragma unroll
+    for (int j = 0; j < MTOPK; j++) {
+        const float *ds = sds[j] + c;
+        float4 s0 = *(const float4 *)ds, s1 = *(const float4 *)(ds + 4);
+        float sdv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+        uint32_t wd[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
+        float qs = sq[j], wgt = sw[j];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            int d = (int16_t)(wd[i >> 1] >> (16 * (i & 1)));
+            if (d == -32768) d = dov[(size_t)sa[j] * MH + c + i];
+            float D = (float)d * qs * sdv[i];
+            acc[i] = __builtin_fmaf(wgt, D, acc[i]);
+        }
+    }
+    if (mode & 4) {
+        float4 x0 = *(const float4 *)xp, x1 = *(const float4 *)(xp + 4);
+        float xv[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[i] = xv[i] + acc[i];
+    }
+    *(float4 *)xp = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    *(float4 *)(xp + 4) = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
 __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ down, const float *__restrict__ uw,
                                                  const int *__restrict__ tp, const int *__restrict__ sp,
                                                  const float *__restrict__ tw, int nb, float *__restrict__ x, int mode) {

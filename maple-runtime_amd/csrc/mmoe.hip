@@ -52,7 +52,11 @@ struct Work {
     float *qsx = nullptr, *qsa = nullptr, *act = nullptr, *down = nullptr;
     int *qsumx = nullptr, *qsuma = nullptr;
     int *dbg_gu = nullptr, *dbg_dn = nullptr;
-    int *gu = nullptr;              // gate/up int32 sums [P][1024] of the 64-token-tile path
+    int *gu = nullptr;              // gate/up sums [P][1024] of the 64-token-tile path (int16 d, or int32 sums with checks on)
+    int *gov = nullptr;             // int32 d of the entries whose int16 slot holds -32768
+    int *dov = nullptr;             // the same for the int16 down results
+    int *eu = nullptr, *pu = nullptr;   // expert -> used-expert index [256], pair -> used-expert index [P]
+    bool compact = false;           // the last expert stage left down as int16 (k_combine16)
     uint16_t *hs = nullptr;         // MoE input split into 2 bf16 parts [2][T][2048] (approximate router)
     float *rpart = nullptr;         // partial router logits [4][T][256]
     float *hmax = nullptr;          // max |hn| per token
@@ -76,7 +80,8 @@ static int work_alloc(Work &w, int maxtok) {
     HC(hipMalloc(&w.qx, T * MH)); HC(hipMalloc(&w.qsx, T * 4)); HC(hipMalloc(&w.qsumx, T * 4));
     HC(hipMalloc(&w.act, P * MFF * 4)); HC(hipMalloc(&w.qa, P * MFF)); HC(hipMalloc(&w.qsa, P * 4)); HC(hipMalloc(&w.qsuma, P * 4));
     HC(hipMalloc(&w.down, P * MH * 4));
-    HC(hipMalloc(&w.gu, P * 2 * MFF * 4));
+    HC(hipMalloc(&w.gu, P * 2 * MFF * 4)); HC(hipMalloc(&w.gov, P * 2 * MFF * 4)); HC(hipMalloc(&w.dov, P * MH * 4));
+    HC(hipMalloc(&w.eu, MNE * 4)); HC(hipMalloc(&w.pu, P * 4));
     HC(hipMalloc(&w.hs, 2 * T * MH * 2)); HC(hipMalloc(&w.hmax, T * 4)); HC(hipMalloc(&w.rpart, 4 * T * MNE * 4));
     HC(hipMalloc(&w.cand, T * RG_MAXC * 4)); HC(hipMalloc(&w.ncand, T * 4));
     HC(hipMalloc(&w.counters, (64 + MNE) * sizeof(unsigned)));
@@ -188,8 +193,8 @@ static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) 
     }
     if (launch(MMOE_K_TOPK, [&] { k_topk_quant<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
     return launch(MMOE_K_GROUP, [&] {
-        k_plan_top<<<1, 256, 0, S.st>>>(w.hist, nb, w.base, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles);
-        k_scatter<<<nch, 512, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp);
+        k_plan_top<<<1, 256, 0, S.st>>>(w.hist, nb, w.base, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles, w.eu);
+        k_scatter<<<nch, 512, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp, w.eu, w.pu);
     });
 }
 
@@ -198,43 +203,49 @@ static int stage_quant_x(Work &w, const float *d_hn, int nb) {
 }
 
 // gate/up (+SiLU), act quantisation, down for np pairs under w.plan / w.eptr / w.utok
-static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int dec; float *x; } LAST;
+static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int dec; float *x; bool compact; } LAST;
 
 static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8); }  // xcd_item needs a multiple of 8
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
     if (tn == 64) {   // int32 sums into gu (the debug buffer when checks are on: it has the same layout)
-        float *gu = (float *)(dg ? dg : w.gu);
-        int *gi = (int *)gu;
-        int nblk = (int)grid8(S.ncu < maxtiles * (MFF / 128) ? S.ncu : maxtiles * (MFF / 128));   // one persistent block per CU
-        return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, gi); });
+        int nblk = (int)grid8(S.ncu * 2 < maxtiles * (MFF / 128) ? S.ncu * 2 : maxtiles * (MFF / 128));   // two persistent blocks per CU
+        if (dg) return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<false><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsumx, dg, nullptr); });
+        return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<true><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsumx, w.gu, w.gov); });
     }
     return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<grid8(maxtiles * (MFF / 16)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
-static int launch_down(Work &w, int maxtiles, int tn, int *dd) {
-    if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
+static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
+    if (tn == 64 && compact) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB, true><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
+    if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB, false><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, nullptr, dd); });
     return launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<grid8(maxtiles * (MH / 64)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
 }
 
 static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
     if (tn == 64) {
-        const int *gu = dg ? dg : w.gu;
         float *act = S.debug ? w.act : nullptr;
-        return launch(MMOE_K_QUANT_ACT, [&] { k_act_quant<<<maxtiles * 8, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, gu, act, w.qa, w.qsa, w.qsuma); });
+        if (dg) return launch(MMOE_K_QUANT_ACT, [&] { k_act_quant<false><<<maxtiles * 8, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, dg, nullptr, act, w.qa, w.qsa, w.qsuma); });
+        return launch(MMOE_K_QUANT_ACT, [&] { k_act_quant<true><<<maxtiles * 8, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, w.gu, w.gov, act, w.qa, w.qsa, w.qsuma); });
     }
     return launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(np + 3) / 4, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); });
 }
-static int stage_experts(Work &w, int np, int nu_max, int tn) {
+// device_grouping: the grouping came from k_plan_top/k_scatter (pu is valid), so the 64-token-tile path may
+// hand the down results to k_combine as int16 (not with checks on: the tests read them as fp32)
+static int stage_experts(Work &w, int np, int nu_max, int tn, bool device_grouping) {
     LAST.w = &w; LAST.np = np; LAST.nu_max = nu_max; LAST.tn = tn; LAST.dec = 0;
     int maxtiles = np / tn + (nu_max < np ? nu_max : np);
     int *dg = S.debug ? w.dbg_gu : nullptr, *dd = S.debug ? w.dbg_dn : nullptr;
+    w.compact = device_grouping && tn == 64 && !S.debug;
+    LAST.compact = w.compact;
     if (launch_gateup(w, maxtiles, tn, dg)) return -1;
     if (launch_quant_act(w, maxtiles, tn, np, dg)) return -1;
-    if (launch_down(w, maxtiles, tn, dd)) return -1;
+    if (launch_down(w, maxtiles, tn, dd, w.compact)) return -1;
     return 0;
 }
 
 static int stage_combine(Work &w, int nb, float *d_x, int mode) {
     int n = nb * (MH / 4);
+    if (w.compact)
+        return launch(MMOE_K_COMBINE, [&] { k_combine16<<<nb, 256, 0, S.st>>>((const int16_t *)w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode, w.pu, w.eptr, w.qsa, w.dov); });
     return launch(MMOE_K_COMBINE, [&] { k_combine<<<(n + 255) / 256, 256, 0, S.st>>>(w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode); });
 }
 
@@ -276,7 +287,7 @@ static int moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) {
     LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = d_hn; LAST.dec = 0;
     if (stage_router(w, L, d_hn, nb, order)) return -1;
     if (stage_route_group(w, L, nb, tn, d_hn)) return -1;
-    if (stage_experts(w, np, MNE, tn)) return -1;
+    if (stage_experts(w, np, MNE, tn, true)) return -1;
     return stage_combine(w, nb, d_x, order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH);
 }
 
@@ -298,7 +309,7 @@ static int experts_host_grouping(Work &w, int nb, int nu, const ExpPtr *eptr_h, 
     if (tp) HC(hipMemcpyAsync(w.tp, tp, sizeof(int) * nb * MTOPK, hipMemcpyHostToDevice, S.st));
     if (launch(MMOE_K_GROUP, [&] { k_plan_from_ustart<<<1, 64, 0, S.st>>>(w.ustart, nu, w.plan, tn, w.tiles); })) return -1;
     if (stage_quant_x(w, w.hn, nb)) return -1;
-    return stage_experts(w, np, nu, tn);
+    return stage_experts(w, np, nu, tn, false);
 }
 
 // loc (maple.c:276-277: per used expert 6 x (region slot, byte offset)) + regs -> device pointers
@@ -692,7 +703,7 @@ double mmoe_bench_stage(int kid, int reps) {
         }
         switch (kid) {
             case MMOE_K_GATEUP: rc = launch_gateup(w, maxtiles, LAST.tn, nullptr); break;
-            case MMOE_K_DOWN: rc = launch_down(w, maxtiles, LAST.tn, nullptr); break;
+            case MMOE_K_DOWN: rc = launch_down(w, maxtiles, LAST.tn, nullptr, LAST.compact); break;
             case MMOE_K_QUANT_ACT: rc = launch_quant_act(w, maxtiles, LAST.tn, LAST.np, nullptr); break;
             case MMOE_K_ROUTER: rc = LAST.hn ? stage_router(w, LAST.L, LAST.hn, LAST.nb, LAST.order) : -1; break;
             default: seterr("mmoe_bench_stage: kernel %d not repeatable", kid); return -1.0;

@@ -215,3 +215,24 @@ def test_moe_batch_mfma_router(layer0):
         compare_layer(layer0, 200, M.ORDER_BATCH, " mfma router", refined=True)
     finally:
         M.check(lib.mmoe_set_router_mode(1), "router mode")
+
+
+def test_moe_batch_tn64_compact_sums(layer0):
+    """With checks off the 64-token-tile path hands gate/up sums to k_act_quant and down results to k_combine as
+    int16 (d = sum - qsum, int32 side buffer for the rare out-of-range entry): act int8 and x must still match."""
+    lib = M.lib()
+    M.check(lib.mmoe_set_debug(0), "debug off")
+    try:
+        nb = 256
+        x, hn = normed_hidden(SEED, 77, nb)
+        xg = run_gpu(layer0.L, hn, x, M.ORDER_BATCH)
+        xo = x.copy()
+        o = O.moe_batch(hn, layer0.router, layer0.table, xo)
+        P = nb * 8
+        qa = M.mfma_to_natural(M.read("QA", (P, 512), np.int8), 512)
+        assert np.array_equal(qa, o["qa"]), "act int8 differs"
+        assert np.array_equal(M.read("QSUMA", (P,), np.int32), o["qsuma"])
+        assert relmax(xg - x, xo - x) <= TOL   # down results travel as int16 to the combine here
+        print("\n  compact sums: x bit-exact", np.array_equal(xg, xo))
+    finally:
+        M.check(lib.mmoe_set_debug(1), "debug on")
