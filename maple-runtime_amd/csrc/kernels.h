@@ -202,56 +202,60 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
 }
 
 // Large batches (batch order, NCH = 8) as a register-tiled GEMM that keeps maple.c's chains: one thread
-// owns one chain j for an 8-token x 8-expert tile (64 independent FMA chains in registers), a block
-// covers 32 tokens x 64 experts x 8 chains. Operands sit in LDS chain-major, hs[j][m][token] and
+// owns one chain j for a TPT-token x 8-expert tile (independent FMA chains in registers), a block
+// covers 4 TPT tokens x 64 experts x 8 chains. Operands sit in LDS chain-major, hs[j][m][token] and
 // ws[j][m][expert] for column j + 8m, so a chain step reads 2 + 2 16-byte words. The router comes
 // pre-converted to fp32 in that order, wT[j][m][e] = w[e][j + 8m] (k_router_chain8_f32). Columns advance
 // in chunks of RG_MC steps, the next chunk loaded into registers while the current one is used.
 // After the last column the 8 chain values meet in LDS and are folded by hsum8.
-#define RG_BT 32
 #define RG_BE 64
 #define RG_MC 16
-#define RG_HP 36   // token stride of hs (32 + 4 padding, keeps 16-byte alignment)
 __global__ void k_router_chain8_f32(const uint16_t *__restrict__ w, float *__restrict__ wT) {
     int i = blockIdx.x * 256 + threadIdx.x;          // over wT: [8][256][256]
     int j = i >> 16, m = (i >> 8) & 255, e = i & 255;
     wT[i] = bf16f(w[(size_t)e * MH + j + 8 * m]);
 }
+// TPT tokens per thread: the block covers BT = 4 TPT tokens (TPT = 4: 16 tokens, 512 blocks at T = 2048 and
+// 32 accumulators per thread, so two or more waves share a SIMD).
+template <int TPT>
 __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ hn, int nb, const float *__restrict__ wT,
                                                      const float *__restrict__ bias, float *__restrict__ rl) {
-    __shared__ __attribute__((aligned(16))) float smem[8 * RG_BT * RG_BE];   // 64 KB: chunk buffers, then the chain fold
-    float *hs = smem, *ws = smem + 8 * RG_MC * RG_HP;
+    constexpr int BT = 4 * TPT, HP = BT + 4;        // tokens per block; token stride of hs (padded, 16-byte aligned)
+    constexpr int NH = BT * 128 / 4 / 256;           // float4 pieces of the token chunk per thread
+    constexpr int SM_CHUNK = 8 * RG_MC * HP + 8 * RG_MC * RG_BE, SM_RED = 8 * BT * RG_BE;
+    __shared__ __attribute__((aligned(16))) float smem[SM_CHUNK > SM_RED ? SM_CHUNK : SM_RED];
+    float *hs = smem, *ws = smem + 8 * RG_MC * HP;
     int t = threadIdx.x, j = t >> 5, tg = (t >> 3) & 3, eg = t & 7;
-    int b0 = blockIdx.x * RG_BT, e0 = blockIdx.y * RG_BE;
+    int b0 = blockIdx.x * BT, e0 = blockIdx.y * RG_BE;
     typedef float f4v __attribute__((ext_vector_type(4)));
-    f4v hr[4], wr[8];
-    float acc[8][8];
+    f4v hr[NH], wr[8];
+    float acc[TPT][8];
 #pragma unroll
-    for (int a = 0; a < 8; a++)
+    for (int a = 0; a < TPT; a++)
 #pragma unroll
         for (int b = 0; b < 8; b++) acc[a][b] = 0.0f;
-    {
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        int idx = t + 256 * k, b = idx >> 5, c4 = idx & 31;
-        hr[k] = *(const f4v *)(hn + (size_t)min(b0 + b, nb - 1) * MH + 0 + 4 * c4);
+#define RG_LOAD(cn)                                                                                             \
+    {                                                                                                           \
+        _Pragma("unroll") for (int k = 0; k < NH; k++) {                                                        \
+            int idx = t + 256 * k, b = idx >> 5, c4 = idx & 31;                                                 \
+            hr[k] = *(const f4v *)(hn + (size_t)min(b0 + b, nb - 1) * MH + (cn) + 4 * c4);                      \
+        }                                                                                                       \
+        _Pragma("unroll") for (int k = 0; k < 8; k++) {                                                         \
+            int idx = t + 256 * k, jj = idx >> 8, mm = (idx >> 4) & 15, e4 = idx & 15;                          \
+            wr[k] = *(const f4v *)(wT + ((size_t)jj * 256 + (cn) / 8 + mm) * 256 + e0 + 4 * e4);                 \
+        }                                                                                                       \
     }
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-        int idx = t + 256 * k, jj = idx >> 8, mm = (idx >> 4) & 15, e4 = idx & 15;
-        wr[k] = *(const f4v *)(wT + ((size_t)jj * 256 + 0 / 8 + mm) * 256 + e0 + 4 * e4);
-    }
-    }
+    RG_LOAD(0);
     for (int c0 = 0; c0 < MH; c0 += 8 * RG_MC) {
         __syncthreads();                             // the previous chunk is no longer read
 #pragma unroll
-        for (int k = 0; k < 4; k++) {
+        for (int k = 0; k < NH; k++) {
             int idx = t + 256 * k, b = idx >> 5, c4 = idx & 31;
-            int c = 4 * c4, base = (c >> 3) * RG_HP + b, j0 = c & 7;
-            hs[((j0 + 0) * RG_MC) * RG_HP + base] = hr[k].x;
-            hs[((j0 + 1) * RG_MC) * RG_HP + base] = hr[k].y;
-            hs[((j0 + 2) * RG_MC) * RG_HP + base] = hr[k].z;
-            hs[((j0 + 3) * RG_MC) * RG_HP + base] = hr[k].w;
+            int c = 4 * c4, base = (c >> 3) * HP + b, j0 = c & 7;
+            hs[((j0 + 0) * RG_MC) * HP + base] = hr[k].x;
+            hs[((j0 + 1) * RG_MC) * HP + base] = hr[k].y;
+            hs[((j0 + 2) * RG_MC) * HP + base] = hr[k].z;
+            hs[((j0 + 3) * RG_MC) * HP + base] = hr[k].w;
         }
 #pragma unroll
         for (int k = 0; k < 8; k++) {
@@ -259,46 +263,36 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ h
             *(f4v *)(ws + (jj * RG_MC + mm) * RG_BE + 4 * e4) = wr[k];
         }
         __syncthreads();
-        if (c0 + 8 * RG_MC < MH) {
-            int cn = c0 + 8 * RG_MC;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                int idx = t + 256 * k, b = idx >> 5, c4 = idx & 31;
-                hr[k] = *(const f4v *)(hn + (size_t)min(b0 + b, nb - 1) * MH + cn + 4 * c4);
-            }
-    #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                int idx = t + 256 * k, jj = idx >> 8, mm = (idx >> 4) & 15, e4 = idx & 15;
-                wr[k] = *(const f4v *)(wT + ((size_t)jj * 256 + cn / 8 + mm) * 256 + e0 + 4 * e4);
-            }
-        }
+        if (c0 + 8 * RG_MC < MH) RG_LOAD(c0 + 8 * RG_MC);
 #pragma unroll 4
         for (int m = 0; m < RG_MC; m++) {
-            const float *hp = hs + (j * RG_MC + m) * RG_HP + tg * 8, *wp = ws + (j * RG_MC + m) * RG_BE + eg * 8;
-            float4 h0 = *(const float4 *)hp, h1 = *(const float4 *)(hp + 4);
+            const float *hp = hs + (j * RG_MC + m) * HP + tg * TPT, *wp = ws + (j * RG_MC + m) * RG_BE + eg * 8;
+            float hv[TPT];
+#pragma unroll
+            for (int a = 0; a < TPT; a += 4) { float4 h = *(const float4 *)(hp + a); hv[a] = h.x; hv[a + 1] = h.y; hv[a + 2] = h.z; hv[a + 3] = h.w; }
             float4 w0 = *(const float4 *)wp, w1 = *(const float4 *)(wp + 4);
-            float hv[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
             float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
-            for (int a = 0; a < 8; a++)
+            for (int a = 0; a < TPT; a++)
 #pragma unroll
                 for (int b = 0; b < 8; b++) acc[a][b] = __builtin_fmaf(wv[b], hv[a], acc[a][b]);
         }
     }
+#undef RG_LOAD
     __syncthreads();
     float *red = smem;                               // red[j][token][expert]
 #pragma unroll
-    for (int a = 0; a < 8; a++)
+    for (int a = 0; a < TPT; a++)
 #pragma unroll
         for (int b = 0; b < 8; b += 4)
-            *(float4 *)(red + (j * RG_BT + tg * 8 + a) * RG_BE + eg * 8 + b) = make_float4(acc[a][b], acc[a][b + 1], acc[a][b + 2], acc[a][b + 3]);
+            *(float4 *)(red + (j * BT + tg * TPT + a) * RG_BE + eg * 8 + b) = make_float4(acc[a][b], acc[a][b + 1], acc[a][b + 2], acc[a][b + 3]);
     __syncthreads();
 #pragma unroll
-    for (int q = 0; q < 8; q++) {
+    for (int q = 0; q < BT * RG_BE / 256; q++) {
         int o = q * 256 + t, tok = o >> 6, e = o & 63;
         float v[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; jj++) v[jj] = red[(jj * RG_BT + tok) * RG_BE + e];
+        for (int jj = 0; jj < 8; jj++) v[jj] = red[(jj * BT + tok) * RG_BE + e];
         float r = hsum8(v);
         if (bias) r = r + bias[e0 + e];
         if (b0 + tok < nb) rl[(size_t)(b0 + tok) * MNE + e0 + e] = r;

@@ -172,7 +172,7 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
     if (nb < 512)   // one block per (token, 32 experts): 8 nb blocks, router reread from L2 per token
         return launch(MMOE_K_ROUTER, [&] { k_router_chains<8><<<dim3(MNE * 8 / 256, nb), 256, 0, S.st>>>(d_hn, nb, lw.rc8, lw.bias, w.rl); });
     if (S_router_exact)
-        return launch(MMOE_K_ROUTER, [&] { k_router_gemm<<<dim3((nb + RG_BT - 1) / RG_BT, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
+        return launch(MMOE_K_ROUTER, [&] { k_router_gemm<4><<<dim3((nb + 15) / 16, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
     // approximate logits on the bf16 MFMA; k_cand + k_chain make the top-8 exact
     w.refine = true;
     return launch(MMOE_K_ROUTER, [&] {

@@ -95,6 +95,11 @@ def test_moe_batch(layer0, nb):
     compare_layer(layer0, nb, M.ORDER_BATCH)
 
 
+def test_moe_batch_gemm_router(layer0):
+    # >= 512 tokens: the exact tiled fp32 router (k_router_gemm); 520 leaves a ragged last token tile
+    compare_layer(layer0, 520, M.ORDER_BATCH)
+
+
 def test_moe_batch_tn64(layer0):
     # 256 tokens -> 2048 pairs: the 64-token tile kernels
     compare_layer(layer0, 256, M.ORDER_BATCH)
