@@ -181,6 +181,10 @@ int mmoe_prof(int on);
 int mmoe_prof_reset(void);
 int mmoe_prof_get(int kid, double *ms_total, long *count);
 int mmoe_device_info(char *name, int len, int *cus, int *clock_khz);
+/* Diagnostic, no counterpart in the reference: checks the branch-light SiLU of the activation kernel
+ * against g / (1 + exp(-g)) with IEEE division, bit for bit, over the fp32 bit patterns [lo, lo + n).
+ * *nbad = number of mismatches, *first = smallest mismatching pattern (0xffffffff if none). */
+int mmoe_selftest_silu(uint32_t lo, uint32_t n, unsigned long long *nbad, uint32_t *first);
 
 /* Synthetic Maple-shaped data in the reference layout (see csrc/synth.c) */
 void mmoe_synth_expert(uint64_t seed, int L, int e, uint8_t *gc, float *gs, uint8_t *uc, float *us, uint8_t *dc, float *ds);

@@ -66,8 +66,48 @@ __device__ __forceinline__ float dexp(float x) {
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    int ki = (int)k, k1 = ki / 2, k2 = ki - k1;
-    return p * pow2i(k1) * pow2i(k2);
+    // p 2^k, k in [-150, 128]. The oracle forms it as (p 2^(k/2)) 2^(k - k/2); the first product is exact,
+    // so both round once, identically.
+    return __builtin_amdgcn_ldexpf(p, (int)k);
+}
+
+// SiLU of a gate value g <= 7: g / (1 + dexp(-g)), bit-identical to that expression with IEEE division
+// (mmoe_selftest_silu checks every finite g <= 7). For -g <= 80 the quotient is a refined reciprocal
+// y = rcp(d) + one Newton step, q = g y, then one residual correction q += (g - d q) y (Markstein's
+// scheme); d = 1 + e lies in [1, 2^116] there, so y stays a normal number. -g > 80 (rare) takes the IEEE
+// division, with dexp's overflow to +inf (g / inf = -0).
+__device__ __forceinline__ float silu_le7(float g) {
+    float x = fminf(-g, 88.8f);
+    float k = __builtin_rintf(x * 1.44269504f);
+    float r = __builtin_fmaf(-k, 0.693145752f, x);
+    r = __builtin_fmaf(-k, 1.42860677e-06f, r);
+    float p = 1.98412698e-04f;
+    p = __builtin_fmaf(p, r, 1.38888889e-03f);
+    p = __builtin_fmaf(p, r, 8.33333333e-03f);
+    p = __builtin_fmaf(p, r, 4.16666667e-02f);
+    p = __builtin_fmaf(p, r, 1.66666667e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    float e = __builtin_amdgcn_ldexpf(p, (int)k);   // = p 2^k1 2^k2 of dexp (one rounding either way)
+    float d = 1.0f + e;
+    if (__builtin_expect(-g > 80.0f, 0)) return g / (-g > 88.8f ? __int_as_float(0x7f800000) : d);
+    float y = __builtin_amdgcn_rcpf(d);
+    y = __builtin_fmaf(__builtin_fmaf(-d, y, 1.0f), y, y);
+    float q = g * y;
+    // the correction turns g = -0 into +0; d > 0, so the quotient carries the sign of g
+    return __builtin_copysignf(__builtin_fmaf(__builtin_fmaf(-d, q, g), y, q), g);
+}
+
+// Exhaustive check of silu_le7 against g / (1 + dexp(-g)): thread i tests bit patterns lo + i + n * stride.
+__global__ void k_selftest_silu(uint32_t lo, uint32_t n, unsigned long long *nbad, uint32_t *first) {
+    unsigned long long bad = 0;
+    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
+        float g = __uint_as_float(lo + i);
+        float a = silu_le7(g), b = g / (1.0f + dexp(-g));
+        if (__float_as_uint(a) != __float_as_uint(b)) { bad++; atomicMin(first, lo + i); }
+    }
+    if (bad) atomicAdd(nbad, bad);
 }
 
 // ---- wave64 reductions (order-free operations only: max, integer sum). DPP inside each 16-lane row
@@ -850,8 +890,6 @@ __global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan
             for (int b = 0; b < 4; b++) {
                 ag[s][b] = (int)(int16_t)(aw[b >> 1] >> (16 * (b & 1)));
                 au[s][b] = (int)(int16_t)(uw2[b >> 1] >> (16 * (b & 1)));
-                if (ag[s][b] == -32768) ag[s][b] = gov[o + b];
-                if (au[s][b] == -32768) au[s][b] = gov[o + MFF + b];
             }
         } else {
             int4 a4 = *(const int4 *)((const int *)gu + o), u4 = *(const int4 *)((const int *)gu + o + MFF);
@@ -860,6 +898,24 @@ __global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan
         }
         sg[s] = *(const float4 *)(ex.gs + col);
         su[s] = *(const float4 *)(ex.us + col);
+    }
+    if (D16) {                                       // out-of-range sums (rare): one branch for all 32
+        bool side = false;
+#pragma unroll
+        for (int s = 0; s < 4; s++)
+#pragma unroll
+            for (int b = 0; b < 4; b++) side |= (ag[s][b] == -32768) | (au[s][b] == -32768);
+        if (side) {
+#pragma unroll
+            for (int s = 0; s < 4; s++) {
+                size_t o = (size_t)pair * 2 * MFF + g * 128 + s * 32 + h * 16 + tq * 4;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    if (ag[s][b] == -32768) ag[s][b] = gov[o + b];
+                    if (au[s][b] == -32768) au[s][b] = gov[o + MFF + b];
+                }
+            }
+        }
     }
     float qs = qsx[tok];
     float v[16];
@@ -871,8 +927,8 @@ __global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan
             float gv = (float)ag[s][b] * qs * sgv[b];
             float uv = (float)au[s][b] * qs * suv[b];
             float gg = gv < 7.0f ? gv : 7.0f;
-            float uu = uv < -7.0f ? -7.0f : (uv > 7.0f ? 7.0f : uv);
-            v[s * 4 + b] = gg / (1.0f + dexp(-gg)) * uu;
+            float uu = __builtin_amdgcn_fmed3f(uv, -7.0f, 7.0f);   // finite uv: the clamp of maple.c
+            v[s * 4 + b] = silu_le7(gg) * uu;
         }
         if (act && live)
             *(float4 *)(act + (size_t)pair * MFF + g * 128 + s * 32 + h * 16 + tq * 4) = make_float4(v[s * 4], v[s * 4 + 1], v[s * 4 + 2], v[s * 4 + 3]);

@@ -715,6 +715,26 @@ double mmoe_bench_stage(int kid, int reps) {
     return ms / reps;
 }
 
+// Exhaustive check of the SiLU used by k_act_quant against its IEEE-division form over the bit patterns
+// [lo, lo + n). Blocks until done; *nbad = mismatches, *first = smallest mismatching pattern (0xffffffff
+// if none).
+int mmoe_selftest_silu(uint32_t lo, uint32_t n, unsigned long long *nbad, uint32_t *first) {
+    if (ctx_ready()) return -1;
+    struct R { unsigned long long bad; uint32_t first; } h = {0, 0xffffffffu};
+    R *d = nullptr;
+    HC(hipMalloc(&d, sizeof(R)));
+    int rc = -1;
+    if (hipMemcpy(d, &h, sizeof h, hipMemcpyHostToDevice) == hipSuccess) {
+        k_selftest_silu<<<S.ncu * 16, 256, 0, S.st>>>(lo, n, &d->bad, &d->first);
+        if (hipGetLastError() == hipSuccess && hipStreamSynchronize(S.st) == hipSuccess &&
+            hipMemcpy(&h, d, sizeof h, hipMemcpyDeviceToHost) == hipSuccess) rc = 0;
+    }
+    (void)hipFree(d);
+    if (rc) { seterr("mmoe_selftest_silu: HIP error"); return -1; }
+    *nbad = h.bad; *first = h.first;
+    return 0;
+}
+
 int mmoe_prof(int on) { S.prof = on != 0; return 0; }
 int mmoe_prof_reset(void) { memset(S.prof_ms, 0, sizeof S.prof_ms); memset(S.prof_n, 0, sizeof S.prof_n); return 0; }
 int mmoe_prof_get(int kid, double *ms_total, long *count) {

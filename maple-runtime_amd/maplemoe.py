@@ -64,6 +64,7 @@ def _declare(L):
         "mmoe_event_record": (i, [i]), "mmoe_bench_stage": (d, [i, i]), "mmoe_event_elapsed_ms": (d, []), "mmoe_prof": (i, [i]),
         "mmoe_prof_reset": (i, []), "mmoe_prof_get": (i, [i, C.POINTER(C.c_double), C.POINTER(C.c_long)]),
         "mmoe_device_info": (i, [C.c_char_p, i, ip, ip]),
+        "mmoe_selftest_silu": (i, [C.c_uint32, C.c_uint32, C.POINTER(C.c_ulonglong), u32p]),
         "mmoe_synth_expert": (None, [u64, i, i, vp, vp, vp, vp, vp, vp]), "mmoe_synth_expert_bytes": (sz, []),
         "mmoe_synth_layer": (None, [u64, i, vp, i]), "mmoe_synth_router": (None, [u64, i, i, vp]),
         "mmoe_synth_hidden": (None, [u64, i, i, vp]), "mmoe_synth_zipf_bias": (None, [u64, d, vp]),

@@ -3,6 +3,7 @@
 Bar: bit-exact for router logits order, top-8 indices, grouping, int8 quantisation and every int32 code*q
 sum; fp32 results within 1e-5 max-normalised (they are in fact compared bit for bit where the operation
 sequence is shared, and the test reports it)."""
+import ctypes as C
 import numpy as np
 import pytest
 
@@ -93,6 +94,17 @@ def compare_layer(hl, nb, order, bias_note="", refined=False):
 @pytest.mark.parametrize("nb", [1, 3, 32, 64, 100, 128])   # 128: config 0 chunk
 def test_moe_batch(layer0, nb):
     compare_layer(layer0, nb, M.ORDER_BATCH)
+
+
+def test_silu_exhaustive():
+    """The activation kernel's SiLU (refined reciprocal instead of IEEE division, ldexp instead of two power-of-two
+    products) equals g / (1 + exp(-g)) with IEEE division for every finite fp32 g <= 7 (the gate clamp)."""
+    lib = M.lib()
+    M.check(lib.mmoe_init(8), "init")
+    for lo, hi in [(0x00000000, 0x40E00000), (0x80000000, 0xFF7FFFFF)]:   # +0 .. 7, -0 .. -FLT_MAX
+        nbad, first = C.c_ulonglong(), C.c_uint32()
+        M.check(lib.mmoe_selftest_silu(lo, hi - lo + 1, C.byref(nbad), C.byref(first)), "selftest")
+        assert nbad.value == 0, f"{nbad.value} mismatches in [{lo:#x}, {hi:#x}], first {first.value:#x}"
 
 
 def test_moe_batch_gemm_router(layer0):
