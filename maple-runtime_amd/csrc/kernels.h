@@ -854,18 +854,33 @@ __device__ __forceinline__ void quant_half(const float *v, int l, int8_t *q, flo
     if (store && (l & 31) == 0) { *qs = qsv; *qsum = l < 32 ? s0 : s1; }
 }
 
-// SiLU(min(g,7)) * clamp(u,-7,7) from the gate/up sums, then the int8 quantisation of act (maple.c:825-832).
-// gu[pair][0..511] gate, [512..1023] up, as written by k_gateup_pk: D16 = false, int32 sums of code * q, and
-// d = sum - qsum here; D16 = true, d itself as int16, or -32768 with d in gov (int32, same index).
-// G = (float)d * qs * s_gate[row], likewise U. grid = tiles x 8 blocks of 8 pairs; a wave takes 2 pairs
-// (half-wave each). act (fp32, for checks) is written only when act != NULL.
-template <bool D16>
+// int8 quantisation of np activation vectors of 512 (maple.c:830-832), two per wave (quant_half), output
+// in mfma order. grid = ceil(np / 8) blocks of 256.
+__global__ void __launch_bounds__(256) k_quant_act(const float *__restrict__ act, int np, int8_t *__restrict__ qa,
+                                                   float *__restrict__ qsa, int *__restrict__ qsuma) {
+    int t = threadIdx.x, l = t & 63;
+    int pair = blockIdx.x * 8 + (t >> 6) * 2 + (l >> 5);
+    bool live = pair < np;
+    const float *ar = act + (size_t)(live ? pair : 0) * MFF;
+    int o = l & 31, g = o >> 3, h = (o >> 2) & 1, tq = o & 3;
+    float v[16];
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+        float4 f = *(const float4 *)(ar + g * 128 + s * 32 + h * 16 + tq * 4);
+        v[s * 4] = f.x; v[s * 4 + 1] = f.y; v[s * 4 + 2] = f.z; v[s * 4 + 3] = f.w;
+    }
+    quant_half<128>(v, l, qa + (size_t)pair * MFF, qsa + pair, qsuma + pair, live);
+}
+
+// SiLU(min(g,7)) * clamp(u,-7,7) from the int32 gate/up sums, then the int8 quantisation of act
+// (maple.c:825-832); the path with checks on (the sums stay readable). gu[pair][0..511] gate, [512..1023] up,
+// as written by k_gateup_pk<false>; G = (float)(sum - qsum) * qs * s_gate[row], likewise U. grid = tiles x 8
+// blocks of 8 pairs; a wave takes 2 pairs (half-wave each). act (fp32) is written when act != NULL.
 __global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                    const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
                                                    const float *__restrict__ qsx, const int *__restrict__ qsumx,
-                                                   const void *__restrict__ gu, const int *__restrict__ gov,
-                                                   float *__restrict__ act, int8_t *__restrict__ qa,
-                                                   float *__restrict__ qsa, int *__restrict__ qsuma) {
+                                                   const int *__restrict__ gu, float *__restrict__ act,
+                                                   int8_t *__restrict__ qa, float *__restrict__ qsa, int *__restrict__ qsuma) {
     int tile = blockIdx.x >> 3, part = blockIdx.x & 7;
     if (tile >= plan->ntile_gu) return;
     Tile tl = tiles[tile];
@@ -878,44 +893,16 @@ __global__ void __launch_bounds__(256) k_act_quant(const Plan *__restrict__ plan
     int tok = utok[pair];
     int o = l & 31, g = o >> 3, h = (o >> 2) & 1, tq = o & 3;
     int ag[4][4], au[4][4]; float4 sg[4], su[4];
-    int qsum = D16 ? 0 : qsumx[tok];
+    int qsum = qsumx[tok];
 #pragma unroll
     for (int s = 0; s < 4; s++) {
         int col = g * 128 + s * 32 + h * 16 + tq * 4;
         size_t o = (size_t)pair * 2 * MFF + col;
-        if (D16) {
-            uint2 a2 = *(const uint2 *)((const int16_t *)gu + o), u2 = *(const uint2 *)((const int16_t *)gu + o + MFF);
-            uint32_t aw[2] = {a2.x, a2.y}, uw2[2] = {u2.x, u2.y};
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                ag[s][b] = (int)(int16_t)(aw[b >> 1] >> (16 * (b & 1)));
-                au[s][b] = (int)(int16_t)(uw2[b >> 1] >> (16 * (b & 1)));
-            }
-        } else {
-            int4 a4 = *(const int4 *)((const int *)gu + o), u4 = *(const int4 *)((const int *)gu + o + MFF);
-            ag[s][0] = a4.x - qsum; ag[s][1] = a4.y - qsum; ag[s][2] = a4.z - qsum; ag[s][3] = a4.w - qsum;
-            au[s][0] = u4.x - qsum; au[s][1] = u4.y - qsum; au[s][2] = u4.z - qsum; au[s][3] = u4.w - qsum;
-        }
+        int4 a4 = *(const int4 *)(gu + o), u4 = *(const int4 *)(gu + o + MFF);
+        ag[s][0] = a4.x - qsum; ag[s][1] = a4.y - qsum; ag[s][2] = a4.z - qsum; ag[s][3] = a4.w - qsum;
+        au[s][0] = u4.x - qsum; au[s][1] = u4.y - qsum; au[s][2] = u4.z - qsum; au[s][3] = u4.w - qsum;
         sg[s] = *(const float4 *)(ex.gs + col);
         su[s] = *(const float4 *)(ex.us + col);
-    }
-    if (D16) {                                       // out-of-range sums (rare): one branch for all 32
-        bool side = false;
-#pragma unroll
-        for (int s = 0; s < 4; s++)
-#pragma unroll
-            for (int b = 0; b < 4; b++) side |= (ag[s][b] == -32768) | (au[s][b] == -32768);
-        if (side) {
-#pragma unroll
-            for (int s = 0; s < 4; s++) {
-                size_t o = (size_t)pair * 2 * MFF + g * 128 + s * 32 + h * 16 + tq * 4;
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    if (ag[s][b] == -32768) ag[s][b] = gov[o + b];
-                    if (au[s][b] == -32768) au[s][b] = gov[o + MFF + b];
-                }
-            }
-        }
     }
     float qs = qsx[tok];
     float v[16];
@@ -1112,7 +1099,8 @@ __global__ void __launch_bounds__(WAVES * 64) k_gateup(const Plan *__restrict__ 
 // 16-byte read pass fall in 16 different bank groups, and a step is a constant offset).
 #define GU_LROW 272
 template <int NFU>
-__device__ __forceinline__ void gu_chunk(v16i (&acc)[2][2], const v4i (&cwc)[2][2], const int8_t *sp, int G2, int r32) {
+__device__ __forceinline__ void gu_chunk(v16i (&acc)[2][2], const v4i (&cwc)[2][2], const int8_t *sp, int G2, int r32,
+                                         bool two = true) {
     v4i bv[2][NFU];
 #pragma unroll
     for (int j = 0; j < NFU; j++) bv[0][j] = *(const v4i *)(sp + (j * 32 + r32) * GU_LROW + G2 * 128);
@@ -1128,7 +1116,8 @@ __device__ __forceinline__ void gu_chunk(v16i (&acc)[2][2], const v4i (&cwc)[2][
             int tt = t & 3;
             v4i av = decode_word((uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w));
 #pragma unroll
-            for (int j = 0; j < NFU; j++) acc[f][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[t & 1][j], acc[f][j], 0, 0, 0);
+            for (int j = 0; j < NFU; j++)
+                if (j == 0 || two) acc[f][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[t & 1][j], acc[f][j], 0, 0, 0);
         }
         // issue order of one step: next step's LDS reads, gate decode, gate MFMAs, up decode, up MFMAs
         if (t + 1 < 8) __builtin_amdgcn_sched_group_barrier(0x100, NFU, 0);
@@ -1151,11 +1140,11 @@ __device__ __forceinline__ void gu_chunk(v16i (&acc)[2][2], const v4i (&cwc)[2][
 // time. The chunk pipeline runs on across items: while the last three chunks of one item are multiplied, the
 // first three of the next are loaded (codes and activations PD = 3 chunks ahead in 4-slot register rings,
 // activations then through two LDS stages), so no item starts with an empty pipeline.
-template <bool D16>
+template <bool ACT>
 __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                       const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
-                                                      const int8_t *__restrict__ qx, const int *__restrict__ qsumx,
-                                                      void *__restrict__ gu, int *__restrict__ gov) {
+                                                      const int8_t *__restrict__ qx, const float *__restrict__ qsx,
+                                                      const int *__restrict__ qsumx, void *__restrict__ out) {
     constexpr int TN = 64, NT = 256, NF = 2, NA = 2, RB = MFF / 128, NCH = MH / 256, BB = TN * GU_LROW;
     constexpr int NPC = TN * 16 / NT;          // 4 activation pieces of 16 bytes per thread per chunk
     constexpr int PD = 3;                      // prefetch distance of the codes in chunks (ring of 4)
@@ -1173,7 +1162,7 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
 
     // current item: uniform bases (scalar registers) + 32-bit per-lane offsets
     Tile tl = tiles[cur / RB];
-    int p0 = tl.p0, ntok = tl.n, rowblk = (cur % RB) * 128 + wv * 32;
+    int p0 = tl.p0, ntok = tl.n, cu = tl.u, rowblk = (cur % RB) * 128 + wv * 32;
     const uint8_t *gcb = eptr[tl.u].gc, *ucb = eptr[tl.u].uc;
     if (tid < TN) toks[0][tid] = utok[p0 + (tid < ntok ? tid : 0)];
     __syncthreads();
@@ -1234,40 +1223,44 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
 #pragma unroll
                 for (int k = 0; k < NPC; k++) br[ch % 2][k] = *(const gptr_u4 *)(qx + nboff[k] + ((ch + PA) % NCH) * 256);
             }
-            gu_chunk<2>(acc, cw[ch % 4], &bs[ch % 2][0], G2, r32);
+            gu_chunk<2>(acc, cw[ch % 4], &bs[ch % 2][0], G2, r32, ntok > 32);
             __builtin_amdgcn_sched_barrier(0);
             if (ch + 1 < NCH || has_next) {
 #pragma unroll
                 for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst + k * 16 * GU_LROW]) = br[(ch + 1) % 2][k];
             }
         }
-        // epilogue: gate and up sums of this item (D16: d = sum - qsum as int16, else the int32 sums); token
-        // r32 of each fragment, rows (i/4)*8 + G2*4 + i%4
+        // epilogue, token r32 of each fragment, rows (i/4)*8 + G2*4 + i%4 of the wave's 32. ACT: the activation
+        // SiLU(min(G,7)) * clamp(U,-7,7) with G = (float)(sum - qsum) * qs * s_gate[row] (maple.c:471-479,
+        // 825-829), fp32 into out[pair][512]; else the raw int32 sums into out[pair][1024] (gate, then up).
+        const float *gsb = ACT ? eptr[cu].gs : nullptr, *usb = ACT ? eptr[cu].us : nullptr;
 #pragma unroll
         for (int j = 0; j < NF; j++) {
             int tk = j * 32 + r32;
             if (tk < ntok) {
                 int pair = p0 + tk;
-                int qsum = D16 ? qsumx[toks[slot][tk]] : 0;
+                int tok = toks[slot][tk];
+                float qs = ACT ? qsx[tok] : 0.0f;
+                int qsum = ACT ? qsumx[tok] : 0;
 #pragma unroll
                 for (int g = 0; g < 4; g++) {
                     int row0 = rowblk + g * 8 + G2 * 4;
+                    if (ACT) {
+                        float4 sg = *(const float4 *)(gsb + row0), su = *(const float4 *)(usb + row0);
+                        float sgv[4] = {sg.x, sg.y, sg.z, sg.w}, suv[4] = {su.x, su.y, su.z, su.w}, o[4];
 #pragma unroll
-                    for (int f = 0; f < 2; f++) {
-                        size_t o = (size_t)pair * 2 * MFF + f * MFF + row0;
-                        if (D16) {
-                            uint32_t w2[2] = {0, 0};
-#pragma unroll
-                            for (int i = 0; i < 4; i++) {
-                                int d = acc[f][j][g * 4 + i] - qsum;
-                                bool ok = d >= -32767 && d <= 32767;
-                                if (!ok) gov[o + i] = d;
-                                w2[i >> 1] |= (uint32_t)(uint16_t)(ok ? d : -32768) << (16 * (i & 1));
-                            }
-                            *(uint2 *)((int16_t *)gu + o) = make_uint2(w2[0], w2[1]);
-                        } else {
-                            *(v4i *)((int *)gu + o) = v4i{acc[f][j][g * 4], acc[f][j][g * 4 + 1], acc[f][j][g * 4 + 2], acc[f][j][g * 4 + 3]};
+                        for (int i = 0; i < 4; i++) {
+                            float gv = (float)(acc[0][j][g * 4 + i] - qsum) * qs * sgv[i];
+                            float uv = (float)(acc[1][j][g * 4 + i] - qsum) * qs * suv[i];
+                            float gg = gv < 7.0f ? gv : 7.0f;
+                            o[i] = silu_le7(gg) * __builtin_amdgcn_fmed3f(uv, -7.0f, 7.0f);
                         }
+                        *(float4 *)((float *)out + (size_t)pair * MFF + row0) = make_float4(o[0], o[1], o[2], o[3]);
+                    } else {
+#pragma unroll
+                        for (int f = 0; f < 2; f++)
+                            *(v4i *)((int *)out + (size_t)pair * 2 * MFF + f * MFF + row0) =
+                                v4i{acc[f][j][g * 4], acc[f][j][g * 4 + 1], acc[f][j][g * 4 + 2], acc[f][j][g * 4 + 3]};
                     }
                 }
             }
@@ -1280,7 +1273,7 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
 #pragma unroll
                 for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
         cur = nxt; slot ^= 1;
-        p0 = ntl.p0; ntok = ntl.n; rowblk = nrowblk;
+        p0 = ntl.p0; ntok = ntl.n; cu = ntl.u; rowblk = nrowblk;
         gcb = ngcb; ucb = nucb; aoff = naoff;
 #pragma unroll
         for (int k = 0; k < NPC; k++) boff[k] = nboff[k];
@@ -1410,8 +1403,8 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
 #pragma unroll
     for (int k = 0; k < NPC; k++) {
         int i = tid + k * NT, tk = i >> 5, part = i & 31;
-        int pr = p0 + (tk < ntok ? tk : 0);
-        *(v4i *)(&bs[tk * DN_LROW + part * 16]) = *(const gptr_u4 *)(qa + (size_t)pr * MFF + part * 16);
+        if (tk < ntok)   // rows of absent pairs only feed outputs that are never stored
+            *(v4i *)(&bs[tk * DN_LROW + part * 16]) = *(const gptr_u4 *)(qa + (size_t)(p0 + tk) * MFF + part * 16);
     }
     if (tid < RPB * 64) *(float4 *)(&sds[rb0 * 256 + tid * 4]) = *(const float4 *)(dsb + rb0 * 256 + tid * 4);
     __syncthreads();
@@ -1440,7 +1433,8 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
                     int tt = t & 3;
                     v4i av = decode_word((uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w));
 #pragma unroll
-                    for (int j = 0; j < NF; j++) acc[f][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], acc[f][j], 0, 0, 0);
+                    for (int j = 0; j < NF; j++)   // tiles of <= 32 pairs skip the empty fragment (uniform branch)
+                        if (j == 0 || ntok > 32) acc[f][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], acc[f][j], 0, 0, 0);
                 }
             }
         // D[pair][row] = (float)(sum - qsum) * qs * s_down[row]; lane: pair j*32 + r32, rows (i/4)*8 + G2*4 + i%4

@@ -52,8 +52,6 @@ struct Work {
     float *qsx = nullptr, *qsa = nullptr, *act = nullptr, *down = nullptr;
     int *qsumx = nullptr, *qsuma = nullptr;
     int *dbg_gu = nullptr, *dbg_dn = nullptr;
-    int *gu = nullptr;              // gate/up sums [P][1024] of the 64-token-tile path (int16 d, or int32 sums with checks on)
-    int *gov = nullptr;             // int32 d of the entries whose int16 slot holds -32768
     int *dov = nullptr;             // the same for the int16 down results
     int *eu = nullptr, *pu = nullptr;   // expert -> used-expert index [256], pair -> used-expert index [P]
     bool compact = false;           // the last expert stage left down as int16 (k_combine16)
@@ -80,7 +78,7 @@ static int work_alloc(Work &w, int maxtok) {
     HC(hipMalloc(&w.qx, T * MH)); HC(hipMalloc(&w.qsx, T * 4)); HC(hipMalloc(&w.qsumx, T * 4));
     HC(hipMalloc(&w.act, P * MFF * 4)); HC(hipMalloc(&w.qa, P * MFF)); HC(hipMalloc(&w.qsa, P * 4)); HC(hipMalloc(&w.qsuma, P * 4));
     HC(hipMalloc(&w.down, P * MH * 4));
-    HC(hipMalloc(&w.gu, P * 2 * MFF * 4)); HC(hipMalloc(&w.gov, P * 2 * MFF * 4)); HC(hipMalloc(&w.dov, P * MH * 4));
+    HC(hipMalloc(&w.dov, P * MH * 4));
     HC(hipMalloc(&w.eu, MNE * 4)); HC(hipMalloc(&w.pu, P * 4));
     HC(hipMalloc(&w.hs, 2 * T * MH * 2)); HC(hipMalloc(&w.hmax, T * 4)); HC(hipMalloc(&w.rpart, 4 * T * MNE * 4));
     HC(hipMalloc(&w.cand, T * RG_MAXC * 4)); HC(hipMalloc(&w.ncand, T * 4));
@@ -207,10 +205,10 @@ static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int 
 
 static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8); }  // xcd_item needs a multiple of 8
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
-    if (tn == 64) {   // int32 sums into gu (the debug buffer when checks are on: it has the same layout)
+    if (tn == 64) {   // checks on: int32 sums into the debug buffer; else the fp32 activation into w.act
         int nblk = (int)grid8(S.ncu * 2 < maxtiles * (MFF / 128) ? S.ncu * 2 : maxtiles * (MFF / 128));   // two persistent blocks per CU
-        if (dg) return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<false><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsumx, dg, nullptr); });
-        return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<true><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsumx, w.gu, w.gov); });
+        if (dg) return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<false><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, dg); });
+        return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<true><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act); });
     }
     return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<grid8(maxtiles * (MFF / 16)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
@@ -222,9 +220,9 @@ static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
 
 static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
     if (tn == 64) {
-        float *act = S.debug ? w.act : nullptr;
-        if (dg) return launch(MMOE_K_QUANT_ACT, [&] { k_act_quant<false><<<maxtiles * 8, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, dg, nullptr, act, w.qa, w.qsa, w.qsuma); });
-        return launch(MMOE_K_QUANT_ACT, [&] { k_act_quant<true><<<maxtiles * 8, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, w.gu, w.gov, act, w.qa, w.qsa, w.qsuma); });
+        // checks on: activation from the int32 sums in the debug buffer; else gate/up wrote it already
+        if (dg) return launch(MMOE_K_QUANT_ACT, [&] { k_act_quant<<<maxtiles * 8, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, dg, w.act, w.qa, w.qsa, w.qsuma); });
+        return launch(MMOE_K_QUANT_ACT, [&] { k_quant_act<<<(np + 7) / 8, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); });
     }
     return launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(np + 3) / 4, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); });
 }
