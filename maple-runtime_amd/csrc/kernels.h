@@ -1366,7 +1366,8 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
 // while the current one is multiplied. Wave w owns rows w*64 .. +64 of each row block (two 32-row
 // fragments) and both 32-pair fragments. grid = tiles x 8 / RPB items (XCD order as xcd_item).
 // Output: D16 = false, D = (float)(sum - qsum) * qs * s_down[row] (fp32); D16 = true, d = sum - qsum as int16
-// (-32768 with d in dov, int32, same index), turned into D by k_combine16 with the same operations.
+// (-32768 with d in dov, int32, same index), turned into D by k_combine16 with the same operations; the int16
+// results pass through a per-wave LDS tile so that each store writes 128 contiguous bytes of 8 pairs.
 #define DN_LROW (MFF + 16)
 template <int RPB, bool D16>
 __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
@@ -1376,7 +1377,9 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
     constexpr int TN = 64, NT = 256, NF = 2, NA = 2, NSPLIT = MH / 256 / RPB;
     constexpr int NPC = TN * (MFF / 16) / NT;   // 8 pieces of 16 bytes per thread
     __shared__ __attribute__((aligned(16))) int8_t bs[TN * DN_LROW];
-    __shared__ __attribute__((aligned(16))) float sds[MH];          // the expert's down scales
+    __shared__ __attribute__((aligned(16))) float sds[D16 ? 4 : MH];   // the expert's down scales (fp32 output)
+    constexpr int DT_LD = 72;                                       // int16 per pair row of the output tiles
+    __shared__ __attribute__((aligned(16))) int16_t dtw[D16 ? 4 * 32 * DT_LD : 8];   // one [32 pairs][64 rows] tile per wave
     int item = xcd_item(blockIdx.x, plan->ntile_gu * NSPLIT);
     if (item < 0) return;
     int tile = item / NSPLIT, rb0 = (item % NSPLIT) * RPB;
@@ -1406,7 +1409,7 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
         if (tk < ntok)   // rows of absent pairs only feed outputs that are never stored
             *(v4i *)(&bs[tk * DN_LROW + part * 16]) = *(const gptr_u4 *)(qa + (size_t)(p0 + tk) * MFF + part * 16);
     }
-    if (tid < RPB * 64) *(float4 *)(&sds[rb0 * 256 + tid * 4]) = *(const float4 *)(dsb + rb0 * 256 + tid * 4);
+    if (!D16 && tid < RPB * 64) *(float4 *)(&sds[rb0 * 256 + tid * 4]) = *(const float4 *)(dsb + rb0 * 256 + tid * 4);
     __syncthreads();
 #pragma unroll
     for (int rr = 0; rr < RPB; rr++) {
@@ -1433,11 +1436,46 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
                     int tt = t & 3;
                     v4i av = decode_word((uint32_t)(tt == 0 ? c4.x : tt == 1 ? c4.y : tt == 2 ? c4.z : c4.w));
 #pragma unroll
-                    for (int j = 0; j < NF; j++)   // tiles of <= 32 pairs skip the empty fragment (uniform branch)
-                        if (j == 0 || ntok > 32) acc[f][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], acc[f][j], 0, 0, 0);
+                    for (int j = 0; j < NF; j++) acc[f][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv[j], acc[f][j], 0, 0, 0);
                 }
             }
         // D[pair][row] = (float)(sum - qsum) * qs * s_down[row]; lane: pair j*32 + r32, rows (i/4)*8 + G2*4 + i%4
+        if (D16) {
+            // d = sum - qsum as int16 into the wave's LDS tile [32 pairs][64 rows], one pair fragment at a time,
+            // then out as 8 pairs x 128 bytes per store (lane: pair l/8 + 8k, 16-byte piece l%8)
+            int16_t *tw = dtw + wv * (32 * DT_LD);
+#pragma unroll
+            for (int j = 0; j < NF; j++) {
+#pragma unroll
+                for (int f = 0; f < NA; f++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        int rl = f * 32 + g * 8 + G2 * 4, tk = j * 32 + r32;
+                        uint32_t w2[2] = {0, 0};
+#pragma unroll
+                        for (int i = 0; i < 4; i++) {
+                            int d = acc[f][j][g * 4 + i] - qsm[j];
+                            bool ok = d >= -32767 && d <= 32767;
+                            if (!ok && tk < ntok) dov[(size_t)(p0 + tk) * MH + rb * 256 + wv * 64 + rl + i] = d;
+                            w2[i >> 1] |= (uint32_t)(uint16_t)(ok ? d : -32768) << (16 * (i & 1));
+                        }
+                        *(uint2 *)(tw + r32 * DT_LD + rl) = make_uint2(w2[0], w2[1]);
+                    }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    int pl = k * 8 + (l >> 3), pc = l & 7, tk = j * 32 + pl;
+                    uint4 v = *(const uint4 *)(tw + pl * DT_LD + pc * 8);
+                    if (tk < ntok) *(uint4 *)((int16_t *)down + (size_t)(p0 + tk) * MH + rb * 256 + wv * 64 + pc * 8) = v;
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");   // the tile is rewritten next
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            continue;
+        }
 #pragma unroll
         for (int j = 0; j < NF; j++) {
             int tk = j * 32 + r32;
@@ -1453,19 +1491,7 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
                     int ad[4]; float o[4];
 #pragma unroll
                     for (int i = 0; i < 4; i++) { ad[i] = acc[f][j][g * 4 + i]; o[i] = (float)(ad[i] - qsm[j]) * qs[j] * sdv[i]; }
-                    if (D16) {
-                        uint32_t w2[2] = {0, 0};
-#pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            int d = ad[i] - qsm[j];
-                            bool ok = d >= -32767 && d <= 32767;
-                            if (!ok) dov[(size_t)pair * MH + row0 + i] = d;
-                            w2[i >> 1] |= (uint32_t)(uint16_t)(ok ? d : -32768) << (16 * (i & 1));
-                        }
-                        *(uint2 *)((int16_t *)down + (size_t)pair * MH + row0) = make_uint2(w2[0], w2[1]);
-                    } else {
-                        *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
-                    }
+                    *(float4 *)(down + (size_t)pair * MH + row0) = make_float4(o[0], o[1], o[2], o[3]);
                     if (dbg) *(int4 *)(dbg + (size_t)pair * MH + row0) = make_int4(ad[0], ad[1], ad[2], ad[3]);
                 }
         }
