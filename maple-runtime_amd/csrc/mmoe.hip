@@ -213,6 +213,9 @@ static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
     return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<grid8(maxtiles * (MFF / 16)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
 static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
+    // large batches: 4 row blocks per workgroup (half the activation staging per row); else 2 (more workgroups)
+    if (tn == 64 && compact && maxtiles >= S.ncu)
+        return launch(MMOE_K_DOWN, [&] { k_down_tile<4, true><<<grid8(maxtiles * (MH / 256 / 4)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
     if (tn == 64 && compact) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB, true><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
     if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB, false><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, nullptr, dd); });
     return launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<grid8(maxtiles * (MH / 64)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
