@@ -181,6 +181,27 @@ int mmoe_prof(int on);
 int mmoe_prof_reset(void);
 int mmoe_prof_get(int kid, double *ms_total, long *count);
 int mmoe_device_info(char *name, int len, int *cus, int *clock_khz);
+
+/* ---- maple.c's checkpoint directory (csrc/ckpt.c) ----
+ * shard-00001.bin .. shard-00009.bin, mapped read-only, and layout.bin (26-byte packed records <kind u8, shard u8,
+ * data offset u64, scale offset u64, rows u32, cols u32> in layout.py's order), as maple.c:61-83 load().
+ * mmoe_ckpt_open checks the record kinds (maple.c:69-80) and, for the MoE tensors, shapes, bounds and 16-byte
+ * alignment (maple.c:1116-1117); 0 or -1 (mmoe_ckpt_error says why). */
+int mmoe_ckpt_open(const char *dir);
+void mmoe_ckpt_close(void);
+const char *mmoe_ckpt_error(void);
+/* Layer L's device regions and location table as maple.c:1106-1131 computes them: per shard (ascending), the
+ * page-aligned span of the layer's 256 x 6 expert tensors; shard[i], lo[i], len[i] for i < return value (<= 4);
+ * loc (may be NULL) receives GLOC[L] (256 x 12: region slot, byte offset for gate codes, gate scales, up codes,
+ * up scales, down codes, down scales). No GPU work. */
+int mmoe_ckpt_layer_plan(int L, int shard[4], uint64_t lo[4], uint64_t len[4], uint32_t *loc);
+/* Layer L's bf16 tensor `which` (0 input_layernorm, 1 post_attention_layernorm, 2 q_norm, 3 k_norm, 4 router)
+ * inside the mapping, or NULL. */
+const uint16_t *mmoe_ckpt_bf16(int L, int which);
+/* Layers L0 .. L0+nl-1: gpre_region for each planned span, then mmoe_set_layer with the location table, the
+ * router and the post-attention norm (maple.c:1106-1131 followed by the mmoe_set_layer call of INTEGRATION).
+ * Needs mmoe_init (or gpre_init) first. */
+int mmoe_ckpt_load(int L0, int nl);
 /* Diagnostic, no counterpart in the reference: checks the branch-light SiLU of the activation kernel
  * against g / (1 + exp(-g)) with IEEE division, bit for bit, over the fp32 bit patterns [lo, lo + n).
  * *nbad = number of mismatches, *first = smallest mismatching pattern (0xffffffff if none). */

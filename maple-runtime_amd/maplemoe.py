@@ -65,6 +65,9 @@ def _declare(L):
         "mmoe_prof_reset": (i, []), "mmoe_prof_get": (i, [i, C.POINTER(C.c_double), C.POINTER(C.c_long)]),
         "mmoe_device_info": (i, [C.c_char_p, i, ip, ip]),
         "mmoe_selftest_silu": (i, [C.c_uint32, C.c_uint32, C.POINTER(C.c_ulonglong), u32p]),
+        "mmoe_ckpt_open": (i, [C.c_char_p]), "mmoe_ckpt_close": (None, []), "mmoe_ckpt_error": (C.c_char_p, []),
+        "mmoe_ckpt_layer_plan": (i, [i, ip, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), vp]),
+        "mmoe_ckpt_bf16": (vp, [i, i]), "mmoe_ckpt_load": (i, [i, i]),
         "mmoe_synth_expert": (None, [u64, i, i, vp, vp, vp, vp, vp, vp]), "mmoe_synth_expert_bytes": (sz, []),
         "mmoe_synth_layer": (None, [u64, i, vp, i]), "mmoe_synth_router": (None, [u64, i, i, vp]),
         "mmoe_synth_hidden": (None, [u64, i, i, vp]), "mmoe_synth_zipf_bias": (None, [u64, d, vp]),
