@@ -231,9 +231,9 @@ def main():
                        value=round(T / pms * 1e3, 1), unit="tokens/s", ms_per_layer=round(pms, 4),
                        layer_tops=round(ops / pms / 1e9, 1), layer_frac_int8_peak=round(ops / pms / 1e9 / INT8_PEAK_TOPS, 4),
                        experts_used=plan["nu"], max_expert_load=int(cnt.max()),
-                       roofline=dict(bound="mfma", kernel="k_gateup_pk (grouped int8 MFMA)", achieved=round(g_ops / g_ms / 1e9, 1),
+                       roofline=dict(bound="mfma", kernel="k_gateup_pk<true> (grouped int8 MFMA)", achieved=round(g_ops / g_ms / 1e9, 1),
                                      peak=INT8_PEAK_TOPS, unit="TOPS", frac=round(g_ops / g_ms / 1e9 / INT8_PEAK_TOPS, 4),
-                                     traffic=pmc_traffic("k_gateup_pk"), avg_launch_us=round(g_ms * 1e3, 2)),
+                                     traffic=pmc_traffic("k_gateup_pk<true>"), avg_launch_us=round(g_ms * 1e3, 2)),
                        kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()})
 
     # ---- config 3: batched decode, 64 sequences x 24 layers (batch order), and config 0: a 128-token chunk
