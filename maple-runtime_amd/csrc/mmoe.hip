@@ -18,6 +18,14 @@
 #include <vector>
 #include "kernels.h"
 #include "decode.h"
+#ifndef GU16_W
+#define GU16_W 4    // small-tile gate/up: waves per workgroup, 16-row fragments per wave
+#define GU16_RF 1
+#endif
+#ifndef DN16_W
+#define DN16_W 4    // small-tile down: waves per workgroup, 16-row fragments per wave
+#define DN16_RF 2
+#endif
 #ifndef DN_RPB
 #define DN_RPB 2   // down row blocks of 256 per workgroup
 #endif
@@ -210,7 +218,7 @@ static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
         if (dg) return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<false><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, dg); });
         return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<true><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act); });
     }
-    return launch(MMOE_K_GATEUP, [&] { k_gateup<16, 1, 1><<<grid8(maxtiles * (MFF / 16)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
+    return launch(MMOE_K_GATEUP, [&] { k_gateup<16, GU16_W, GU16_RF><<<grid8(maxtiles * (MFF / (16 * GU16_W * GU16_RF))), 64 * GU16_W, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
 static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
     // large batches: 4 row blocks per workgroup (half the activation staging per row); else 2 (more workgroups)
@@ -218,7 +226,7 @@ static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
         return launch(MMOE_K_DOWN, [&] { k_down_tile<4, true><<<grid8(maxtiles * (MH / 256 / 4)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
     if (tn == 64 && compact) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB, true><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
     if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB, false><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, nullptr, dd); });
-    return launch(MMOE_K_DOWN, [&] { k_down<16, 1, 4><<<grid8(maxtiles * (MH / 64)), 64, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
+    return launch(MMOE_K_DOWN, [&] { k_down<16, DN16_W, DN16_RF><<<grid8(maxtiles * (MH / (16 * DN16_W * DN16_RF))), 64 * DN16_W, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
 }
 
 static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
