@@ -190,23 +190,49 @@ __device__ __forceinline__ float hsum8(const float *v) {
 // its chain-major copy (wc[e][j][m] = w[e][j + NCH m]), so a chain reads contiguous memory; its loads are
 // issued 16 at a time ahead of the FMAs. Chain j runs over columns j, j + NCH, ... with fma(w, x, acc); the
 // chains are then folded as described above (NCH = 16: chain j + chain j+8 first).
-template <int NCH>
-__global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__ hn, int nb, const uint16_t *__restrict__ wc,
-                                                       const float *__restrict__ bias, float *__restrict__ rl) {
+// NORM: `in` is the hidden state x and the block first forms hn = rmsnorm(x, post_ln) for its token with
+// exactly k_rmsnorm's arithmetic (thread t sums columns t, t+256, ... in fp64, then the same 256-wide tree);
+// blocks with blockIdx.x == 0 write hn to hn_out. Else `in` is hn.
+template <int NCH, bool NORM = false>
+__global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__ in, int nb, const uint16_t *__restrict__ wc,
+                                                       const float *__restrict__ bias, float *__restrict__ rl,
+                                                       const uint16_t *__restrict__ post_ln = nullptr, float *__restrict__ hn_out = nullptr) {
     constexpr int LEN = MH / NCH, HP = LEN + 4;
     __shared__ __attribute__((aligned(16))) float hc[NCH * HP];
+    __shared__ double red[NORM ? 256 : 1];
+    __shared__ float kk;
     int tid = threadIdx.x, b = blockIdx.y, j = tid % NCH, e = blockIdx.x * (256 / NCH) + tid / NCH;
     const gptr_u4 *wp = (const gptr_u4 *)(wc + ((size_t)e * NCH + j) * LEN);
     v4i wv[16];
 #pragma unroll
     for (int q = 0; q < 16; q++) wv[q] = wp[q];
-    const float *xr = hn + (size_t)b * MH;
+    const float *xr = in + (size_t)b * MH;
+    if (NORM) {
+        float v[8]; double sq = 0.0;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        int c = (tid + 256 * i) * 4;
-        float4 f = *(const float4 *)(xr + c);
-        hc[((c + 0) % NCH) * HP + (c + 0) / NCH] = f.x; hc[((c + 1) % NCH) * HP + (c + 1) / NCH] = f.y;
-        hc[((c + 2) % NCH) * HP + (c + 2) / NCH] = f.z; hc[((c + 3) % NCH) * HP + (c + 3) / NCH] = f.w;
+        for (int i = 0; i < 8; i++) { v[i] = xr[tid + i * 256]; sq += (double)v[i] * (double)v[i]; }
+        red[tid] = sq;
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) { if (tid < o) red[tid] += red[tid + o]; __syncthreads(); }
+        if (tid == 0) kk = 1.0f / sqrtf((float)(red[0] / (double)MH) + 1e-6f);
+        __syncthreads();
+        float k = kk;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            int c = tid + i * 256;
+            float wn = post_ln ? bf16f(post_ln[c]) : 1.0f;
+            float h = v[i] * k * wn;
+            hc[(c % NCH) * HP + c / NCH] = h;
+            if (blockIdx.x == 0) hn_out[(size_t)b * MH + c] = h;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            int c = (tid + 256 * i) * 4;
+            float4 f = *(const float4 *)(xr + c);
+            hc[((c + 0) % NCH) * HP + (c + 0) / NCH] = f.x; hc[((c + 1) % NCH) * HP + (c + 1) / NCH] = f.y;
+            hc[((c + 2) % NCH) * HP + (c + 2) / NCH] = f.z; hc[((c + 3) % NCH) * HP + (c + 3) / NCH] = f.w;
+        }
     }
     __syncthreads();
     const float *h = hc + j * HP;

@@ -63,6 +63,8 @@ struct Work {
     int *dov = nullptr;             // the same for the int16 down results
     int *eu = nullptr, *pu = nullptr;   // expert -> used-expert index [256], pair -> used-expert index [P]
     bool compact = false;           // the last expert stage left down as int16 (k_combine16)
+    const float *norm_x = nullptr;  // set by mmoe_stack_dev: the router normalises this x into hn (post_ln norm_w)
+    const uint16_t *norm_w = nullptr;
     uint16_t *hs = nullptr;         // MoE input split into 2 bf16 parts [2][T][2048] (approximate router)
     float *rpart = nullptr;         // partial router logits [4][T][256]
     float *hmax = nullptr;          // max |hn| per token
@@ -172,11 +174,16 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
     LayerW &lw = S.layers[L];
     w.refine = false;
     if (!lw.router) { seterr("layer %d has no router (mmoe_set_layer)", L); return -1; }
+    // w.norm_x set (stacked path): the chain routers form hn = rmsnorm(x, post_ln) into d_hn themselves
+    float *hn_w = const_cast<float *>(d_hn);
     if (order == MMOE_ORDER_STEP) {
+        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { k_router_chains<16, true><<<dim3(MNE * 16 / 256, nb), 256, 0, S.st>>>(w.norm_x, nb, lw.rc16, lw.bias, w.rl, w.norm_w, hn_w); });
         return launch(MMOE_K_ROUTER, [&] { k_router_chains<16><<<dim3(MNE * 16 / 256, nb), 256, 0, S.st>>>(d_hn, nb, lw.rc16, lw.bias, w.rl); });
     }
-    if (nb < 512)   // one block per (token, 32 experts): 8 nb blocks, router reread from L2 per token
+    if (nb < 512) {   // one block per (token, 32 experts): 8 nb blocks, router reread from L2 per token
+        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { k_router_chains<8, true><<<dim3(MNE * 8 / 256, nb), 256, 0, S.st>>>(w.norm_x, nb, lw.rc8, lw.bias, w.rl, w.norm_w, hn_w); });
         return launch(MMOE_K_ROUTER, [&] { k_router_chains<8><<<dim3(MNE * 8 / 256, nb), 256, 0, S.st>>>(d_hn, nb, lw.rc8, lw.bias, w.rl); });
+    }
     if (S_router_exact)
         return launch(MMOE_K_ROUTER, [&] { k_router_gemm<4><<<dim3((nb + 15) / 16, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
     // approximate logits on the bf16 MFMA; k_cand + k_chain make the top-8 exact
@@ -604,6 +611,13 @@ int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order) {
         if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("mmoe_stack_dev: layer %d not set", L); return -1; }
         if (nb <= DEC_MAXTOK && S_dec_enabled) { if (moe_dec(L, d_x, 1, nb, d_x, order)) return -1; continue; }
         const uint16_t *pw = S.layers[L].post_ln;
+        if (order == MMOE_ORDER_STEP || nb < 512) {   // the chain router forms hn itself (no rmsnorm launch)
+            w.norm_x = d_x; w.norm_w = pw;
+            int rc = moe_dev(L, w.hn, nb, d_x, order);
+            w.norm_x = nullptr; w.norm_w = nullptr;
+            if (rc) return -1;
+            continue;
+        }
         if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(d_x, pw, w.hn, nb); })) return -1;
         if (moe_dev(L, w.hn, nb, d_x, order)) return -1;
     }
