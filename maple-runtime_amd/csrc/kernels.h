@@ -563,73 +563,76 @@ __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, 
 __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl, const float *__restrict__ hn, int nb,
                                                     int *__restrict__ top, float *__restrict__ tw, int8_t *__restrict__ qx,
                                                     float *__restrict__ qsx, int *__restrict__ qsumx, int *__restrict__ hist);
-// The plan for the device-side routing of a large batch, in one block, from the per-chunk expert counts
-// hist[chunk of 64 tokens][expert] that k_topk_quant accumulated (read, then cleared for the next call).
-__global__ void __launch_bounds__(256) k_plan_top(int *__restrict__ hist, int nb, int *__restrict__ base, Plan *__restrict__ plan,
-                                                  const ExpPtr *__restrict__ layer_tab, ExpPtr *__restrict__ eptr_u, int tn,
-                                                  Tile *__restrict__ tiles, int *__restrict__ eu) {
+// Grouping of a large batch (maple.c:924-938, 1018-1019) in one launch: block c (chunk of 64 tokens, 512
+// threads) reads the per-chunk expert counts hist[chunk][expert] that k_topk_quant accumulated (read only; the
+// combine of the same call clears them) and forms in LDS the per-expert totals and their exclusive scans: pair
+// offsets (ustart), used-expert indices (ue, eu) and tile offsets. Block 0 also publishes the plan, the tile
+// table and the used experts' pointer table. Then thread (token, slot) places its pair: slot = the expert's
+// offset + pairs of earlier chunks + the number of earlier tokens of the chunk that picked the expert
+// (popcount of a 64-bit token mask), stable in token order as maple.c's counting sort; it writes utok/uw
+// (maple.c:934-936), tp (pair ids of token b ascending), sp (pair of slot s) and pu (used expert of a pair).
+__global__ void __launch_bounds__(512) k_group(const int *__restrict__ hist, int nb, Plan *__restrict__ plan,
+                                               const ExpPtr *__restrict__ layer_tab, ExpPtr *__restrict__ eptr_u, int tn,
+                                               Tile *__restrict__ tiles, int *__restrict__ eu_out, const int *__restrict__ top,
+                                               const float *__restrict__ tw, int *__restrict__ utok, float *__restrict__ uw,
+                                               int *__restrict__ tp, int *__restrict__ sp, int *__restrict__ pu) {
     constexpr int MAXCH = (2048 + 63) / 64;
-    __shared__ int sc[MNE], su[MNE], st[MNE];
-    int e = threadIdx.x, nchunk = (nb + 63) / 64;
-    int cnt[MAXCH];
-#pragma unroll
-    for (int c = 0; c < MAXCH; c++) cnt[c] = c < nchunk ? hist[c * MNE + e] : 0;   // independent loads
-#pragma unroll
-    for (int c = 0; c < MAXCH; c++) if (c < nchunk) hist[c * MNE + e] = 0;        // ready for the next call
-    int run = 0, hv[MAXCH];
-#pragma unroll
-    for (int c = 0; c < MAXCH; c++) { hv[c] = run; run += cnt[c]; }   // hv: exclusive prefix over chunks
-    int used = run > 0, nt = (run + tn - 1) / tn;
-    sc[e] = run; su[e] = used; st[e] = nt;
-    __syncthreads();
-    for (int o = 1; o < MNE; o <<= 1) {
-        int a = e >= o ? sc[e - o] : 0, bq = e >= o ? su[e - o] : 0, cq = e >= o ? st[e - o] : 0;
-        __syncthreads();
-        sc[e] += a; su[e] += bq; st[e] += cq;
-        __syncthreads();
-    }
-    int pstart = sc[e] - run, uidx = su[e] - used, tstart = st[e] - nt;
-    eu[e] = used ? uidx : -1;   // expert -> used-expert index (for pu in k_scatter)
-    if (used) {
-        plan->ue[uidx] = e;
-        plan->ustart[uidx] = pstart;
-        plan->tstart[uidx] = tstart;
-        if (layer_tab) eptr_u[uidx] = layer_tab[e];
-        for (int i = 0; i < nt; i++) tiles[tstart + i] = Tile{uidx, pstart + i * tn, min(tn, run - i * tn), 0};
-    }
-#pragma unroll
-    for (int c = 0; c < MAXCH; c++) if (c < nchunk) base[c * MNE + e] = hv[c] + pstart;
-    if (e == MNE - 1) {
-        int nu = su[e];
-        plan->nu = nu; plan->np = sc[e]; plan->ntile_gu = st[e]; plan->tn = tn;
-        plan->ustart[nu] = sc[e]; plan->tstart[nu] = st[e];
-    }
-}
-
-// Block = one chunk of 64 tokens, 512 threads, thread = one (token, slot) pair. Pair slot of (b, s) =
-// base[chunk][e] + number of earlier tokens of the chunk that picked e, counted as the popcount of a
-// per-expert 64-bit token mask of the chunk. Writes utok/uw (maple.c:934-936), tp (pair ids of token b
-// ascending) and sp (pair id of slot s, for the decode combine order).
-__global__ void __launch_bounds__(512) k_scatter(const int *__restrict__ top, const float *__restrict__ tw, int nb,
-                                                 const int *__restrict__ base, int *__restrict__ utok, float *__restrict__ uw,
-                                                 int *__restrict__ tp, int *__restrict__ sp, const int *__restrict__ eu,
-                                                 int *__restrict__ pu) {
+    __shared__ int sc[MNE], su[MNE], st[MNE], sbase[MNE], seu[MNE];
     __shared__ unsigned long long msk[MNE];
     __shared__ int slots[64][MTOPK];
-    int c = blockIdx.x, t = threadIdx.x, tk = t >> 3, s = t & 7, b = c * 64 + tk;
-    if (t < MNE) msk[t] = 0ull;
+    int c = blockIdx.x, t = threadIdx.x, nchunk = (nb + 63) / 64;
+    int run = 0, pre = 0, used = 0, nt = 0;
+    if (t < MNE) {
+        int cnt[MAXCH];
+#pragma unroll
+        for (int k = 0; k < MAXCH; k++) cnt[k] = k < nchunk ? hist[k * MNE + t] : 0;   // independent loads
+#pragma unroll
+        for (int k = 0; k < MAXCH; k++) { if (k == c) pre = run; run += cnt[k]; }
+        used = run > 0; nt = (run + tn - 1) / tn;
+        sc[t] = run; su[t] = used; st[t] = nt; msk[t] = 0ull;
+    }
     __syncthreads();
+    for (int o = 1; o < MNE; o <<= 1) {
+        int a = 0, bq = 0, cq = 0;
+        if (t < MNE && t >= o) { a = sc[t - o]; bq = su[t - o]; cq = st[t - o]; }
+        __syncthreads();
+        if (t < MNE) { sc[t] += a; su[t] += bq; st[t] += cq; }
+        __syncthreads();
+    }
+    if (t < MNE) {
+        int e = t, pstart = sc[e] - run, uidx = su[e] - used, tstart = st[e] - nt;
+        sbase[e] = pstart + pre;
+        seu[e] = used ? uidx : -1;
+        if (c == 0) {
+            eu_out[e] = seu[e];
+            if (used) {
+                plan->ue[uidx] = e;
+                plan->ustart[uidx] = pstart;
+                plan->tstart[uidx] = tstart;
+                if (layer_tab) eptr_u[uidx] = layer_tab[e];
+                for (int i = 0; i < nt; i++) tiles[tstart + i] = Tile{uidx, pstart + i * tn, min(tn, run - i * tn), 0};
+            }
+            if (e == MNE - 1) {
+                int nu = su[e];
+                plan->nu = nu; plan->np = sc[e]; plan->ntile_gu = st[e]; plan->tn = tn;
+                plan->ustart[nu] = sc[e]; plan->tstart[nu] = st[e];
+            }
+        }
+    }
+    __syncthreads();
+    // placement: thread (token tk of the chunk, slot s)
+    int tk = t >> 3, s = t & 7, b = c * 64 + tk;
     bool live = b < nb;
     int e = live ? top[b * MTOPK + s] : 0;
     float wv = live ? tw[b * MTOPK + s] : 0.0f;
-    int bs = live ? base[c * MNE + e] : 0;
+    int bs = live ? sbase[e] : 0;
     if (live) atomicOr(&msk[e], 1ull << tk);
     __syncthreads();
     int slot = bs + __popcll(msk[e] & ((1ull << tk) - 1ull));
     if (live) {
         utok[slot] = b; uw[slot] = wv;
         if (sp) sp[b * MTOPK + s] = slot;
-        if (pu) pu[slot] = eu[e];
+        if (pu) pu[slot] = seu[e];
     }
     slots[tk][s] = slot;
     __syncthreads();
@@ -727,7 +730,7 @@ __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl
     int b = blockIdx.x * 4 + wv;
     if (b >= nb) return;  // whole wave exits together
     int ek = topk_wave(rl + (size_t)b * MNE, E[wv], l, top + b * MTOPK, tw + b * MTOPK);
-    if (hist && l < MTOPK) atomicAdd(&hist[(b >> 6) * MNE + ek], 1);   // per-chunk expert counts for k_plan_top
+    if (hist && l < MTOPK) atomicAdd(&hist[(b >> 6) * MNE + ek], 1);   // per-chunk expert counts for k_group
     quant_wave<MH>(hn + (size_t)b * MH, l, qx + (size_t)b * MH, qsx + b, qsumx + b);
 }
 
@@ -1541,7 +1544,9 @@ __global__ void __launch_bounds__(256) k_combine16(const int16_t *__restrict__ d
                                                    const int *__restrict__ tp, const int *__restrict__ sp,
                                                    const float *__restrict__ tw, int nb, float *__restrict__ x, int mode,
                                                    const int *__restrict__ pu, const ExpPtr *__restrict__ eptr,
-                                                   const float *__restrict__ qsa, const int *__restrict__ dov) {
+                                                   const float *__restrict__ qsa, const int *__restrict__ dov,
+                                                   int *__restrict__ hz, int hzn) {
+    if (hz && (int)(blockIdx.x * 256 + threadIdx.x) < hzn) hz[blockIdx.x * 256 + threadIdx.x] = 0;   // k_group's counts, for the next call
     __shared__ int sa[MTOPK];
     __shared__ float sw[MTOPK], sq[MTOPK];
     __shared__ const float *sds[MTOPK];
@@ -1591,8 +1596,10 @@ __global__ void __launch_bounds__(256) k_combine16(const int16_t *__restrict__ d
 
 __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ down, const float *__restrict__ uw,
                                                  const int *__restrict__ tp, const int *__restrict__ sp,
-                                                 const float *__restrict__ tw, int nb, float *__restrict__ x, int mode) {
+                                                 const float *__restrict__ tw, int nb, float *__restrict__ x, int mode,
+                                                 int *__restrict__ hz = nullptr, int hzn = 0) {
     int gid = blockIdx.x * 256 + threadIdx.x;
+    if (hz && gid < hzn) hz[gid] = 0;   // k_group's counts, for the next call
     int b = gid / (MH / 4), c = (gid % (MH / 4)) * 4;
     if (b >= nb) return;
     float4 *xp = (float4 *)(x + (size_t)b * MH + c);

@@ -52,7 +52,7 @@ static void seterr(const char *fmt, ...) {
 struct Work {
     int maxtok = 0, maxp = 0;
     float *hn = nullptr, *x = nullptr, *rl = nullptr, *tw = nullptr, *uw = nullptr;
-    int *top = nullptr, *hist = nullptr, *base = nullptr, *utok = nullptr, *tp = nullptr, *sp = nullptr, *ustart = nullptr;
+    int *top = nullptr, *hist = nullptr, *utok = nullptr, *tp = nullptr, *sp = nullptr, *ustart = nullptr;
     Plan *plan = nullptr;
     Tile *tiles = nullptr;
     ExpPtr *eptr = nullptr;
@@ -63,6 +63,7 @@ struct Work {
     int *dov = nullptr;             // the same for the int16 down results
     int *eu = nullptr, *pu = nullptr;   // expert -> used-expert index [256], pair -> used-expert index [P]
     bool compact = false;           // the last expert stage left down as int16 (k_combine16)
+    int hist_used = 0;              // entries of hist the device grouping filled; the combine clears them
     const float *norm_x = nullptr;  // set by mmoe_stack_dev: the router normalises this x into hn (post_ln norm_w)
     const uint16_t *norm_w = nullptr;
     uint16_t *hs = nullptr;         // MoE input split into 2 bf16 parts [2][T][2048] (approximate router)
@@ -80,8 +81,8 @@ static int work_alloc(Work &w, int maxtok) {
     size_t T = maxtok, P = w.maxp;
     HC(hipMalloc(&w.hn, T * MH * 4)); HC(hipMalloc(&w.x, T * MH * 4)); HC(hipMalloc(&w.rl, T * MNE * 4));
     HC(hipMalloc(&w.top, T * MTOPK * 4)); HC(hipMalloc(&w.tw, T * MTOPK * 4));
-    HC(hipMalloc(&w.hist, (size_t)nch * MNE * 4)); HC(hipMalloc(&w.base, (size_t)nch * MNE * 4));
-    HC(hipMemset(w.hist, 0, (size_t)nch * MNE * 4));   // k_plan_top clears what it used
+    HC(hipMalloc(&w.hist, (size_t)nch * MNE * 4));
+    HC(hipMemset(w.hist, 0, (size_t)nch * MNE * 4));   // the combine after k_group clears what it used
     HC(hipMalloc(&w.plan, sizeof(Plan))); HC(hipMalloc(&w.tiles, sizeof(Tile) * ((size_t)w.maxp / 16 + MNE + 8))); HC(hipMalloc(&w.eptr, MNE * sizeof(ExpPtr)));
     HC(hipMalloc(&w.utok, P * 4)); HC(hipMalloc(&w.uw, P * 4)); HC(hipMalloc(&w.tp, P * 4)); HC(hipMalloc(&w.sp, P * 4));
     HC(hipMalloc(&w.ustart, (MNE + 1) * 4));
@@ -205,9 +206,10 @@ static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) 
             })) return -1;
     }
     if (launch(MMOE_K_TOPK, [&] { k_topk_quant<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
+    w.hist_used = nch * MNE;   // cleared by this call's combine
     return launch(MMOE_K_GROUP, [&] {
-        k_plan_top<<<1, 256, 0, S.st>>>(w.hist, nb, w.base, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles, w.eu);
-        k_scatter<<<nch, 512, 0, S.st>>>(w.top, w.tw, nb, w.base, w.utok, w.uw, w.tp, w.sp, w.eu, w.pu);
+        k_group<<<nch, 512, 0, S.st>>>(w.hist, nb, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles, w.eu, w.top, w.tw, w.utok, w.uw,
+                                       w.tp, w.sp, w.pu);
     });
 }
 
@@ -244,7 +246,7 @@ static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
     }
     return launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(np + 3) / 4, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); });
 }
-// device_grouping: the grouping came from k_plan_top/k_scatter (pu is valid), so the 64-token-tile path may
+// device_grouping: the grouping came from k_group (pu is valid), so the 64-token-tile path may
 // hand the down results to k_combine as int16 (not with checks on: the tests read them as fp32)
 static int stage_experts(Work &w, int np, int nu_max, int tn, bool device_grouping) {
     LAST.w = &w; LAST.np = np; LAST.nu_max = nu_max; LAST.tn = tn; LAST.dec = 0;
@@ -260,9 +262,12 @@ static int stage_experts(Work &w, int np, int nu_max, int tn, bool device_groupi
 
 static int stage_combine(Work &w, int nb, float *d_x, int mode) {
     int n = nb * (MH / 4);
+    int hzn = w.hist_used;   // the device grouping's counts (k_group) go back to zero here
+    w.hist_used = 0;
+    int *hz = hzn ? w.hist : nullptr;
     if (w.compact)
-        return launch(MMOE_K_COMBINE, [&] { k_combine16<<<nb, 256, 0, S.st>>>((const int16_t *)w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode, w.pu, w.eptr, w.qsa, w.dov); });
-    return launch(MMOE_K_COMBINE, [&] { k_combine<<<(n + 255) / 256, 256, 0, S.st>>>(w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode); });
+        return launch(MMOE_K_COMBINE, [&] { k_combine16<<<nb, 256, 0, S.st>>>((const int16_t *)w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode, w.pu, w.eptr, w.qsa, w.dov, hz, hzn); });
+    return launch(MMOE_K_COMBINE, [&] { k_combine<<<(n + 255) / 256, 256, 0, S.st>>>(w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode, hz, hzn); });
 }
 
 // Small batches (decode): three kernels, see decode.h. in = hn (do_norm 0) or the hidden state x whose
