@@ -253,3 +253,45 @@ def test_moe_batch_tn64_compact_sums(layer0):
         print("\n  compact sums: x bit-exact", np.array_equal(xg, xo))
     finally:
         M.check(lib.mmoe_set_debug(1), "debug on")
+
+
+@pytest.fixture(scope="module")
+def zipf_layer():
+    """Layer 6: its own experts and router plus the bench's Zipf(1.1) expert bias (config 2)"""
+    lib = M.lib()
+    M.check(lib.mmoe_init(2048), "mmoe_init")
+    hl = HostLayer(SEED, 6)
+    hl.rid = M.register_layer(6, hl.blk, hl.router)
+    hl.bias = M.zipf_bias(SEED, 1.1)
+    M.check(lib.mmoe_set_bias(6, M.ptr(hl.bias)), "bias")
+    yield hl
+    M.check(lib.mmoe_set_bias(6, None), "bias off")
+
+
+@pytest.mark.parametrize("T", [2048, 2047])
+def test_full_size_tokens_independent(zipf_layer, T):
+    """BASELINE config 2 at full size (2048 Zipf-routed tokens, checks off: the int16 / fused-activation path).
+    Each token's MoE output depends on that token only, and the batch combine sums a token's pairs in ascending
+    expert order whatever the batch, so the full batch must reproduce, bit for bit, the rows of sub-batches run
+    alone (two halves, and a scattered 48-token sample); the sample is also checked against the oracle."""
+    lib = M.lib()
+    L = zipf_layer.L
+    M.check(lib.mmoe_set_debug(0), "debug off")
+    try:
+        x, hn = normed_hidden(SEED, 500 + T, T)
+        xf = run_gpu(L, hn, x, M.ORDER_BATCH)
+        h = T // 2
+        for lo, hi in ((0, h), (h, T)):
+            xs = run_gpu(L, np.ascontiguousarray(hn[lo:hi]), np.ascontiguousarray(x[lo:hi]), M.ORDER_BATCH)
+            assert np.array_equal(xs, xf[lo:hi]), f"rows {lo}..{hi} differ from the full batch"
+        rng = np.random.default_rng(T)
+        idx = np.sort(rng.choice(T, 48, replace=False))
+        hs, xsmp = np.ascontiguousarray(hn[idx]), np.ascontiguousarray(x[idx])
+        xg = run_gpu(L, hs, xsmp, M.ORDER_BATCH)
+        assert np.array_equal(xg, xf[idx]), "sampled rows differ from the full batch"
+        xo = xsmp.copy()
+        O.moe_batch(hs, zipf_layer.router, zipf_layer.table, xo, bias=zipf_layer.bias)
+        assert relmax(xf[idx] - xsmp, xo - xsmp) <= TOL
+        print(f"\n  T={T}: halves and sample bit-exact; sample vs oracle bit-exact {np.array_equal(xf[idx], xo)}")
+    finally:
+        M.check(lib.mmoe_set_debug(1), "debug on")
