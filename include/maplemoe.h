@@ -60,8 +60,13 @@ int gpre_region(const void *p, size_t len);
 double gpre_moe(const float *x, int nb, int nu, const uint32_t *loc, const int *regs, const int *next,
                 const int *ustart, const int *ptok, const float *pw, const int *tp, float *y);
 int gpre_stage(size_t bytes);
-/* Dense q/k/v/o projections (gpu_pre.m:200-256): not part of the MoE path; gpre_dense_done returns -1 so
- * maple.c keeps them on the CPU (maple.c:1141). */
+/* Dense q/k/v/o projections, replaces gpu_pre.m:200-256 (declared maple.c:261-263, called maple.c:1136-1141,
+ * 692, 723). gpre_dense_add(g, codes, scales, rows, cols) stages one ternary matrix of group g (2L: q, k, v;
+ * 2L+1: o), rows a multiple of 256, cols 2048, at most 3 per group; its outputs follow the group's earlier
+ * ones. gpre_dense_done(maxtok) copies them to HBM (0, or -1 when a matrix was malformed or the context is
+ * missing: maple.c then keeps the projections on the CPU). gpre_dense(g, x, nb, y): synchronous,
+ * y[nb][rows of g] = the matrices times x[nb][2048] (host arrays), with maple.c's int8 arithmetic (prep,
+ * tdot_multi): equal to its CPU projections bit for bit. Returns device seconds, or -1. */
 void gpre_dense_add(int g, const uint8_t *codes, const float *scales, int rows, int cols);
 int gpre_dense_done(int maxtok);
 double gpre_dense(int g, const float *x, int nb, float *y);

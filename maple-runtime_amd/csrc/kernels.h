@@ -1310,6 +1310,85 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
 #undef GU_LOADC
 }
 
+// ---- dense ternary projections (attention q/k/v and o; maple.c jobB_qkv / jobB_o, 459-470, through
+// tdot_multi 423-458): y[b][yoff + r] = (float)(sum_c code * q[b] - qsum[b]) * qs[b] * s[r], K = 2048 ----
+struct DenseMat { const uint8_t *codes; const float *scales; int rows, yoff; };
+// One workgroup = 256 rows (wave w: rows w*64 .. +64 as two 32-row fragments) x 64 tokens, on
+// v_mfma_i32_32x32x32_i8 with gu_chunk's operand mapping (the two row fragments take the places of gate and
+// up). Activations pass through two padded LDS stages, codes 2 chunks ahead in registers, as k_gateup.
+// grid = (sum of rows / 256, ceil(nb / 64)); rbs[m] = first row block of matrix m (rbs[nmat] = total).
+__global__ void __launch_bounds__(256) k_dense(const DenseMat *__restrict__ mats, const int *__restrict__ rbs, int nmat,
+                                               int nb, int ys, const int8_t *__restrict__ qx, const float *__restrict__ qsx,
+                                               const int *__restrict__ qsumx, float *__restrict__ y) {
+    constexpr int TN = 64, NCH = MH / 256, BB = TN * GU_LROW, NPC = TN * 16 / 256;
+    __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
+    int rb = blockIdx.x, m = 0;
+    while (m + 1 < nmat && rb >= rbs[m + 1]) m++;
+    DenseMat M = mats[m];
+    int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G2 = l >> 5, r32 = l & 31;
+    int row0 = (rb - rbs[m]) * 256 + wv * 64, t0 = blockIdx.y * TN, ntok = min(TN, nb - t0);
+    int part = tid & 15, bdst = (tid >> 4) * GU_LROW + part * 16;
+    uint32_t boff[NPC];
+#pragma unroll
+    for (int k = 0; k < NPC; k++) boff[k] = (uint32_t)(t0 + min((tid >> 4) + 16 * k, ntok - 1)) * MH + part * 16;
+    const uint8_t *fa = M.codes + (size_t)(row0 + r32) * (MH / 4) + G2 * 32, *fb = fa + (size_t)32 * (MH / 4);
+    v16i acc[2][2];
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
+    v4i cw[4][2][2], br[2][NPC];
+#define DN2_LOADC(slot_, c_)                                                                                    \
+    {                                                                                                           \
+        cw[slot_][0][0] = *(const gptr_u4 *)(fa + (c_) * 64); cw[slot_][0][1] = *(const gptr_u4 *)(fa + (c_) * 64 + 16); \
+        cw[slot_][1][0] = *(const gptr_u4 *)(fb + (c_) * 64); cw[slot_][1][1] = *(const gptr_u4 *)(fb + (c_) * 64 + 16); \
+    }
+    DN2_LOADC(0, 0); DN2_LOADC(1, 1);
+#pragma unroll
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+        for (int k = 0; k < NPC; k++) br[c][k] = *(const gptr_u4 *)(qx + boff[k] + c * 256);
+#pragma unroll
+    for (int k = 0; k < NPC; k++) *(v4i *)(&bs[0][bdst + k * 16 * GU_LROW]) = br[0][k];
+#pragma unroll
+    for (int ch = 0; ch < NCH; ch++) {
+        __syncthreads();
+        if (ch + 2 < NCH) {
+            DN2_LOADC((ch + 2) % 4, ch + 2)
+#pragma unroll
+            for (int k = 0; k < NPC; k++) br[ch % 2][k] = *(const gptr_u4 *)(qx + boff[k] + (ch + 2) * 256);
+        }
+        gu_chunk<2>(acc, cw[ch % 4], &bs[ch % 2][0], G2, r32);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ch + 1 < NCH) {
+#pragma unroll
+            for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst + k * 16 * GU_LROW]) = br[(ch + 1) % 2][k];
+        }
+    }
+#undef DN2_LOADC
+    // token t0 + j*32 + r32; rows row0 + f*32 + (i/4)*8 + G2*4 + i%4
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        int tk = j * 32 + r32;
+        if (tk >= ntok) continue;
+        int b = t0 + tk;
+        float qs = qsx[b]; int qsum = qsumx[b];
+#pragma unroll
+        for (int f = 0; f < 2; f++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                int r = row0 + f * 32 + g * 8 + G2 * 4;
+                float4 sc = *(const float4 *)(M.scales + r);
+                float sv[4] = {sc.x, sc.y, sc.z, sc.w}, o[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) o[i] = (float)(acc[f][j][g * 4 + i] - qsum) * qs * sv[i];
+                *(float4 *)(y + (size_t)b * ys + M.yoff + r) = make_float4(o[0], o[1], o[2], o[3]);
+            }
+    }
+}
+
 // Down (maple.c:498-505): D[pair][row] = (float)(sum c*qa - qsuma) * qsa * s_down[row]. Block = WAVES waves
 // of RF 16-row fragments; K = 512 staged in LDS at once. Pairs of a tile are contiguous (no gather).
 // 1-D grid of (token tile x row block) items in XCD order, as k_gateup.

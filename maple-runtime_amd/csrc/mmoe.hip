@@ -418,11 +418,99 @@ double gpre_moe(const float *x, int nb, int nu, const uint32_t *loc, const int *
 // gpu_pre.m:257-264: seconds spent moving weights to the card (here: the one-time region copies)
 double gpre_blit_seconds(void) { return S.t_region; }
 
-// Dense attention projections (gpu_pre.m:200-256) are not part of the MoE path: gpre_dense_done reports
-// failure, which makes maple.c keep q/k/v/o on the CPU (maple.c:1141).
-void gpre_dense_add(int g, const uint8_t *codes, const float *scales, int rows, int cols) { (void)g; (void)codes; (void)scales; (void)rows; (void)cols; }
-int gpre_dense_done(int maxtok) { (void)maxtok; fprintf(stderr, "maplemoe: attention projections stay on the CPU (not part of this build)\n"); return -1; }
-double gpre_dense(int g, const float *x, int nb, float *y) { (void)g; (void)x; (void)nb; (void)y; seterr("gpre_dense: not part of this build"); return -1.0; }
+// ---- dense ternary projections: attention q/k/v (group 2L) and o (group 2L + 1), gpu_pre.m:200-256 ----
+// The matrices are staged on the host by gpre_dense_add and copied into one HBM buffer by gpre_dense_done.
+// gpre_dense quantises x as maple.c's prep (maple.c:183-194) and runs k_dense, the int8 GEMM with maple.c's
+// integer and fp32 sequence (tdot_multi), so y equals maple.c's CPU projections (jobB_qkv / jobB_o) bit for
+// bit (the Metal version multiplies fp32 activations instead).
+#define DGRP 48
+static struct {
+    std::vector<uint8_t> host;                   // staging until gpre_dense_done
+    struct Mat { size_t codes, scales; int rows; } mat[DGRP][3];
+    int n[DGRP], rows[DGRP], maxtok;
+    uint8_t *dev;                                // all matrices in HBM
+    DenseMat *dmat;                              // per group, 3 slots
+    int *drbs;                                   // per group, 4 row-block offsets
+    float *y;                                    // [maxtok][max rows]
+    int ymax, ready, bad;
+    double t;
+} DN;
+
+void gpre_dense_add(int g, const uint8_t *codes, const float *scales, int rows, int cols) {
+    if (DN.ready) { seterr("gpre_dense_add after gpre_dense_done: ignored"); return; }
+    if (g < 0 || g >= DGRP || DN.n[g] >= 3 || cols != MH || rows < 256 || rows % 256 || !codes || !scales) {
+        DN.bad = 1;   // reported by gpre_dense_done (this call returns nothing, as in gpu_pre.m)
+        return;
+    }
+    auto put = [&](const void *p, size_t n) {
+        size_t o = (DN.host.size() + 255) / 256 * 256;
+        DN.host.resize(o + n);
+        memcpy(DN.host.data() + o, p, n);
+        return o;
+    };
+    auto &m = DN.mat[g][DN.n[g]++];
+    m.codes = put(codes, (size_t)rows * cols / 4);
+    m.scales = put(scales, (size_t)rows * 4);
+    m.rows = rows;
+    DN.rows[g] += rows;
+}
+
+int gpre_dense_done(int maxtok) {
+    if (ctx_ready()) return -1;
+    if (DN.bad) { seterr("gpre_dense_add: a matrix was not 256k x 2048 (or more than 3 per group)"); fprintf(stderr, "maplemoe: %s\n", mmoe_last_error()); return -1; }
+    if (DN.host.empty() || maxtok < 1 || maxtok > 2048 || maxtok > S.main.maxtok) {
+        seterr("gpre_dense_done: nothing added, or maxtok %d outside 1..%d (gpre_init)", maxtok, S.main.maxtok);
+        return -1;
+    }
+    HC(hipMalloc(&DN.dev, DN.host.size()));
+    HC(hipMemcpy(DN.dev, DN.host.data(), DN.host.size(), hipMemcpyHostToDevice));
+    DenseMat hm[DGRP][3] = {};
+    int hr[DGRP][4] = {};
+    DN.ymax = 0;
+    for (int g = 0; g < DGRP; g++) {
+        int yo = 0;
+        for (int k = 0; k < DN.n[g]; k++) {
+            hm[g][k] = DenseMat{DN.dev + DN.mat[g][k].codes, (const float *)(DN.dev + DN.mat[g][k].scales), DN.mat[g][k].rows, yo};
+            hr[g][k + 1] = hr[g][k] + DN.mat[g][k].rows / 256;
+            yo += DN.mat[g][k].rows;
+        }
+        for (int k = DN.n[g] + 1; k < 4; k++) hr[g][k] = hr[g][DN.n[g]];
+        if (yo > DN.ymax) DN.ymax = yo;
+    }
+    HC(hipMalloc(&DN.dmat, sizeof hm)); HC(hipMemcpy(DN.dmat, hm, sizeof hm, hipMemcpyHostToDevice));
+    HC(hipMalloc(&DN.drbs, sizeof hr)); HC(hipMemcpy(DN.drbs, hr, sizeof hr, hipMemcpyHostToDevice));
+    HC(hipMalloc(&DN.y, (size_t)maxtok * DN.ymax * 4));
+    DN.maxtok = maxtok;
+    fprintf(stderr, "maplemoe: attention projections in HBM, %.0f MB\n", DN.host.size() / 1e6);
+    std::vector<uint8_t>().swap(DN.host);
+    DN.ready = 1;
+    return 0;
+}
+
+// y[nb][rows of group g] = group g's matrices times x[nb][2048] (host arrays); returns device seconds
+double gpre_dense(int g, const float *x, int nb, float *y) {
+    if (!DN.ready) { seterr("gpre_dense before gpre_dense_done"); return -1.0; }
+    if (g < 0 || g >= DGRP || !DN.n[g]) { seterr("gpre_dense: group %d has no matrices", g); return -1.0; }
+    if (nb < 1 || nb > DN.maxtok) { seterr("gpre_dense: nb %d outside 1..%d", nb, DN.maxtok); return -1.0; }
+    Work &w = S.main;
+    int ys = DN.rows[g], nrb = ys / 256;
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { seterr("gpre_dense: event"); return -1.0; }
+    (void)hipEventRecord(a, S.st);
+    if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_dense: copy x"); return -1.0; }
+    if (stage_quant_x(w, w.hn, nb)) return -1.0;
+    if (launch(MMOE_K_GATEUP, [&] {
+            k_dense<<<dim3(nrb, (nb + 63) / 64), 256, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, ys, w.qx, w.qsx, w.qsumx, DN.y);
+        })) return -1.0;
+    (void)hipEventRecord(b, S.st);
+    if (hipMemcpyAsync(y, DN.y, (size_t)nb * ys * 4, hipMemcpyDeviceToHost, S.st) != hipSuccess || hipStreamSynchronize(S.st) != hipSuccess) {
+        seterr("gpre_dense: %s", hipGetErrorString(hipGetLastError())); return -1.0;
+    }
+    float ms = 0; (void)hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a); (void)hipEventDestroy(b);
+    DN.t += ms * 1e-3;
+    return ms * 1e-3;
+}
 
 // Output head (gpu_head.m): not part of the MoE path; init failure makes maple.c use its CPU head.
 int gpu_head_init(const uint16_t *w, int rows, int cols) { (void)w; (void)rows; (void)cols; return -1; }

@@ -45,7 +45,7 @@ def _declare(L):
     sig = {
         "gpre_init": (i, [i, i]), "gpre_region": (i, [vp, sz]), "gpre_stage": (i, [sz]),
         "gpre_moe": (d, [vp, i, i, vp, vp, vp, vp, vp, vp, vp, vp]), "gpre_blit_seconds": (d, []),
-        "gpre_dense_done": (i, [i]), "gfull_init": (i, [i, i, i, vp, vp, vp]),
+        "gpre_dense_done": (i, [i]), "gpre_dense_add": (None, [i, vp, vp, i, i]), "gpre_dense": (d, [i, vp, i, vp]), "gfull_init": (i, [i, i, i, vp, vp, vp]),
         "gfull_begin": (None, [vp, i, i]), "gfull_attn": (d, [i, i, vp]),
         "gfull_moe": (None, [i, vp, vp, vp, vp, vp, vp]), "gfull_read": (None, [vp, vp]),
         "gfull_write_x": (None, [vp]), "gfull_maxtok": (i, []), "gfull_report": (None, []),
