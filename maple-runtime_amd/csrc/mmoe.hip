@@ -1,9 +1,9 @@
 // mmoe.hip -- libmaplemoe: the MI355X (gfx950) MoE hot path behind maple.c's GPU entry points.
 //
 // Exports, with maple.c's own C signatures (maple.c:247-272), the entry points maple.c links against when
-// built with -DGPU_HEAD: gpre_* (experts of a prompt chunk), gfull_* (device-resident hidden state), gpux_*
-// (decode experts) and gpu_head_*. Those outside the MoE path return the failure value maple.c already
-// handles by falling back to its CPU code. New mmoe_* entry points run the whole layer on the device:
+// built with -DGPU_HEAD: gpre_* (experts of a prompt chunk and the dense q/k/v/o projections), gfull_*
+// (device-resident hidden state), gpux_* (decode experts) and gpu_head_*. Those outside the built scope (the
+// output head, attention) return the failure value maple.c already handles by falling back to its CPU code. New mmoe_* entry points run the whole layer on the device:
 // router logits, softmax/top-8, grouping, int8 quantisation, gate/up + SiLU, re-quantisation, down and the
 // combine (declared in include/maplemoe.h).
 //
