@@ -267,6 +267,25 @@ def main():
         extra["prefill_128"] = dict(workload="config 0: 128-token chunk, 1 MoE layer, unbiased router",
                                     value=round(T0 / cms * 1e3, 1), unit="tokens/s", ms_per_layer=round(cms, 4))
 
+        # dense q/k/v projections of one layer (gpre_dense, k_dense) on a 2048-token chunk: kernel time only
+        rng = np.random.default_rng(SEED)
+        keep = []
+        for rows in (2048, 512, 512):
+            c = rng.integers(0, 3, (rows, 512, 4), dtype=np.uint8)
+            packed = (c[..., 0] | (c[..., 1] << 2) | (c[..., 2] << 4) | (c[..., 3] << 6)).astype(np.uint8)
+            sc = rng.uniform(0.01, 0.05, rows).astype(np.float32)
+            lib.gpre_dense_add(0, M.ptr(packed), M.ptr(sc), rows, 2048); keep += [packed, sc]
+        if lib.gpre_dense_done(2048) == 0:
+            xq = rng.standard_normal((2048, 2048)).astype(np.float32); yq = np.empty((2048, 3072), np.float32)
+            lib.gpre_dense(0, M.ptr(xq), 2048, M.ptr(yq))
+            dk = prof_pass(lambda: lib.gpre_dense(0, M.ptr(xq), 2048, M.ptr(yq)), 5)
+            kt_ms = dk["gateup"][0] / dk["gateup"][1]
+            dops = 2 * 2048 * 3072 * 2048
+            log(f"dense q/k/v 2048 tokens: k_dense {kt_ms * 1e3:.1f} us, {dops / kt_ms / 1e9:.0f} TOPS")
+            extra["dense_qkv_2048"] = dict(workload="q/k/v projections (3072 x 2048 ternary) of a 2048-token chunk, gpre_dense",
+                                           kernel_us=round(kt_ms * 1e3, 2), tops=round(dops / kt_ms / 1e9, 1),
+                                           frac_int8_peak=round(dops / kt_ms / 1e9 / INT8_PEAK_TOPS, 4))
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_decode(blocks, routers, args.cpu_seconds)

@@ -1313,24 +1313,25 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
 // ---- dense ternary projections (attention q/k/v and o; maple.c jobB_qkv / jobB_o, 459-470, through
 // tdot_multi 423-458): y[b][yoff + r] = (float)(sum_c code * q[b] - qsum[b]) * qs[b] * s[r], K = 2048 ----
 struct DenseMat { const uint8_t *codes; const float *scales; int rows, yoff; };
-// One workgroup = 256 rows (wave w: rows w*64 .. +64 as two 32-row fragments) x 64 tokens, on
+// One workgroup = WAVES x 64 rows (wave w: rows w*64 .. +64 as two 32-row fragments) x 64 tokens, on
 // v_mfma_i32_32x32x32_i8 with gu_chunk's operand mapping (the two row fragments take the places of gate and
 // up). Activations pass through two padded LDS stages, codes 2 chunks ahead in registers, as k_gateup.
-// grid = (sum of rows / 256, ceil(nb / 64)); rbs[m] = first row block of matrix m (rbs[nmat] = total).
-__global__ void __launch_bounds__(256) k_dense(const DenseMat *__restrict__ mats, const int *__restrict__ rbs, int nmat,
+// grid = (sum of rows / (64 WAVES), ceil(nb / 64)); rbs[m] = first row block of matrix m (rbs[nmat] = total).
+template <int WAVES>
+__global__ void __launch_bounds__(WAVES * 64) k_dense(const DenseMat *__restrict__ mats, const int *__restrict__ rbs, int nmat,
                                                int nb, int ys, const int8_t *__restrict__ qx, const float *__restrict__ qsx,
                                                const int *__restrict__ qsumx, float *__restrict__ y) {
-    constexpr int TN = 64, NCH = MH / 256, BB = TN * GU_LROW, NPC = TN * 16 / 256;
+    constexpr int TN = 64, NCH = MH / 256, BB = TN * GU_LROW, NT = WAVES * 64, NPC = TN * 16 / NT, TPP = NT / 16;
     __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
     int rb = blockIdx.x, m = 0;
     while (m + 1 < nmat && rb >= rbs[m + 1]) m++;
     DenseMat M = mats[m];
     int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, G2 = l >> 5, r32 = l & 31;
-    int row0 = (rb - rbs[m]) * 256 + wv * 64, t0 = blockIdx.y * TN, ntok = min(TN, nb - t0);
+    int row0 = (rb - rbs[m]) * (WAVES * 64) + wv * 64, t0 = blockIdx.y * TN, ntok = min(TN, nb - t0);
     int part = tid & 15, bdst = (tid >> 4) * GU_LROW + part * 16;
     uint32_t boff[NPC];
 #pragma unroll
-    for (int k = 0; k < NPC; k++) boff[k] = (uint32_t)(t0 + min((tid >> 4) + 16 * k, ntok - 1)) * MH + part * 16;
+    for (int k = 0; k < NPC; k++) boff[k] = (uint32_t)(t0 + min((tid >> 4) + TPP * k, ntok - 1)) * MH + part * 16;
     const uint8_t *fa = M.codes + (size_t)(row0 + r32) * (MH / 4) + G2 * 32, *fb = fa + (size_t)32 * (MH / 4);
     v16i acc[2][2];
 #pragma unroll
@@ -1351,7 +1352,7 @@ __global__ void __launch_bounds__(256) k_dense(const DenseMat *__restrict__ mats
 #pragma unroll
         for (int k = 0; k < NPC; k++) br[c][k] = *(const gptr_u4 *)(qx + boff[k] + c * 256);
 #pragma unroll
-    for (int k = 0; k < NPC; k++) *(v4i *)(&bs[0][bdst + k * 16 * GU_LROW]) = br[0][k];
+    for (int k = 0; k < NPC; k++) *(v4i *)(&bs[0][bdst + k * TPP * GU_LROW]) = br[0][k];
 #pragma unroll
     for (int ch = 0; ch < NCH; ch++) {
         __syncthreads();
@@ -1364,7 +1365,7 @@ __global__ void __launch_bounds__(256) k_dense(const DenseMat *__restrict__ mats
         __builtin_amdgcn_sched_barrier(0);
         if (ch + 1 < NCH) {
 #pragma unroll
-            for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst + k * 16 * GU_LROW]) = br[(ch + 1) % 2][k];
+            for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst + k * TPP * GU_LROW]) = br[(ch + 1) % 2][k];
         }
     }
 #undef DN2_LOADC

@@ -424,6 +424,9 @@ double gpre_blit_seconds(void) { return S.t_region; }
 // integer and fp32 sequence (tdot_multi), so y equals maple.c's CPU projections (jobB_qkv / jobB_o) bit for
 // bit (the Metal version multiplies fp32 activations instead).
 #define DGRP 48
+#ifndef DENSE_W
+#define DENSE_W 2   // k_dense waves per workgroup (64 rows each)
+#endif
 static struct {
     std::vector<uint8_t> host;                   // staging until gpre_dense_done
     struct Mat { size_t codes, scales; int rows; } mat[DGRP][3];
@@ -471,7 +474,7 @@ int gpre_dense_done(int maxtok) {
         int yo = 0;
         for (int k = 0; k < DN.n[g]; k++) {
             hm[g][k] = DenseMat{DN.dev + DN.mat[g][k].codes, (const float *)(DN.dev + DN.mat[g][k].scales), DN.mat[g][k].rows, yo};
-            hr[g][k + 1] = hr[g][k] + DN.mat[g][k].rows / 256;
+            hr[g][k + 1] = hr[g][k] + DN.mat[g][k].rows / (64 * DENSE_W);
             yo += DN.mat[g][k].rows;
         }
         for (int k = DN.n[g] + 1; k < 4; k++) hr[g][k] = hr[g][DN.n[g]];
@@ -493,14 +496,14 @@ double gpre_dense(int g, const float *x, int nb, float *y) {
     if (g < 0 || g >= DGRP || !DN.n[g]) { seterr("gpre_dense: group %d has no matrices", g); return -1.0; }
     if (nb < 1 || nb > DN.maxtok) { seterr("gpre_dense: nb %d outside 1..%d", nb, DN.maxtok); return -1.0; }
     Work &w = S.main;
-    int ys = DN.rows[g], nrb = ys / 256;
+    int ys = DN.rows[g], nrb = ys / (64 * DENSE_W);
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { seterr("gpre_dense: event"); return -1.0; }
     (void)hipEventRecord(a, S.st);
     if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_dense: copy x"); return -1.0; }
     if (stage_quant_x(w, w.hn, nb)) return -1.0;
     if (launch(MMOE_K_GATEUP, [&] {
-            k_dense<<<dim3(nrb, (nb + 63) / 64), 256, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, ys, w.qx, w.qsx, w.qsumx, DN.y);
+            k_dense<DENSE_W><<<dim3(nrb, (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, ys, w.qx, w.qsx, w.qsumx, DN.y);
         })) return -1.0;
     (void)hipEventRecord(b, S.st);
     if (hipMemcpyAsync(y, DN.y, (size_t)nb * ys * 4, hipMemcpyDeviceToHost, S.st) != hipSuccess || hipStreamSynchronize(S.st) != hipSuccess) {
