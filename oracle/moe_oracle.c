@@ -337,3 +337,126 @@ void mo_experts_grouped(const float *hn, int nb, int nu, const mo_expert *ex, co
         }
     free(D);
 }
+
+/* ---------------------------------------------------------------- attention half (maple.c:706-724) */
+/* maple.c:403-411. Its build (-O3 -ffast-math -mfma) contracts each line into one FMA whose addend is the
+ * rounded second product: t[i] = fma(v[i], c, -(v[i+32] s)), t[i+32] = fma(v[i+32], c, v[i] s) (the form
+ * that matches the compiled maple.c bit for bit; tests/test_oracle_attn.py). */
+void mo_rope(float *v, const float *cs) {
+    float t[MO_ROT];
+    for (int i = 0; i < MO_ROT / 2; i++) {
+        float c = cs[2 * i], s = cs[2 * i + 1], a = v[i], w = v[i + MO_ROT / 2];
+        t[i] = fmaf(a, c, -(w * s));
+        t[i + MO_ROT / 2] = fmaf(w, c, a * s);
+    }
+    memcpy(v, t, sizeof t);
+}
+
+/* maple.c:314-320: IEEE binary16, round to nearest even */
+static uint16_t f2h(float f) {
+    union { float f; uint32_t u; } c = {f};
+    uint32_t sign = (c.u >> 16) & 0x8000u, a = c.u & 0x7fffffffu;
+    if (a >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (a > 0x7f800000u ? 0x200u : 0));   /* inf / nan */
+    if (a >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);                /* rounds past 65504 */
+    if (a < 0x38800000u) {                                                  /* subnormal half (or zero) */
+        if (a < 0x33000000u) return (uint16_t)sign;                         /* below half the smallest */
+        uint32_t m = (a & 0x7fffffu) | 0x800000u; int e = (int)(a >> 23);  /* value = m * 2^(e - 150) */
+        int sh = 126 - e;                                                   /* half units of 2^-24: m >> (sh) */
+        uint32_t q = m >> sh, rem = m & ((1u << sh) - 1), half = 1u << (sh - 1);
+        if (rem > half || (rem == half && (q & 1))) q++;
+        return (uint16_t)(sign | q);
+    }
+    uint32_t h = ((a >> 13) - ((127 - 15) << 10)), rem = a & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1))) h++;
+    return (uint16_t)(sign | h);
+}
+void mo_f16(const float *s, uint16_t *d, int n) { for (int i = 0; i < n; i++) d[i] = f2h(s[i]); }
+float mo_h2f(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000u) << 16, e = (h >> 10) & 31, m = h & 0x3ffu;
+    union { uint32_t u; float f; } c;
+    if (e == 31) c.u = sign | 0x7f800000u | (m << 13);
+    else if (e) c.u = sign | ((e + 112) << 23) | (m << 13);
+    else { c.f = (float)m * (1.0f / 16777216.0f); c.u |= sign; }
+    return c.f;
+}
+
+/* maple.c:516-558 */
+void mo_attend(const float *q, const uint16_t *kc, const uint16_t *vc, int kvh, int pos, int glob, int win,
+               float *out, float *sc) {
+    int lo = glob ? 0 : (pos - win > 0 ? pos - win : 0), T = pos - lo + 1;
+    const float scale = 1.0f / sqrtf((float)MO_HD);
+    float mx[4], inv[4];
+    for (int j = 0; j < 4; j++) { mx[j] = -1e30f; memset(out + j * MO_HD, 0, MO_HD * sizeof(float)); }
+    for (int t = 0; t < T; t++) {
+        const uint16_t *kk = kc + (size_t)(lo + t) * 512 + kvh * MO_HD;
+        float kf[MO_HD];
+        for (int d = 0; d < MO_HD; d++) kf[d] = mo_h2f(kk[d]);
+        for (int j = 0; j < 4; j++) {
+            float a[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            for (int d = 0; d < MO_HD; d += 8)
+                for (int l = 0; l < 8; l++) a[l] = fmaf(kf[d + l], q[j * MO_HD + d + l], a[l]);
+            float s = hsum8(a) * scale;
+            sc[j * T + t] = s;
+            if (s > mx[j]) mx[j] = s;
+        }
+    }
+    for (int j = 0; j < 4; j++) {
+        float sum = 0, *sj = sc + j * T;
+        for (int t = 0; t < T; t++) { sj[t] = mo_exp(sj[t] - mx[j]); sum += sj[t]; }
+        inv[j] = 1.0f / sum;
+    }
+    for (int t = 0; t < T; t++) {
+        const uint16_t *vv = vc + (size_t)(lo + t) * 512 + kvh * MO_HD;
+        for (int j = 0; j < 4; j++) {
+            float w = sc[j * T + t] * inv[j];
+            for (int d = 0; d < MO_HD; d++) out[j * MO_HD + d] = fmaf(w, mo_h2f(vv[d]), out[j * MO_HD + d]);
+        }
+    }
+}
+
+/* maple.c:706-724 (CPU path), one sequence */
+void mo_attn_chunk(float *x, int nb, int pos0, int glob, int win, const uint16_t *in_ln, const uint16_t *q_norm,
+                   const uint16_t *k_norm, mo_t2 wq, mo_t2 wk, mo_t2 wv, mo_t2 wo, const float *cs,
+                   uint16_t *kc, uint16_t *vc, uint16_t *ko, float *att) {
+    float *hn = malloc(sizeof(float) * MO_H), *qkv = malloc(sizeof(float) * (size_t)nb * 3072);
+    float *at = malloc(sizeof(float) * (size_t)nb * MO_H), *sc = malloc(sizeof(float) * 4 * (size_t)(pos0 + nb));
+    int8_t *q8 = malloc(MO_H);
+    for (int b = 0; b < nb; b++) {
+        float qs; int32_t qsum;
+        mo_rmsnorm(x + (size_t)b * MO_H, in_ln, MO_H, hn);
+        qs = mo_prep(hn, MO_H, q8, &qsum);
+        float *o = qkv + (size_t)b * 3072;
+        for (int r = 0; r < 2048; r++) o[r] = mo_tdot(wq.p + (size_t)r * (wq.cols / 4), wq.s[r], q8, qs, qsum, wq.cols);
+        for (int r = 0; r < 512; r++) o[2048 + r] = mo_tdot(wk.p + (size_t)r * (wk.cols / 4), wk.s[r], q8, qs, qsum, wk.cols);
+        for (int r = 0; r < 512; r++) o[2560 + r] = mo_tdot(wv.p + (size_t)r * (wv.cols / 4), wv.s[r], q8, qs, qsum, wv.cols);
+    }
+    for (int b = 0; b < nb; b++) {
+        int pos = pos0 + b;
+        float *o = qkv + (size_t)b * 3072;
+        for (int h = 0; h < MO_NH; h++) {
+            mo_rmsnorm(o + h * MO_HD, q_norm, MO_HD, o + h * MO_HD);
+            if (!glob) mo_rope(o + h * MO_HD, cs + (size_t)pos * MO_ROT);
+        }
+        for (int h = 0; h < MO_NKV; h++) {
+            mo_rmsnorm(o + 2048 + h * MO_HD, k_norm, MO_HD, o + 2048 + h * MO_HD);
+            if (!glob) mo_rope(o + 2048 + h * MO_HD, cs + (size_t)pos * MO_ROT);
+        }
+        mo_f16(o + 2048, kc + (size_t)pos * 512, 512);
+        mo_f16(o + 2560, vc + (size_t)pos * 512, 512);
+        if (ko) { memcpy(ko + (size_t)b * 1024, kc + (size_t)pos * 512, 1024); memcpy(ko + (size_t)b * 1024 + 512, vc + (size_t)pos * 512, 1024); }
+    }
+    for (int b = 0; b < nb; b++)
+        for (int kvh = 0; kvh < MO_NKV; kvh++)
+            mo_attend(qkv + (size_t)b * 3072 + kvh * 4 * MO_HD, kc, vc, kvh, pos0 + b, glob, win,
+                      at + (size_t)b * MO_H + kvh * 4 * MO_HD, sc);
+    for (int b = 0; b < nb; b++) {
+        float qs; int32_t qsum;
+        qs = mo_prep(at + (size_t)b * MO_H, MO_H, q8, &qsum);
+        for (int r = 0; r < MO_H; r++) {
+            float y = mo_tdot(wo.p + (size_t)r * (wo.cols / 4), wo.s[r], q8, qs, qsum, wo.cols);
+            x[(size_t)b * MO_H + r] = x[(size_t)b * MO_H + r] + y;
+        }
+    }
+    if (att) memcpy(att, at, sizeof(float) * (size_t)nb * MO_H);
+    free(hn); free(qkv); free(at); free(sc); free(q8);
+}

@@ -130,6 +130,37 @@ void mo_moe_step(const float *hn, const uint16_t *router, const float *bias, con
 void mo_experts_grouped(const float *hn, int nb, int nu, const mo_expert *ex, const int32_t *ustart,
                         const int32_t *utok, const float *uw, const int32_t *tp, float *y, mo_trace *tr);
 
+/* ---- attention half of a layer (maple.c step_batch CPU path, 706-724) ----
+ * Pinning: mo_rope / mo_f16 bit-exact against maple.c's rope / to_f16 (oracle/_ref); mo_attend and
+ * mo_attn_chunk within 1e-6 of maple.c's attend_group / step_batch (its -ffast-math build vectorises the
+ * softmax loop with libmvec's expf; this restatement fixes one order, with mo_exp). */
+#define MO_NH 16
+#define MO_NKV 4
+#define MO_HD 128
+#define MO_ROT 64
+typedef struct { const uint8_t *p; const float *s; int rows, cols; } mo_t2;   /* maple.c:36 T2 */
+/* maple.c:403-411 rope on the first 64 dims of a head, pairs (i, i+32), as its FMA-contracted build computes
+ * it; cs = the position's 32 (cos, sin) pairs as maple.c:1151-1152 tabulates them ((float)cos / sin of
+ * pos * INV_FREQ[i] in double) */
+void mo_rope(float *v, const float *cs);
+/* maple.c:314-320 to_f16: fp32 -> fp16 with round to nearest even (F16C rounding mode 0); and back (exact) */
+void mo_f16(const float *s, uint16_t *d, int n);
+float mo_h2f(uint16_t h);
+/* maple.c:516-558 attend_group (AVX2 path): the 4 query heads q[4][128] of key/value head kvh attend over
+ * positions lo..pos (lo = 0 on global layers, max(0, pos - win) else) of the fp16 cache kc/vc [pos][512]:
+ * score = hsum of 8 FMA lanes (lane l: dims l, l+8, ...) times 1/sqrtf(128); p = mo_exp(score - max); the
+ * sum over positions in order; out[j][d] = FMA chain over positions of (p * (1/sum)) * v. sc: 4 x (pos+1) */
+void mo_attend(const float *q, const uint16_t *kc, const uint16_t *vc, int kvh, int pos, int glob, int win,
+               float *out, float *sc);
+/* maple.c:706-724 for one sequence: x[nb][2048] of positions pos0 .. pos0+nb-1 -> hn = rmsnorm(x, in_ln),
+ * prep, q/k/v = tdot rows (wq 2048, wk 512, wv 512 rows); per token q/k heads rmsnorm (q_norm, k_norm, 128)
+ * then rope (local layers, glob == 0); k, v to fp16 into the layer's cache kc/vc [pos][512] and ko[b][1024]
+ * (k | v, may be NULL); attention per (token, kv head); prep of the attention output, o = tdot rows of wo;
+ * x += o. cs: the rope table [pos][32][2]. att (may be NULL) receives the attention output [nb][2048]. */
+void mo_attn_chunk(float *x, int nb, int pos0, int glob, int win, const uint16_t *in_ln, const uint16_t *q_norm,
+                   const uint16_t *k_norm, mo_t2 wq, mo_t2 wk, mo_t2 wv, mo_t2 wo, const float *cs,
+                   uint16_t *kc, uint16_t *vc, uint16_t *ko, float *att);
+
 #ifdef __cplusplus
 }
 #endif

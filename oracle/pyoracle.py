@@ -20,6 +20,11 @@ class Expert(C.Structure):
                 ("dc", C.c_void_p), ("ds", C.c_void_p)]
 
 
+class T2(C.Structure):
+    """maple.c:36 T2 / mo_t2: packed codes, row scales, rows, cols"""
+    _fields_ = [("p", C.c_void_p), ("s", C.c_void_p), ("rows", C.c_int), ("cols", C.c_int)]
+
+
 class Trace(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in ("rl", "top", "tw", "nu", "ue", "ustart", "utok", "uw", "tp", "qx", "qsx",
                                            "qsumx", "gu_i32", "gate", "up", "act", "qa", "qsa", "qsuma", "dn_i32", "down")]
@@ -45,7 +50,10 @@ def oracle():
                         ("mo_unpack", None, [vp, i, i, vp]),
                         ("mo_moe_batch", None, [vp, i, vp, vp, vp, vp, vp, vp]),
                         ("mo_moe_step", None, [vp, vp, vp, vp, vp, vp]),
-                        ("mo_experts_grouped", None, [vp, i, i, vp, vp, vp, vp, vp, vp, vp])]:
+                        ("mo_experts_grouped", None, [vp, i, i, vp, vp, vp, vp, vp, vp, vp]),
+                        ("mo_rope", None, [vp, vp]), ("mo_f16", None, [vp, vp, i]), ("mo_h2f", C.c_float, [C.c_uint16]),
+                        ("mo_attend", None, [vp, vp, vp, i, i, i, i, vp, vp]),
+                        ("mo_attn_chunk", None, [vp, i, i, i, i, vp, vp, vp, T2, T2, T2, T2, vp, vp, vp, vp, vp])]:
             f = getattr(_or, n)
             f.restype, f.argtypes = r, a
     return _or
@@ -71,7 +79,10 @@ def ref():
                         ("ref_topk", None, [vp, i, vp, vp]), ("ref_group", i, [vp, vp, i, vp, vp, vp, vp, vp, vp]),
                         ("ref_rmsnorm", None, [vp, vp, i, vp]), ("ref_act", None, [vp, vp, vp, i]),
                         ("ref_moe_batch", None, [i, vp, i, vp] + [vp] * 14),
-                        ("ref_moe_step", None, [i, vp, vp, vp, vp, vp, vp, vp]), ("ref_now", C.c_double, [])]:
+                        ("ref_moe_step", None, [i, vp, vp, vp, vp, vp, vp, vp]), ("ref_now", C.c_double, []),
+                        ("ref_ctx", i, []), ("ref_rope", None, [vp, i]), ("ref_f16", None, [vp, vp, i]),
+                        ("ref_cs", None, [i, vp]), ("ref_set_attn", None, [i] + [vp] * 11),
+                        ("ref_cache", None, [i, i, vp, vp, i]), ("ref_attn_chunk", None, [i, i, vp, i, i, vp])]:
             f = getattr(_ref, n)
             f.restype, f.argtypes = r, a
     return _ref
@@ -152,3 +163,48 @@ def moe_step(hn, router, experts, x, bias=None):
     tr, arrs = new_trace(1, TOPK)
     oracle().mo_moe_step(_p(hn), _p(router), _p(bias), C.cast(experts, C.c_void_p), _p(x), C.byref(tr))
     return arrs
+
+
+# ------------------------------------------------------------------ attention half (maple.c:706-724)
+WIN = 512
+
+
+def rope_table(npos):
+    """maple.c:1151-1152: (cos, sin) of pos * INV_FREQ[i] in double, stored as fp32; INV_FREQ (maple.c:1085)"""
+    inv = 1.0 / np.power(10000.0, (2.0 * np.arange(32)) / 64)
+    f = np.arange(npos, dtype=np.float64)[:, None] * inv[None, :]
+    cs = np.empty((npos, 32, 2), np.float32)
+    cs[..., 0] = np.cos(f).astype(np.float32); cs[..., 1] = np.sin(f).astype(np.float32)
+    return cs
+
+
+class AttnLayer:
+    """Attention tensors of one layer in the reference layout (maple.c:38 Layer: in_ln, q_norm, k_norm bf16;
+    q 2048x2048, k and v 512x2048, o 2048x2048 ternary with fp32 row scales), seeded."""
+
+    def __init__(self, seed):
+        rng = np.random.default_rng(seed)
+        bf = lambda a: (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+        self.in_ln = bf(rng.uniform(0.5, 1.5, H)); self.q_norm = bf(rng.uniform(0.5, 1.5, 128))
+        self.k_norm = bf(rng.uniform(0.5, 1.5, 128))
+        self.mats = {}
+        for name, rows in (("q", 2048), ("k", 512), ("v", 512), ("o", 2048)):
+            c = rng.choice(np.array([0, 1, 2], np.uint8), size=(rows, H), p=[0.3, 0.4, 0.3])
+            packed = np.empty((rows, H // 4), np.uint8)
+            oracle().mo_pack(_p(np.ascontiguousarray(c)), rows, H, _p(packed))
+            self.mats[name] = (packed, rng.uniform(0.01, 0.05, rows).astype(np.float32))
+
+    def t2(self, name):
+        packed, s = self.mats[name]
+        return T2(packed.ctypes.data, s.ctypes.data, packed.shape[0], H)
+
+
+def attn_chunk(layer, x, pos0, glob, kc, vc, cs, win=WIN):
+    """mo_attn_chunk: x [nb][2048] updated in a copy; kc/vc [ctx][512] fp16 updated in place; returns
+    (x, ko [nb][1024], att [nb][2048])"""
+    x = np.ascontiguousarray(x, np.float32).copy(); nb = x.shape[0]
+    ko = np.zeros((nb, 1024), np.uint16); att = np.zeros((nb, H), np.float32)
+    oracle().mo_attn_chunk(_p(x), nb, pos0, glob, win, _p(layer.in_ln), _p(layer.q_norm), _p(layer.k_norm),
+                           layer.t2("q"), layer.t2("k"), layer.t2("v"), layer.t2("o"), _p(cs), _p(kc), _p(vc),
+                           _p(ko), _p(att))
+    return x, ko, att

@@ -219,3 +219,76 @@ void ref_moe_step(int L, const float *hn, float *x, float *rl_out, int32_t *top_
 
 /* Wall-clock helper for the CPU baseline (maple.c:47) */
 double ref_now(void) { return now(); }
+
+/* ---- attention half (maple.c:706-724), for pinning the oracle's mo_rope / mo_f16 / mo_attn_chunk ----
+ * maple.c's main() sets INV_FREQ (maple.c:1085) and allocates the fp16 caches and the score rows
+ * (maple.c:1088-1090); these entry points do the same once, with a context of REF_CTX positions. */
+#define REF_CTX 1024
+static int REF_ATT_READY;
+static void ref_att_init(void) {
+    if (REF_ATT_READY) return;
+    for (int i = 0; i < ROT / 2; i++) INV_FREQ[i] = 1.0 / pow(10000.0, (2.0 * i) / ROT);   /* maple.c:1085 */
+    CTX = REF_CTX;
+    KC = calloc((size_t)NL * CTX * NKV * HD, sizeof(uint16_t));
+    VC = calloc((size_t)NL * CTX * NKV * HD, sizeof(uint16_t));
+    SCR = malloc(sizeof(float) * (size_t)BMAX * NH * CTX);
+    REF_ATT_READY = 1;
+}
+int ref_ctx(void) { return REF_CTX; }
+/* maple.c:403-411 */
+void ref_rope(float *v, int pos) { FAST_ENTER; ref_att_init(); rope(v, pos); FAST_LEAVE; }
+/* maple.c:314-320 */
+void ref_f16(const float *s, uint16_t *d, int n) { FAST_ENTER; to_f16(d, s, n); FAST_LEAVE; }
+/* maple.c:1151-1152: the (cos, sin) table gfull_init receives, npos positions x 32 pairs */
+void ref_cs(int npos, float *cs) {
+    FAST_ENTER; ref_att_init();
+    for (int pos = 0; pos < npos; pos++) for (int i = 0; i < ROT / 2; i++) {
+        double f = pos * INV_FREQ[i]; cs[(pos * 32 + i) * 2] = (float)cos(f); cs[(pos * 32 + i) * 2 + 1] = (float)sin(f);
+    }
+    FAST_LEAVE;
+}
+/* Layer L's attention tensors (maple.c:71-77 does this from layout.bin) */
+void ref_set_attn(int L, const uint16_t *in_ln, const uint16_t *q_norm, const uint16_t *k_norm,
+                  const uint8_t *qc, const float *qs, const uint8_t *kc, const float *ks, const uint8_t *vc, const float *vs,
+                  const uint8_t *oc, const float *os) {
+    FAST_ENTER;
+    Layer *l = &LY[L];
+    l->in_ln = (BF){in_ln, 1, H}; l->q_norm = (BF){q_norm, 1, HD}; l->k_norm = (BF){k_norm, 1, HD};
+    l->q = (T2){qc, qs, NH * HD, H}; l->k = (T2){kc, ks, NKV * HD, H}; l->v = (T2){vc, vs, NKV * HD, H};
+    l->o = (T2){oc, os, H, NH * HD};
+    FAST_LEAVE;
+}
+/* Layer L's cache of sequence 0 (maple.c KC/VC at KOFF(0, L, .)): set positions 0..npos-1, or read them */
+void ref_cache(int L, int npos, uint16_t *kc, uint16_t *vc, int set) {
+    FAST_ENTER; ref_att_init();
+    size_t n = (size_t)npos * NKV * HD * 2;
+    if (set) { memcpy(KC + KOFF(0, L, 0), kc, n); memcpy(VC + KOFF(0, L, 0), vc, n); }
+    else { memcpy(kc, KC + KOFF(0, L, 0), n); memcpy(vc, VC + KOFF(0, L, 0), n); }
+    FAST_LEAVE;
+}
+/* The attention half of step_batch (maple.c:706-724, the CPU path) for nb tokens of sequence 0 at positions
+ * pos0..: statements restated, every function maple.c's own. x[nb][2048] is updated in place; att (may be
+ * NULL) receives maple.c's attention output ATTB. */
+void ref_attn_chunk(int L, int glob, float *x, int nb, int pos0, float *att) {
+    FAST_ENTER; ref_att_init();
+    BN = nb; BL = &LY[L];
+    for (int b = 0; b < nb; b++) memcpy(XB[b], x + (size_t)b * H, H * sizeof(float));
+    for (int b = 0; b < nb; b++) { rmsnorm(HNB[b], XB[b], &BL->in_ln, H); prep(&VHB[b], HNB[b], H); }
+    run(jobB_qkv, NULL, NH * HD + 2 * NKV * HD);
+    for (int b = 0; b < nb; b++) {
+        int pos = pos0 + b;
+        for (int h = 0; h < NH; h++) { rmsnorm(QB[b] + h * HD, QB[b] + h * HD, &BL->q_norm, HD); if (!glob) rope(QB[b] + h * HD, pos); }
+        for (int h = 0; h < NKV; h++) { rmsnorm(KB_[b] + h * HD, KB_[b] + h * HD, &BL->k_norm, HD); if (!glob) rope(KB_[b] + h * HD, pos); }
+        to_f16(KC + KOFF(0, L, pos), KB_[b], NKV * HD);
+        to_f16(VC + KOFF(0, L, pos), VB_[b], NKV * HD);
+        ASEQ[b] = 0; APOS[b] = pos;
+    }
+    AL = L; AGLOB = glob;
+    run(jobB_att, NULL, nb * NKV);
+    for (int b = 0; b < nb; b++) prep(&VATTB[b], ATTB[b], H);
+    run(jobB_o, NULL, H);
+    for (int b = 0; b < nb; b++) for (int i = 0; i < H; i++) XB[b][i] += YB[b][i];
+    for (int b = 0; b < nb; b++) memcpy(x + (size_t)b * H, XB[b], H * sizeof(float));
+    if (att) for (int b = 0; b < nb; b++) memcpy(att + (size_t)b * H, ATTB[b], H * sizeof(float));
+    FAST_LEAVE;
+}
