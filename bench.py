@@ -114,6 +114,83 @@ def cpu_baseline_decode(blocks, routers, seconds):
                        f"-O3 -ffast-math -mavx2 -mfma -mf16c, {nt} threads of run()), same synthetic weights")
 
 
+
+def valid_ternary_bytes():
+    """the 81 byte values whose four 2-bit fields are all codes 0..2 (w = -1, 0, +1)"""
+    v = np.arange(256)
+    ok = ((v & 3) < 3) & (((v >> 2) & 3) < 3) & (((v >> 4) & 3) < 3) & ((v >> 6) < 3)
+    return v[ok].astype(np.uint8)
+
+
+def rope_table(npos):
+    """maple.c:1151-1152: (cos, sin) of pos * 10000^(-2i/64), i < 32, computed in double, stored as fp32"""
+    f = np.arange(npos, dtype=np.float64)[:, None] * (1.0 / np.power(10000.0, 2.0 * np.arange(32) / 64))[None, :]
+    return np.ascontiguousarray(np.stack([np.cos(f), np.sin(f)], -1).astype(np.float32))
+
+
+def full_prefill(lib, rids, args):
+    T, CTX = 2048, 4096
+    rng = np.random.default_rng(SEED + 4)
+    vb = valid_ternary_bytes()
+    keep = []
+    M.check(lib.mmoe_dense_reset(), "dense reset")
+    for L in range(NL):
+        for g, rows_list in ((2 * L, (2048, 512, 512)), (2 * L + 1, (2048,))):
+            for rows in rows_list:
+                packed = rng.choice(vb, size=(rows, 512))
+                sc = rng.uniform(0.01, 0.05, rows).astype(np.float32)
+                lib.gpre_dense_add(g, M.ptr(packed), M.ptr(sc), rows, 2048); keep += [packed, sc]
+    if lib.gpre_dense_done(T) != 0:
+        log("gpre_dense_done:", lib.mmoe_last_error().decode()); return None, None
+    del keep
+    # dense q/k/v projections of layer 0 alone (gpre_dense, k_dense): kernel time only
+    xq = rng.standard_normal((T, 2048)).astype(np.float32); yq = np.empty((T, 3072), np.float32)
+    lib.gpre_dense(0, M.ptr(xq), T, M.ptr(yq))
+    dk = prof_pass(lambda: lib.gpre_dense(0, M.ptr(xq), T, M.ptr(yq)), 5)
+    kt_ms = dk["dense"][0] / dk["dense"][1]
+    dops = 2 * T * 3072 * 2048
+    log(f"dense q/k/v 2048 tokens: k_dense {kt_ms * 1e3:.1f} us, {dops / kt_ms / 1e9:.0f} TOPS")
+    dense = dict(workload="q/k/v projections (3072 x 2048 ternary) of a 2048-token chunk, gpre_dense",
+                 kernel_us=round(kt_ms * 1e3, 2), tops=round(dops / kt_ms / 1e9, 1),
+                 frac_int8_peak=round(dops / kt_ms / 1e9 / INT8_PEAK_TOPS, 4))
+    bf = lambda a: (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    norms = np.empty((NL, 4352), np.float32)
+    routers = np.empty((NL, 256, 2048), np.uint16)
+    zb = M.zipf_bias(SEED, 1.1)
+    for L in range(NL):
+        w = bf(rng.uniform(0.5, 1.5, 4352))
+        norms[L] = (w.astype(np.uint32) << 16).view(np.float32)
+        routers[L] = M.synth_router(SEED, L, dist=0)
+    M.check(lib.gfull_init(CTX, T, 512, M.ptr(norms), M.ptr(routers), M.ptr(rope_table(CTX))), "gfull_init")
+    loc = M.block_loc()
+    for L in range(NL):   # expert tables (the layer blocks of the decode run), router and post-norm as above
+        regs = np.array([rids[L], -1, -1, -1], np.int32)
+        M.check(lib.mmoe_set_layer(L, M.ptr(loc), M.ptr(regs), M.ptr(routers[L]), M.ptr(bf(norms[L, 2048:4096]))), "set_layer")
+        M.check(lib.mmoe_set_bias(L, M.ptr(zb)), "bias")
+    x = M.synth_hidden(SEED, 5, T)
+    out = dict(workload="config 4: 2048-token chunk x 24 whole layers (attention 16q/4kv x 128, q/k norms, rope, "
+                        "fp16 cache; MoE with Zipf(1.1) bias), mmoe_gfull_stack",
+               unit="tokens/s")
+    for pos0 in (0, 2048):
+        lib.gfull_begin(M.ptr(x), T, pos0)   # the chunk's hidden state in HBM; each step runs it through 24 layers
+
+        def fstep():
+            M.check(lib.mmoe_gfull_stack(0, NL), "gfull_stack")
+        fms, _ = timed(fstep, 3, 1)
+        fk = prof_pass(fstep, 1)
+        att = sum(v[0] for k, v in fk.items() if k in ("dense", "qkn", "att_scores", "att_softmax", "att_pv"))
+        tot = sum(v[0] for v in fk.values())
+        log(f"full prefill 2048 at pos0 {pos0}: {fms:.2f} ms / 24 layers, {T / fms * 1e3:.0f} tok/s; "
+            f"kernel time attention half {att:.2f} ms, MoE {tot - att:.2f} ms")
+        for k, (tt, n) in sorted(fk.items(), key=lambda kv: -kv[1][0]):
+            log(f"  {k:12s} {tt / n * 1e3:8.2f} us avg x {n}")
+        key = "first_chunk" if pos0 == 0 else "second_chunk"
+        out[key] = dict(pos0=pos0, value=round(T / fms * 1e3, 1), ms_per_chunk=round(fms, 3),
+                        attention_ms=round(att, 3), moe_ms=round(tot - att, 3),
+                        kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in fk.items()})
+    lib.gfull_read(None, None)
+    return out, dense
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -122,6 +199,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-full", action="store_true", help="skip config 4 (24 whole layers with attention)")
     ap.add_argument("--graph", type=int, default=1, help="replay the 24-layer decode as a HIP graph")
     ap.add_argument("--router", choices=["exact", "mfma"], default="exact",
                     help="router of the 2048-token prefill: fp32 FMA chains for every logit, or bf16 MFMA logits "
@@ -267,24 +345,15 @@ def main():
         extra["prefill_128"] = dict(workload="config 0: 128-token chunk, 1 MoE layer, unbiased router",
                                     value=round(T0 / cms * 1e3, 1), unit="tokens/s", ms_per_layer=round(cms, 4))
 
-        # dense q/k/v projections of one layer (gpre_dense, k_dense) on a 2048-token chunk: kernel time only
-        rng = np.random.default_rng(SEED)
-        keep = []
-        for rows in (2048, 512, 512):
-            c = rng.integers(0, 3, (rows, 512, 4), dtype=np.uint8)
-            packed = (c[..., 0] | (c[..., 1] << 2) | (c[..., 2] << 4) | (c[..., 3] << 6)).astype(np.uint8)
-            sc = rng.uniform(0.01, 0.05, rows).astype(np.float32)
-            lib.gpre_dense_add(0, M.ptr(packed), M.ptr(sc), rows, 2048); keep += [packed, sc]
-        if lib.gpre_dense_done(2048) == 0:
-            xq = rng.standard_normal((2048, 2048)).astype(np.float32); yq = np.empty((2048, 3072), np.float32)
-            lib.gpre_dense(0, M.ptr(xq), 2048, M.ptr(yq))
-            dk = prof_pass(lambda: lib.gpre_dense(0, M.ptr(xq), 2048, M.ptr(yq)), 5)
-            kt_ms = dk["gateup"][0] / dk["gateup"][1]
-            dops = 2 * 2048 * 3072 * 2048
-            log(f"dense q/k/v 2048 tokens: k_dense {kt_ms * 1e3:.1f} us, {dops / kt_ms / 1e9:.0f} TOPS")
-            extra["dense_qkv_2048"] = dict(workload="q/k/v projections (3072 x 2048 ternary) of a 2048-token chunk, gpre_dense",
-                                           kernel_us=round(kt_ms * 1e3, 2), tops=round(dops / kt_ms / 1e9, 1),
-                                           frac_int8_peak=round(dops / kt_ms / 1e9 / INT8_PEAK_TOPS, 4))
+    # ---- config 4: a 2048-token chunk through 24 whole layers (attention + MoE) on the card, positions 0..2047
+    # and 2048..4095 of a 4096-position key/value cache (mmoe_gfull_stack); the dense q/k/v/o projections of all
+    # 24 layers (random ternary, per-row fp32 scales) sit in HBM beside the experts
+    if not args.no_prefill and not args.no_full:
+        full, dense = full_prefill(lib, rids, args)
+        if full:
+            extra["full_prefill_2048"] = full
+        if dense:
+            extra["dense_qkv_2048"] = dense
 
     cpu = None
     if not args.no_cpu:

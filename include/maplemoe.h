@@ -71,13 +71,21 @@ void gpre_dense_add(int g, const uint8_t *codes, const float *scales, int rows, 
 int gpre_dense_done(int maxtok);
 double gpre_dense(int g, const float *x, int nb, float *y);
 double gpre_blit_seconds(void);
+/* Drops the dense projections from HBM so gpre_dense_add can stage a new set (no counterpart in maple.c,
+ * which loads them once per run; for callers and tests that load several models in one process). */
+int mmoe_dense_reset(void);
 
-/* Whole layer on the card, replaces gpu_pre.m:387-594 (declared maple.c:265-272). Attention is not part of
- * this build: gfull_init returns -1 and gfull_attn -1.0, so maple.c uses gpre_moe (maple.c:1156-1158).
- * gfull_begin / gfull_moe / gfull_read / gfull_write_x / gfull_maxtok / gfull_report keep their meaning
- * on a device hidden state prepared with mmoe_gfull_setup and mmoe_gfull_post_norm (below): gfull_moe is
- * asynchronous and adds each token's weighted expert outputs into that state; gfull_read waits and copies
- * it back (*ko is set to NULL: no K/V cache here). */
+/* Whole layers on the card, replaces gpu_pre.m:387-594 (declared maple.c:265-272, driven by maple.c:1001-1031,
+ * set up at maple.c:1140-1154). gfull_init needs the dense projections (gpre_dense_add per layer: group 2L = q,
+ * k, v, group 2L+1 = o; gpre_dense_done) and takes norms[24][4352] (in_ln | post_ln | q_norm | k_norm, fp32
+ * holding bf16 values), the 24 routers (bf16 [256][2048] each) and the rope table cs[ctx][32][2]; it keeps a
+ * per-layer fp16 key/value cache of ctx positions in HBM. gfull_begin loads a chunk of nb hidden vectors at
+ * positions pos0..; gfull_attn(L, glob) runs the attention half of layer L (maple.c:706-724: rmsnorm, q/k/v,
+ * head norms, rope unless glob, cache, causal attention over the window win (all positions when glob), o,
+ * x += o), then post-norm and the router: rl gets nb x 256 logits; synchronous, returns device seconds (-1.0 on
+ * error). gfull_moe adds the experts of the host's grouping into x (asynchronous). gfull_read waits, copies x
+ * back and sets *ko to the chunk's fp16 k | v of every layer ([24][gfull_maxtok()][1024]). Results: k, v, x
+ * after attention and the logits equal maple.c's CPU statements bit for bit. */
 int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t *router, const float *cs);
 void gfull_begin(const float *x, int nb, int pos0);
 double gfull_attn(int L, int glob, float *rl);
@@ -124,6 +132,12 @@ int mmoe_graph_reset(void);
  * hn = rmsnorm(x, post_ln[L]), rl[nb][256] = router logits (copied to the host if rl != NULL). */
 int mmoe_gfull_setup(int maxtok);
 int mmoe_gfull_post_norm(int L, float *rl);
+/* Layers L0 .. L0+nl-1 of the gfull chunk entirely on the device, asynchronous (no counterpart in maple.c,
+ * whose step_batch_card, maple.c:1005-1022, brings the logits to the host for top-8 and grouping between the
+ * halves): per layer the attention half of gfull_attn (glob = (L % 4) == 3, maple.c:1008) and then the MoE
+ * block of mmoe_stack_dev on the hidden state (post-norm, router, top-8, grouping, experts, combine). Needs
+ * gfull_init, gfull_begin and mmoe_set_layer for every layer (expert tables); gfull_read waits for it. */
+int mmoe_gfull_stack(int L0, int nl);
 
 /* Intermediate results of the last call on the main context (tests and checks, like GPRE_CHECK) */
 #define MMOE_R_LOGITS 0   /* float [nb][256] */
@@ -176,7 +190,12 @@ void *mmoe_stream(void);
 #define MMOE_K_QUANT_ACT 6
 #define MMOE_K_DOWN 7
 #define MMOE_K_COMBINE 8
-#define MMOE_PROF_NKERNELS 9
+#define MMOE_K_DENSE 9          /* k_dense: q/k/v and o projections */
+#define MMOE_K_QKN 10           /* k_qkn: head norms, rope, fp16 cache */
+#define MMOE_K_ATT_SCORES 11
+#define MMOE_K_ATT_SOFTMAX 12
+#define MMOE_K_ATT_PV 13
+#define MMOE_PROF_NKERNELS 14
 int mmoe_event_record(int slot);
 /* Re-launch one stage (MMOE_K_GATEUP, _DOWN, _QUANT_ACT, _ROUTER) of the last main-context call reps times
  * back to back between two events; returns average ms per launch, or -1.0. */

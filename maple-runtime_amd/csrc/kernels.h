@@ -1317,7 +1317,8 @@ struct DenseMat { const uint8_t *codes; const float *scales; int rows, yoff; };
 // v_mfma_i32_32x32x32_i8 with gu_chunk's operand mapping (the two row fragments take the places of gate and
 // up). Activations pass through two padded LDS stages, codes 2 chunks ahead in registers, as k_gateup.
 // grid = (sum of rows / (64 WAVES), ceil(nb / 64)); rbs[m] = first row block of matrix m (rbs[nmat] = total).
-template <int WAVES>
+// ACC: y += the product (maple.c:724, x += o), else y = the product.
+template <int WAVES, bool ACC = false>
 __global__ void __launch_bounds__(WAVES * 64) k_dense(const DenseMat *__restrict__ mats, const int *__restrict__ rbs, int nmat,
                                                int nb, int ys, const int8_t *__restrict__ qx, const float *__restrict__ qsx,
                                                const int *__restrict__ qsumx, float *__restrict__ y) {
@@ -1385,7 +1386,9 @@ __global__ void __launch_bounds__(WAVES * 64) k_dense(const DenseMat *__restrict
                 float sv[4] = {sc.x, sc.y, sc.z, sc.w}, o[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) o[i] = (float)(acc[f][j][g * 4 + i] - qsum) * qs * sv[i];
-                *(float4 *)(y + (size_t)b * ys + M.yoff + r) = make_float4(o[0], o[1], o[2], o[3]);
+                float4 *yp = (float4 *)(y + (size_t)b * ys + M.yoff + r);
+                if (ACC) { float4 yv = *yp; o[0] = yv.x + o[0]; o[1] = yv.y + o[1]; o[2] = yv.z + o[2]; o[3] = yv.w + o[3]; }
+                *yp = make_float4(o[0], o[1], o[2], o[3]);
             }
     }
 }

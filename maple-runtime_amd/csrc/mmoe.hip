@@ -18,6 +18,7 @@
 #include <vector>
 #include "kernels.h"
 #include "decode.h"
+#include "attn.h"
 #ifndef GU16_W
 #define GU16_W 4    // small-tile gate/up: waves per workgroup, 16-row fragments per wave
 #define GU16_RF 1
@@ -490,6 +491,19 @@ int gpre_dense_done(int maxtok) {
     return 0;
 }
 
+// Drops the projections from HBM; gpre_dense_add may stage a new set.
+int mmoe_dense_reset(void) {
+    if (DN.dev) HC(hipFree(DN.dev));
+    if (DN.dmat) HC(hipFree(DN.dmat));
+    if (DN.drbs) HC(hipFree(DN.drbs));
+    if (DN.y) HC(hipFree(DN.y));
+    std::vector<uint8_t>().swap(DN.host);
+    memset(DN.mat, 0, sizeof DN.mat); memset(DN.n, 0, sizeof DN.n); memset(DN.rows, 0, sizeof DN.rows);
+    DN.maxtok = 0; DN.dev = nullptr; DN.dmat = nullptr; DN.drbs = nullptr; DN.y = nullptr;
+    DN.ymax = DN.ready = DN.bad = 0;
+    return 0;
+}
+
 // y[nb][rows of group g] = group g's matrices times x[nb][2048] (host arrays); returns device seconds
 double gpre_dense(int g, const float *x, int nb, float *y) {
     if (!DN.ready) { seterr("gpre_dense before gpre_dense_done"); return -1.0; }
@@ -502,7 +516,7 @@ double gpre_dense(int g, const float *x, int nb, float *y) {
     (void)hipEventRecord(a, S.st);
     if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_dense: copy x"); return -1.0; }
     if (stage_quant_x(w, w.hn, nb)) return -1.0;
-    if (launch(MMOE_K_GATEUP, [&] {
+    if (launch(MMOE_K_DENSE, [&] {
             k_dense<DENSE_W><<<dim3(nrb, (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, ys, w.qx, w.qsx, w.qsumx, DN.y);
         })) return -1.0;
     (void)hipEventRecord(b, S.st);
@@ -521,21 +535,106 @@ int gpu_head_init_i8(const int8_t *w, const float *scale, int rows, int cols) { 
 void gpu_head_run(const float *x, float *y) { (void)x; (void)y; seterr("gpu_head_run: not part of this build"); }
 void gpu_head_run_multi(const float *x, int n, float *y) { (void)x; (void)n; (void)y; seterr("gpu_head_run_multi: not part of this build"); }
 
-// ---- whole-layer state (gpu_pre.m:387-594). Attention is not part of this build, so gfull_init reports
-// failure and maple.c runs gpre_moe with CPU attention (maple.c:1156-1158). The device hidden state and
-// gfull_moe work for callers that prepare the MoE input with mmoe_gfull_setup / mmoe_gfull_post_norm.
+static int set_router(int L, const uint16_t *router);
+
+// ---- whole layers on the card (gpu_pre.m:387-594): the hidden state of a chunk stays in HBM; per layer
+// gfull_attn runs rmsnorm -> q/k/v (k_dense) -> q/k norm + rope + fp16 cache -> attention -> o (x += o) ->
+// post-norm -> router logits (exact chains), and gfull_moe the experts of the pairs the host picked.
+// One sequence; the chunk's nb tokens sit at positions pos0 .. pos0+nb-1 of a cache of ctx positions.
+#define GF_NWL 4352   // per layer in the norms gfull_init receives: in_ln 2048 | post_ln 2048 | q_norm 128 | k_norm 128
+static struct {
+    int ready, ctx, win, maxtok, pos0;
+    uint16_t *nw;                 // bf16 [24][4352] (the fp32 norms are bf16 values: exact)
+    float *cs;                    // [ctx][32][2]
+    __half *kc, *vc, *ko;         // [24][ctx][512] x 2, [24][maxtok][1024]
+    uint16_t *ko_host;            // gfull_read's copy
+    float *qkv, *att, *sc, *inv;  // [maxtok][3072], [maxtok][2048], [maxtok * 16][ctx], [maxtok * 16]
+    double t_attn;
+} GF;
+
 int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t *router, const float *cs) {
-    (void)ctx; (void)maxtok; (void)win; (void)norms; (void)router; (void)cs;
-    fprintf(stderr, "maplemoe: whole layers need attention on the card, not part of this build\n");
-    return -1;
+    if (ctx_ready()) return -1;
+    if (!DN.ready) { seterr("gfull_init: the dense projections are not on the card (gpre_dense_done)"); fprintf(stderr, "maplemoe: %s\n", mmoe_last_error()); return -1; }
+    if (ctx < 1 || maxtok < 1 || maxtok > S.main.maxtok || maxtok > DN.maxtok || win < 0 || !norms || !router || !cs) {
+        seterr("gfull_init: ctx %d / maxtok %d (context %d) / win %d", ctx, maxtok, S.main.maxtok, win); return -1;
+    }
+    if (GF.ready) {   // a second set-up replaces the first
+        HC(hipFree(GF.nw)); HC(hipFree(GF.cs)); HC(hipFree(GF.kc)); HC(hipFree(GF.vc)); HC(hipFree(GF.ko));
+        HC(hipFree(GF.qkv)); HC(hipFree(GF.att)); HC(hipFree(GF.sc)); HC(hipFree(GF.inv)); free(GF.ko_host);
+        GF.ready = 0;
+    }
+    std::vector<uint16_t> nw((size_t)24 * GF_NWL);
+    for (size_t i = 0; i < nw.size(); i++) { uint32_t u; memcpy(&u, &norms[i], 4); nw[i] = (uint16_t)(u >> 16); }
+    HC(hipMalloc(&GF.nw, nw.size() * 2)); HC(hipMemcpy(GF.nw, nw.data(), nw.size() * 2, hipMemcpyHostToDevice));
+    HC(hipMalloc(&GF.cs, (size_t)ctx * 64 * 4)); HC(hipMemcpy(GF.cs, cs, (size_t)ctx * 64 * 4, hipMemcpyHostToDevice));
+    size_t kvb = (size_t)24 * ctx * 512 * 2, kob = (size_t)24 * maxtok * 1024 * 2;
+    HC(hipMalloc(&GF.kc, kvb)); HC(hipMalloc(&GF.vc, kvb)); HC(hipMalloc(&GF.ko, kob));
+    HC(hipMemset(GF.kc, 0, kvb)); HC(hipMemset(GF.vc, 0, kvb));
+    GF.ko_host = (uint16_t *)malloc(kob);
+    HC(hipMalloc(&GF.qkv, (size_t)maxtok * 3072 * 4)); HC(hipMalloc(&GF.att, (size_t)maxtok * MH * 4));
+    HC(hipMalloc(&GF.sc, (size_t)maxtok * 16 * ctx * 4)); HC(hipMalloc(&GF.inv, (size_t)maxtok * 16 * 4));
+    for (int L = 0; L < 24; L++) {
+        if (set_router(L, router + (size_t)L * MNE * MH)) return -1;
+        LayerW &lw = S.layers[L];
+        if (!lw.post_ln) HC(hipMalloc(&lw.post_ln, MH * 2));
+        HC(hipMemcpy(lw.post_ln, nw.data() + (size_t)L * GF_NWL + MH, MH * 2, hipMemcpyHostToDevice));
+    }
+    GF.ctx = ctx; GF.win = win; GF.maxtok = maxtok; GF.ready = 1;
+    S.gfull = true;
+    fprintf(stderr, "maplemoe: whole layers on the card, key/value cache %.0f MB\n", 2.0 * kvb / 1e6);
+    return 0;
 }
+// a new chunk: nb hidden vectors (embeddings) at positions pos0..
 void gfull_begin(const float *x, int nb, int pos0) {
-    (void)pos0;
     if (!S.gfull || nb < 1 || nb > S.main.maxtok) { seterr("gfull_begin: not set up or nb %d out of range", nb); return; }
-    S.gfull_nb = nb;
+    if (GF.ready && (nb > GF.maxtok || pos0 < 0 || pos0 + nb > GF.ctx)) { seterr("gfull_begin: positions %d..%d past ctx %d", pos0, pos0 + nb - 1, GF.ctx); return; }
+    S.gfull_nb = nb; GF.pos0 = pos0;
     HCV(hipMemcpyAsync(S.main.x, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st));
 }
-double gfull_attn(int L, int glob, float *rl) { (void)L; (void)glob; (void)rl; seterr("gfull_attn: attention is not part of this build"); return -1.0; }
+// The attention half of layer L (asynchronous): x += o(attention(q, k, v of rmsnorm(x, in_ln))), k and v into
+// the layer's cache and ko.
+static int gfull_attn_launch(int L, int glob) {
+    if (!GF.ready || !S.gfull_nb) { seterr("gfull_attn: gfull_init / gfull_begin first"); return -1; }
+    if (L < 0 || L >= 24) { seterr("gfull_attn: layer %d", L); return -1; }
+    if (DN.rows[2 * L] != 3072 || DN.rows[2 * L + 1] != 2048) {
+        seterr("gfull_attn: layer %d projections are not q,k,v (3072 rows) and o (2048) (gpre_dense_add)", L); return -1;
+    }
+    Work &w = S.main;
+    int nb = S.gfull_nb, pos0 = GF.pos0, ctx = GF.ctx, win = GF.win, g = 2 * L;
+    const uint16_t *nwl = GF.nw + (size_t)L * GF_NWL;
+    __half *kcl = GF.kc + (size_t)L * ctx * 512, *vcl = GF.vc + (size_t)L * ctx * 512, *kol = GF.ko + (size_t)L * GF.maxtok * 1024;
+    if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(w.x, nwl, w.hn, nb); })) return -1;
+    if (stage_quant_x(w, w.hn, nb)) return -1;
+    if (launch(MMOE_K_DENSE, [&] {
+        k_dense<DENSE_W><<<dim3(3072 / (64 * DENSE_W), (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, 3072, w.qx, w.qsx, w.qsumx, GF.qkv);
+    })) return -1;
+    if (launch(MMOE_K_QKN, [&] {
+        k_qkn<<<dim3(nb, 24), 64, 0, S.st>>>(GF.qkv, pos0, glob, nwl + 4096, nwl + 4224, GF.cs, kcl, vcl, kol);
+    })) return -1;
+    if (launch(MMOE_K_ATT_SCORES, [&] { k_att_scores<<<nb * 4, 256, 0, S.st>>>(GF.qkv, pos0, glob, win, kcl, GF.sc, ctx); })) return -1;
+    if (launch(MMOE_K_ATT_SOFTMAX, [&] { k_att_softmax<<<nb * 16, 64, 0, S.st>>>(pos0, glob, win, GF.sc, GF.inv, ctx); })) return -1;
+    if (launch(MMOE_K_ATT_PV, [&] { k_att_pv<<<nb * 4, 512, 0, S.st>>>(pos0, glob, win, GF.sc, GF.inv, vcl, GF.att, ctx); })) return -1;
+    if (stage_quant_x(w, GF.att, nb)) return -1;
+    return launch(MMOE_K_DENSE, [&] {
+        k_dense<DENSE_W, true><<<dim3(MH / (64 * DENSE_W), (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + (g + 1) * 3, DN.drbs + (g + 1) * 4, DN.n[g + 1], nb, MH, w.qx, w.qsx, w.qsumx, w.x);
+    });
+}
+// The attention half of layer L and the router: rl gets nb x 256 logits. Synchronous; returns device seconds.
+double gfull_attn(int L, int glob, float *rl) {
+    hipEvent_t a, b;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { seterr("gfull_attn: event"); return -1.0; }
+    (void)hipEventRecord(a, S.st);
+    int rc = gfull_attn_launch(L, glob);
+    (void)hipEventRecord(b, S.st);
+    if (!rc) rc = mmoe_gfull_post_norm(L, rl);
+    if (!rc && hipStreamSynchronize(S.st) != hipSuccess) { seterr("gfull_attn: stream"); rc = -1; }
+    float ms = 0;
+    if (!rc) (void)hipEventElapsedTime(&ms, a, b);
+    (void)hipEventDestroy(a); (void)hipEventDestroy(b);
+    if (rc) return -1.0;
+    GF.t_attn += ms * 1e-3;
+    return ms * 1e-3;
+}
 // gpu_pre.m:508-566: asynchronous; adds each token's weighted expert outputs into the device hidden state
 void gfull_moe(int nu, const uint32_t *loc, const int *regs, const int *ustart, const int *ptok, const float *pw, const int *tp) {
     if (!S.gfull) { seterr("gfull_moe: gfull state not set up"); return; }
@@ -545,18 +644,22 @@ void gfull_moe(int nu, const uint32_t *loc, const int *regs, const int *ustart, 
     if (experts_host_grouping(S.main, S.gfull_nb, nu, ep, ustart, ptok, pw, tp)) return;
     stage_combine(S.main, S.gfull_nb, S.main.x, MMOE_COMBINE_ADD);
 }
-// gpu_pre.m:569-584: waits, copies the hidden state back; K/V are not kept by this build (*ko = NULL)
+// gpu_pre.m:569-584: waits, copies the hidden state back; *ko -> the chunk's k,v of every layer
+// (24 x maxtok x 1024 fp16, k | v per token; NULL before gfull_init)
 void gfull_read(float *x, const uint16_t **ko) {
-    if (ko) *ko = NULL;
     HCV(hipStreamSynchronize(S.st));
     if (x && S.gfull) HCV(hipMemcpy(x, S.main.x, (size_t)S.gfull_nb * MH * 4, hipMemcpyDeviceToHost));
+    if (ko) {
+        *ko = NULL;
+        if (GF.ready) { HCV(hipMemcpy(GF.ko_host, GF.ko, (size_t)24 * GF.maxtok * 1024 * 2, hipMemcpyDeviceToHost)); *ko = GF.ko_host; }
+    }
 }
 void gfull_write_x(const float *x) {
     if (!S.gfull) { seterr("gfull_write_x: not set up"); return; }
     HCV(hipMemcpyAsync(S.main.x, x, (size_t)S.gfull_nb * MH * 4, hipMemcpyHostToDevice, S.st));
 }
-int gfull_maxtok(void) { return S.main.maxtok; }
-void gfull_report(void) { fprintf(stderr, "maplemoe: %.3f s of expert work on the card\n", S.t_moe); }
+int gfull_maxtok(void) { return GF.ready ? GF.maxtok : S.main.maxtok; }
+void gfull_report(void) { fprintf(stderr, "maplemoe: card %.3f s attention half, %.3f s expert work\n", GF.t_attn, S.t_moe); }
 
 // ---- decode expert cache (gpu_exp.m:155-291). Slots hold experts in the reference layout in HBM; a hit
 // runs prep, gate/up, SiLU, re-quant and down on the device with maple.c's int8 semantics.
@@ -651,8 +754,20 @@ int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *
     ExpPtr ep[MNE];
     if (resolve_loc(loc, regs, MNE, ep)) return -1;
     if (!lw.tab) HC(hipMalloc(&lw.tab, sizeof(ExpPtr) * MNE));
-    if (!lw.router) HC(hipMalloc(&lw.router, (size_t)MNE * MH * 2));
     HC(hipMemcpy(lw.tab, ep, sizeof ep, hipMemcpyHostToDevice));
+    if (set_router(L, router)) return -1;
+    if (post_ln) {
+        if (!lw.post_ln) HC(hipMalloc(&lw.post_ln, MH * 2));
+        HC(hipMemcpy(lw.post_ln, post_ln, MH * 2, hipMemcpyHostToDevice));
+    }
+    return 0;
+}
+
+// Layer L's router (bf16 [256][2048]) into HBM with its chain-major copies (both orders, and fp32 for the
+// tiled batch router) and the bound the MFMA router option uses.
+static int set_router(int L, const uint16_t *router) {
+    LayerW &lw = S.layers[L];
+    if (!lw.router) HC(hipMalloc(&lw.router, (size_t)MNE * MH * 2));
     HC(hipMemcpy(lw.router, router, (size_t)MNE * MH * 2, hipMemcpyHostToDevice));
     if (!lw.rc16) HC(hipMalloc(&lw.rc16, (size_t)MNE * MH * 2));
     if (!lw.rc8) HC(hipMalloc(&lw.rc8, (size_t)MNE * MH * 2));
@@ -664,10 +779,6 @@ int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *
     k_router_l1max<<<1, 256, 0, S.st>>>(lw.router, lw.w1max);
     HC(hipGetLastError());
     HC(hipStreamSynchronize(S.st));
-    if (post_ln) {
-        if (!lw.post_ln) HC(hipMalloc(&lw.post_ln, MH * 2));
-        HC(hipMemcpy(lw.post_ln, post_ln, MH * 2, hipMemcpyHostToDevice));
-    }
     return 0;
 }
 
@@ -716,6 +827,17 @@ int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order) {
         }
         if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(d_x, pw, w.hn, nb); })) return -1;
         if (moe_dev(L, w.hn, nb, d_x, order)) return -1;
+    }
+    return 0;
+}
+
+int mmoe_gfull_stack(int L0, int nl) {
+    if (ctx_ready()) return -1;
+    if (L0 < 0 || nl < 1 || L0 + nl > 24) { seterr("mmoe_gfull_stack: layers %d..%d outside 0..23", L0, L0 + nl - 1); return -1; }
+    for (int L = L0; L < L0 + nl; L++) {
+        if (!S.layers[L].tab) { seterr("mmoe_gfull_stack: layer %d has no experts (mmoe_set_layer)", L); return -1; }
+        if (gfull_attn_launch(L, (L % 4) == 3)) return -1;
+        if (mmoe_stack_dev(L, 1, S.main.x, S.gfull_nb, MMOE_ORDER_BATCH)) return -1;
     }
     return 0;
 }

@@ -24,7 +24,8 @@ ORDER_BATCH, ORDER_STEP = 0, 1
 COMBINE_OVERWRITE, COMBINE_BATCH, COMBINE_ADD, COMBINE_STEP = 0, 1, 4, 6
 R = dict(LOGITS=0, TOP=1, TW=2, PLAN=3, UTOK=4, UW=5, TP=6, SP=7, QX=8, QSX=9, QSUMX=10, ACT=11, QA=12, QSA=13,
          QSUMA=14, DOWN=15, GU_I32=16, DN_I32=17, X=18, HN=19)
-KERNELS = ["rmsnorm", "router", "topk", "group", "quant", "gateup", "quant_act", "down", "combine"]
+KERNELS = ["rmsnorm", "router", "topk", "group", "quant", "gateup", "quant_act", "down", "combine", "dense", "qkn",
+           "att_scores", "att_softmax", "att_pv"]
 
 _lib = None
 
@@ -45,7 +46,7 @@ def _declare(L):
     sig = {
         "gpre_init": (i, [i, i]), "gpre_region": (i, [vp, sz]), "gpre_stage": (i, [sz]),
         "gpre_moe": (d, [vp, i, i, vp, vp, vp, vp, vp, vp, vp, vp]), "gpre_blit_seconds": (d, []),
-        "gpre_dense_done": (i, [i]), "gpre_dense_add": (None, [i, vp, vp, i, i]), "gpre_dense": (d, [i, vp, i, vp]), "gfull_init": (i, [i, i, i, vp, vp, vp]),
+        "gpre_dense_done": (i, [i]), "gpre_dense_add": (None, [i, vp, vp, i, i]), "gpre_dense": (d, [i, vp, i, vp]), "mmoe_dense_reset": (i, []), "gfull_init": (i, [i, i, i, vp, vp, vp]),
         "gfull_begin": (None, [vp, i, i]), "gfull_attn": (d, [i, i, vp]),
         "gfull_moe": (None, [i, vp, vp, vp, vp, vp, vp]), "gfull_read": (None, [vp, vp]),
         "gfull_write_x": (None, [vp]), "gfull_maxtok": (i, []), "gfull_report": (None, []),
@@ -57,7 +58,7 @@ def _declare(L):
         "mmoe_moe": (i, [i, vp, i, vp, i]), "mmoe_moe_dev": (i, [i, vp, i, vp, i]),
         "mmoe_rmsnorm_dev": (i, [vp, vp, i, vp]), "mmoe_stack_dev": (i, [i, i, vp, i, i]),
         "mmoe_stack_graph": (i, [i, i, vp, i, i, i]), "mmoe_graph_reset": (i, []),
-        "mmoe_gfull_setup": (i, [i]), "mmoe_gfull_post_norm": (i, [i, vp]),
+        "mmoe_gfull_setup": (i, [i]), "mmoe_gfull_post_norm": (i, [i, vp]), "mmoe_gfull_stack": (i, [i, i]),
         "mmoe_read": (i, [i, vp, sz]), "mmoe_set_debug": (i, [i]), "mmoe_set_decode_path": (i, [i]), "mmoe_set_router_mode": (i, [i]), "mmoe_last_error": (C.c_char_p, []),
         "mmoe_dev_alloc": (vp, [sz]), "mmoe_dev_free": (i, [vp]), "mmoe_h2d": (i, [vp, vp, sz]),
         "mmoe_d2h": (i, [vp, vp, sz]), "mmoe_d2d": (i, [vp, vp, sz]), "mmoe_sync": (i, []), "mmoe_stream": (vp, []),

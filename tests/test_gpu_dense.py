@@ -36,6 +36,7 @@ def cpu_projection(x, mats):
 def test_gpre_dense_matches_cpu_projections():
     lib = M.lib()
     M.check(lib.mmoe_init(2048), "mmoe_init")
+    M.check(lib.mmoe_dense_reset(), "dense reset")
     assert lib.gpre_dense(0, None, 1, None) < 0                              # before gpre_dense_done
     rng = np.random.default_rng(SEED + 7)
     groups = {0: [2048, 512, 512], 1: [2048]}                               # layer 0: q, k, v; then o
