@@ -8,130 +8,237 @@
 //   attention     maple.c:516-558 (attend_group, AVX2 path): scores as 8 FMA lanes over the head dimension
 //                 folded by hsum8, softmax with the library's exp and a sum in position order, output as an
 //                 FMA chain over positions.
-// These kernels are correctness-first: one thread per score and per output element, no MFMA.
+// Work split: scores and the weighted sum of values take groups of consecutive tokens of one key/value head per
+// workgroup, so each cached key or value row is read once for the group and feeds all its query heads; a
+// token's own window is enforced with a zero weight outside it (an FMA with weight 0 leaves a chain unchanged,
+// exactly), so a group shares one loop over positions.
 #pragma once
 #include <hip/hip_fp16.h>
 #include "kernels.h"
 
 #define AT_HD 128
 #define AT_QKV 3072   // q 16 x 128 | k 4 x 128 | v 4 x 128 per token
-
-// One wave per (token b, head h): h < 16 query heads, 16..19 key heads, 20..23 value heads. q/k heads are
-// normalised (q_norm / k_norm), roped on local layers (glob == 0); q stays fp32 in qkv, k and v go to the
-// layer's cache kc/vc [position][512] and to ko[b][1024] (k | v) as fp16.
-__global__ void __launch_bounds__(64) k_qkn(float *__restrict__ qkv, int pos0, int glob, const uint16_t *__restrict__ qn,
-                                            const uint16_t *__restrict__ kn, const float *__restrict__ cs,
-                                            __half *__restrict__ kc, __half *__restrict__ vc, __half *__restrict__ ko) {
-    __shared__ float xs[AT_HD];
-    __shared__ float kk;
-    int b = blockIdx.x, h = blockIdx.y, l = threadIdx.x, pos = pos0 + b;
-    float *src = qkv + (size_t)b * AT_QKV + h * AT_HD;   // q 0..2047, k 2048..2559, v 2560..3071
-    float a0 = src[l], a1 = src[l + 64];
-    if (h >= 20) {
-        int c = (h - 20) * AT_HD;
-        __half h0 = __float2half_rn(a0), h1 = __float2half_rn(a1);
-        vc[(size_t)pos * 512 + c + l] = h0; vc[(size_t)pos * 512 + c + l + 64] = h1;
-        ko[(size_t)b * 1024 + 512 + c + l] = h0; ko[(size_t)b * 1024 + 512 + c + l + 64] = h1;
-        return;
-    }
-    xs[l] = a0; xs[l + 64] = a1;
-    __syncthreads();
-    if (l == 0) {
-        double ss = 0.0;
-        for (int i = 0; i < AT_HD; i++) ss += (double)xs[i] * (double)xs[i];
-        kk = 1.0f / sqrtf((float)(ss / (double)AT_HD) + 1e-6f);
-    }
-    __syncthreads();
-    float k = kk;
-    const uint16_t *w = h < 16 ? qn : kn;
-    a0 = a0 * k * bf16f(w[l]); a1 = a1 * k * bf16f(w[l + 64]);
-    if (!glob) {   // rope on dims 0..63 (lane l holds dim l in a0): pairs (i, i + 32)
-        __syncthreads();
-        xs[l] = a0;
-        __syncthreads();
-        int i = l & 31;
-        float c = cs[((size_t)pos * 32 + i) * 2], s = cs[((size_t)pos * 32 + i) * 2 + 1];
-        if (l < 32) a0 = __builtin_fmaf(a0, c, -(xs[l + 32] * s));
-        else a0 = __builtin_fmaf(a0, c, xs[l - 32] * s);
-    }
-    if (h < 16) { src[l] = a0; src[l + 64] = a1; return; }
-    int c = (h - 16) * AT_HD;
-    __half h0 = __float2half_rn(a0), h1 = __float2half_rn(a1);
-    kc[(size_t)pos * 512 + c + l] = h0; kc[(size_t)pos * 512 + c + l + 64] = h1;
-    ko[(size_t)b * 1024 + c + l] = h0; ko[(size_t)b * 1024 + c + l + 64] = h1;
-}
+#define AT_XS 129     // LDS row stride of a head (a lane per head reads its own row without bank conflicts)
 
 __device__ __forceinline__ int att_lo(int pos, int glob, int win) { return glob ? 0 : (pos - win > 0 ? pos - win : 0); }
 
-// Scores of the 4 query heads of key/value head kvh of token b (block = (b, kvh), thread = position t):
-// sc[(b * 16 + kvh * 4 + j) * ctx + t - lo] = hsum8(8 FMA lanes over the dims) * 1/sqrtf(128).
-__global__ void __launch_bounds__(256) k_att_scores(const float *__restrict__ qkv, int pos0, int glob, int win,
-                                                    const __half *__restrict__ kc, float *__restrict__ sc, int ctx) {
-    __shared__ float qs[4][AT_HD];
-    int b = blockIdx.x >> 2, kvh = blockIdx.x & 3, tid = threadIdx.x, pos = pos0 + b;
-    int lo = att_lo(pos, glob, win), T = pos - lo + 1;
-    for (int i = tid; i < 4 * AT_HD; i += 256) qs[i >> 7][i & 127] = qkv[(size_t)b * AT_QKV + (kvh * 4 + (i >> 7)) * AT_HD + (i & 127)];
+// Raises *a to v (float maximum through integer atomics: non-negative floats order as signed integers,
+// negative ones in reverse as unsigned integers).
+__device__ __forceinline__ void atomic_max_f32(float *a, float v) {
+    if (__float_as_int(v) >= 0) atomicMax((int *)a, __float_as_int(v));
+    else atomicMin((unsigned int *)a, __float_as_uint(v));
+}
+
+// One workgroup per token b (it also sets the token's 16 score maxima to -1e30). q heads 0..15 and k heads 16..19 are normalised (q_norm / k_norm, sum of squares
+// in fp64 in index order, one lane per head), roped on local layers (glob == 0); q stays fp32 in qkv, k and v
+// go to the layer's cache kc/vc [position][512] and to ko[b][1024] (k | v) as fp16.
+__global__ void __launch_bounds__(256) k_qkn(float *__restrict__ qkv, int pos0, int glob, const uint16_t *__restrict__ qn,
+                                             const uint16_t *__restrict__ kn, const float *__restrict__ cs,
+                                             __half *__restrict__ kc, __half *__restrict__ vc, __half *__restrict__ ko,
+                                             float *__restrict__ mx) {
+    __shared__ float xs[20 * AT_XS];
+    __shared__ float kk[20];
+    int b = blockIdx.x, t = threadIdx.x, pos = pos0 + b;
+    float *row = qkv + (size_t)b * AT_QKV;
+    if (t < 16) mx[b * 16 + t] = -1e30f;   // the score maxima k_att_scores raises
+    for (int i = t; i < 20 * AT_HD; i += 256) xs[(i >> 7) * AT_XS + (i & 127)] = row[i];
+    for (int i = t; i < 512; i += 256) {
+        __half h = __float2half_rn(row[2560 + i]);
+        vc[(size_t)pos * 512 + i] = h; ko[(size_t)b * 1024 + 512 + i] = h;
+    }
     __syncthreads();
-    const float scale = 1.0f / sqrtf((float)AT_HD);
-    for (int t = tid; t < T; t += 256) {
-        const uint4 *kr = (const uint4 *)(kc + (size_t)(lo + t) * 512 + kvh * AT_HD);
-        float a[4][8];
+    if (t < 20) {
+        const float *x = xs + t * AT_XS;
+        double ss = 0.0;
+        for (int i = 0; i < AT_HD; i++) ss += (double)x[i] * (double)x[i];
+        kk[t] = 1.0f / sqrtf((float)(ss / (double)AT_HD) + 1e-6f);
+    }
+    __syncthreads();
+    float y[10];   // elements t + 256 m of the 20 heads
+#pragma unroll
+    for (int m = 0; m < 10; m++) {
+        int i = t + m * 256, h = i >> 7, d = i & 127;
+        y[m] = xs[h * AT_XS + d] * kk[h] * bf16f((h < 16 ? qn : kn)[d]);
+    }
+    if (!glob) {   // rope on dims 0..63 of every head: pairs (i, i + 32)
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < 10; m++) { int i = t + m * 256; xs[(i >> 7) * AT_XS + (i & 127)] = y[m]; }
+        __syncthreads();
+#pragma unroll
+        for (int m = 0; m < 10; m++) {
+            int i = t + m * 256, h = i >> 7, d = i & 127;
+            if (d >= 64) continue;
+            float c = cs[((size_t)pos * 32 + (d & 31)) * 2], sn = cs[((size_t)pos * 32 + (d & 31)) * 2 + 1];
+            if (d < 32) y[m] = __builtin_fmaf(y[m], c, -(xs[h * AT_XS + d + 32] * sn));
+            else y[m] = __builtin_fmaf(y[m], c, xs[h * AT_XS + d - 32] * sn);
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < 10; m++) {
+        int i = t + m * 256;
+        if (i < 2048) { row[i] = y[m]; continue; }
+        __half h = __float2half_rn(y[m]);
+        kc[(size_t)pos * 512 + i - 2048] = h; ko[(size_t)b * 1024 + i - 2048] = h;
+    }
+}
+
+// Scores of the 4 query heads of key/value head kvh for a group of NB consecutive tokens (block x = (group,
+// kvh)), one thread per cached position (block y = a run of 64 positions from the group's first window start):
+// sc[(b * 16 + kvh * 4 + j) * ctx + p - lo_b] = hsum8(8 FMA lanes over the dims) * 1/sqrtf(128), for the tokens b
+// whose window [lo_b, pos_b] holds p; mx[b * 16 + h] is raised to the row maximum. The q values are the same for
+// every lane and are read with wave-uniform loads (scalar registers feed the FMAs).
+template <int NB>
+__global__ void __launch_bounds__(64) k_att_scores(const float *__restrict__ qkv, int nb, int pos0, int glob, int win,
+                                                    const __half *__restrict__ kc, float *__restrict__ sc,
+                                                    float *__restrict__ mx, int ctx) {
+    int grp = blockIdx.x >> 2, kvh = blockIdx.x & 3, tid = threadIdx.x;
+    int b0 = grp * NB, nbt = min(NB, nb - b0);
+    int lo0 = att_lo(pos0 + b0, glob, win), phi = pos0 + b0 + nbt - 1, pstart = lo0 + blockIdx.y * 64;
+    if (pstart > phi) return;   // the whole block past the group's last position
+    int p = pstart + tid;
+    const uint4 *kr = (const uint4 *)(kc + (size_t)min(p, phi) * 512 + kvh * AT_HD);
+    const float *qb[NB];
+#pragma unroll
+    for (int bi = 0; bi < NB; bi++) qb[bi] = qkv + (size_t)min(b0 + bi, nb - 1) * AT_QKV + kvh * 4 * AT_HD;
+    float a[NB][4][8];
+#pragma unroll
+    for (int bi = 0; bi < NB; bi++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
 #pragma unroll
-            for (int l = 0; l < 8; l++) a[j][l] = 0.0f;
-#pragma unroll 4
-        for (int d8 = 0; d8 < AT_HD / 8; d8++) {
-            uint4 u = kr[d8];
-            const __half *hh = (const __half *)&u;
-            float kf[8];
+            for (int l = 0; l < 8; l++) a[bi][j][l] = 0.0f;
+#pragma unroll 2
+    for (int d8 = 0; d8 < AT_HD / 8; d8++) {
+        uint4 u = kr[d8];
+        const __half *hh = (const __half *)&u;
+        float kf[8];
 #pragma unroll
-            for (int l = 0; l < 8; l++) kf[l] = __half2float(hh[l]);
+        for (int l = 0; l < 8; l++) kf[l] = __half2float(hh[l]);
+#pragma unroll
+        for (int bi = 0; bi < NB; bi++)
 #pragma unroll
             for (int j = 0; j < 4; j++)
 #pragma unroll
-                for (int l = 0; l < 8; l++) a[j][l] = __builtin_fmaf(kf[l], qs[j][d8 * 8 + l], a[j][l]);
-        }
+                for (int l = 0; l < 8; l++) a[bi][j][l] = __builtin_fmaf(kf[l], qb[bi][j * AT_HD + d8 * 8 + l], a[bi][j][l]);
+    }
+    const float scale = 1.0f / sqrtf((float)AT_HD);
 #pragma unroll
-        for (int j = 0; j < 4; j++) sc[((size_t)b * 16 + kvh * 4 + j) * ctx + t] = hsum8(a[j]) * scale;
+    for (int bi = 0; bi < NB; bi++) {
+        int pb = pos0 + b0 + bi, lb = att_lo(pb, glob, win);
+        bool in = bi < nbt && p >= lb && p <= pb;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float v = hsum8(a[bi][j]) * scale;
+            if (in) sc[((size_t)(b0 + bi) * 16 + kvh * 4 + j) * ctx + p - lb] = v;
+            float m = wave_max(in ? v : -1e30f);
+            if (tid == 0 && bi < nbt) atomic_max_f32(mx + (b0 + bi) * 16 + kvh * 4 + j, m);
+        }
     }
 }
 
-// Per (token, head) row r = b * 16 + head: max over the row, p = exp(s - max) in place, the sum in position
-// order (lane 0 over LDS chunks), inv[r] = 1 / sum.
-#define AT_SMCH 1024
-__global__ void __launch_bounds__(64) k_att_softmax(int pos0, int glob, int win, float *__restrict__ sc,
-                                                    float *__restrict__ inv, int ctx) {
-    __shared__ float pl[AT_SMCH];
-    int r = blockIdx.x, b = r >> 4, l = threadIdx.x, pos = pos0 + b;
+// Softmax sums of the 16 rows (heads) of token b, one workgroup per token: p = exp(s - max) (max from
+// k_att_scores) over 256-position chunks staged in LDS, summed in position order by 16 lanes (one row each);
+// inv[b * 16 + h] = 1 / sum. k_att_pv recomputes the same p.
+#define AT_SMCH 256
+__global__ void __launch_bounds__(256) k_att_softmax(int pos0, int glob, int win, const float *__restrict__ sc,
+                                                     const float *__restrict__ mx, float *__restrict__ inv, int ctx) {
+    constexpr int LD = AT_SMCH + 4;   // 16-byte aligned rows; the 16 summing lanes hit distinct bank groups
+    __shared__ __attribute__((aligned(16))) float pl[16 * LD];
+    int b = blockIdx.x, tid = threadIdx.x, pos = pos0 + b;
     int T = pos - att_lo(pos, glob, win) + 1;
-    float *row = sc + (size_t)r * ctx;
-    float mx = -1e30f;
-    for (int t = l; t < T; t += 64) mx = fmaxf(mx, row[t]);
-    mx = wave_max(mx);
+    const float *rows = sc + (size_t)b * 16 * ctx;
+    const float *mr = mx + b * 16;
     float sum = 0.0f;
     for (int c0 = 0; c0 < T; c0 += AT_SMCH) {
         int n = min(AT_SMCH, T - c0);
-        for (int t = l; t < n; t += 64) { float p = dexp(row[c0 + t] - mx); row[c0 + t] = p; pl[t] = p; }
+        if (tid < n)
+#pragma unroll 4
+            for (int r = 0; r < 16; r++) pl[r * LD + tid] = dexp(rows[(size_t)r * ctx + c0 + tid] - mr[r]);
         __syncthreads();
-        if (l == 0) for (int t = 0; t < n; t++) sum += pl[t];
+        if (tid < 16) {   // in position order; 16 values are read ahead of their additions
+            const float4 *q4 = (const float4 *)(pl + tid * LD);
+            int t = 0;
+            for (; t + 16 <= n; t += 16) {
+                float4 a = q4[t / 4], b = q4[t / 4 + 1], c = q4[t / 4 + 2], d = q4[t / 4 + 3];
+                sum += a.x; sum += a.y; sum += a.z; sum += a.w; sum += b.x; sum += b.y; sum += b.z; sum += b.w;
+                sum += c.x; sum += c.y; sum += c.z; sum += c.w; sum += d.x; sum += d.y; sum += d.z; sum += d.w;
+            }
+            for (const float *q = pl + tid * LD; t < n; t++) sum += q[t];
+        }
         __syncthreads();
     }
-    if (l == 0) inv[r] = 1.0f / sum;
+    if (tid < 16) inv[b * 16 + tid] = 1.0f / sum;
 }
 
-// Output of head (kvh * 4 + j), dim d of token b (block = (b, kvh), thread = (j, d)): the FMA chain over
-// positions of (p * inv) * v, into att[b][2048].
-__global__ void __launch_bounds__(512) k_att_pv(int pos0, int glob, int win, const float *__restrict__ sc,
-                                                const float *__restrict__ inv, const __half *__restrict__ vc,
+// Output of a group of NB consecutive tokens for key/value head kvh (block = (group, kvh), groups with the
+// longest windows first): wave j is query head kvh * 4 + j, lane l dims 2l and 2l + 1. Per run of AT_PVCH
+// positions the weights w = exp(s - max) * inv of the group's tokens are staged in LDS (0 outside a token's window; the
+// next run's are loaded into registers while the current one is consumed) and each output is the FMA chain over
+// positions of w * v, into att[b][2048].
+#define AT_PVCH 128
+template <int NB>
+__global__ void __launch_bounds__(256) k_att_pv(int nb, int pos0, int glob, int win, const float *__restrict__ sc,
+                                                const float *__restrict__ mx, const float *__restrict__ inv, const __half *__restrict__ vc,
                                                 float *__restrict__ att, int ctx) {
-    int b = blockIdx.x >> 2, kvh = blockIdx.x & 3, tid = threadIdx.x, j = tid >> 7, d = tid & 127, pos = pos0 + b;
-    int lo = att_lo(pos, glob, win), T = pos - lo + 1;
-    int r = b * 16 + kvh * 4 + j;
-    const float *p = sc + (size_t)r * ctx;
-    const __half *v = vc + (size_t)lo * 512 + kvh * AT_HD + d;
-    float iv = inv[r], o = 0.0f;
+    constexpr int PER = 4 * NB * AT_PVCH / 256;   // staged weights per thread
+    __shared__ __attribute__((aligned(16))) float wl[4][AT_PVCH][NB];
+    int ngrp = (nb + NB - 1) / NB;
+    int grp = ngrp - 1 - (int)(blockIdx.x >> 2), kvh = blockIdx.x & 3;
+    int tid = threadIdx.x, j = tid >> 6, lane = tid & 63;
+    int b0 = grp * NB, nbt = min(NB, nb - b0);
+    int lo0 = att_lo(pos0 + b0, glob, win), phi = pos0 + b0 + nbt - 1;
+    const uint32_t *vp = (const uint32_t *)(vc + kvh * AT_HD) + lane;   // dims 2 lane, 2 lane + 1 (256 words a position)
+    // the staging slots of this thread: i = tid + 256 k -> (jj, bi, tt), tt fastest (coalesced rows of sc)
+    const float *src[PER];
+    int lbk[PER], pbk[PER];
+    float ivk[PER], mxk[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        int i = tid + 256 * k, tt = i % AT_PVCH, bi = (i / AT_PVCH) % NB, jj = i / (AT_PVCH * NB);
+        int pb = pos0 + b0 + bi, lb = att_lo(pb, glob, win), r = (b0 + bi) * 16 + kvh * 4 + jj;
+        bool ok = bi < nbt;
+        pbk[k] = ok ? pb : -1; lbk[k] = ok ? lb : 1 << 30;
+        src[k] = sc + (size_t)(ok ? r : 0) * ctx - lb + tt;   // + p0 gives the entry of position p0 + tt
+        ivk[k] = ok ? inv[r] : 0.0f; mxk[k] = ok ? mx[r] : 0.0f;
+    }
+    auto fetch = [&](int p0, float *w) {
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            int p = p0 + (tid + 256 * k) % AT_PVCH;
+            w[k] = (p >= lbk[k] && p <= pbk[k]) ? dexp(src[k][p0] - mxk[k]) * ivk[k] : 0.0f;
+        }
+    };
+    float acc[NB][2];
+#pragma unroll
+    for (int bi = 0; bi < NB; bi++) acc[bi][0] = acc[bi][1] = 0.0f;
+    float wn[PER];
+    fetch(lo0, wn);
+    for (int p0 = lo0; p0 <= phi; p0 += AT_PVCH) {
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            int i = tid + 256 * k, tt = i % AT_PVCH, bi = (i / AT_PVCH) % NB, jj = i / (AT_PVCH * NB);
+            wl[jj][tt][bi] = wn[k];
+        }
+        __syncthreads();
+        if (p0 + AT_PVCH <= phi) fetch(p0 + AT_PVCH, wn);
+        int n = min(AT_PVCH, phi + 1 - p0);
+        const uint32_t *vr = vp + (size_t)p0 * 256;
 #pragma unroll 8
-    for (int t = 0; t < T; t++) o = __builtin_fmaf(p[t] * iv, __half2float(v[(size_t)t * 512]), o);
-    att[(size_t)b * MH + (kvh * 4 + j) * AT_HD + d] = o;
+        for (int tt = 0; tt < n; tt++) {
+            uint32_t h2 = vr[(size_t)tt * 256];
+            float v0 = __half2float(__ushort_as_half((unsigned short)(h2 & 0xffff)));
+            float v1 = __half2float(__ushort_as_half((unsigned short)(h2 >> 16)));
+#pragma unroll
+            for (int bi = 0; bi < NB; bi++) {
+                float w = wl[j][tt][bi];
+                acc[bi][0] = __builtin_fmaf(w, v0, acc[bi][0]);
+                acc[bi][1] = __builtin_fmaf(w, v1, acc[bi][1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int bi = 0; bi < NB; bi++)
+        if (bi < nbt) *(float2 *)(att + (size_t)(b0 + bi) * MH + (kvh * 4 + j) * AT_HD + 2 * lane) = make_float2(acc[bi][0], acc[bi][1]);
 }

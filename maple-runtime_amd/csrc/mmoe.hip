@@ -541,6 +541,7 @@ static int set_router(int L, const uint16_t *router);
 // gfull_attn runs rmsnorm -> q/k/v (k_dense) -> q/k norm + rope + fp16 cache -> attention -> o (x += o) ->
 // post-norm -> router logits (exact chains), and gfull_moe the experts of the pairs the host picked.
 // One sequence; the chunk's nb tokens sit at positions pos0 .. pos0+nb-1 of a cache of ctx positions.
+#define AT_SC_NB 2    // tokens per k_att_scores workgroup
 #define GF_NWL 4352   // per layer in the norms gfull_init receives: in_ln 2048 | post_ln 2048 | q_norm 128 | k_norm 128
 static struct {
     int ready, ctx, win, maxtok, pos0;
@@ -548,7 +549,7 @@ static struct {
     float *cs;                    // [ctx][32][2]
     __half *kc, *vc, *ko;         // [24][ctx][512] x 2, [24][maxtok][1024]
     uint16_t *ko_host;            // gfull_read's copy
-    float *qkv, *att, *sc, *inv;  // [maxtok][3072], [maxtok][2048], [maxtok * 16][ctx], [maxtok * 16]
+    float *qkv, *att, *sc, *inv, *mx;  // [maxtok][3072], [maxtok][2048], [maxtok * 16][ctx], [maxtok * 16] x 2
     double t_attn;
 } GF;
 
@@ -560,7 +561,7 @@ int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t 
     }
     if (GF.ready) {   // a second set-up replaces the first
         HC(hipFree(GF.nw)); HC(hipFree(GF.cs)); HC(hipFree(GF.kc)); HC(hipFree(GF.vc)); HC(hipFree(GF.ko));
-        HC(hipFree(GF.qkv)); HC(hipFree(GF.att)); HC(hipFree(GF.sc)); HC(hipFree(GF.inv)); free(GF.ko_host);
+        HC(hipFree(GF.qkv)); HC(hipFree(GF.att)); HC(hipFree(GF.sc)); HC(hipFree(GF.inv)); HC(hipFree(GF.mx)); free(GF.ko_host);
         GF.ready = 0;
     }
     std::vector<uint16_t> nw((size_t)24 * GF_NWL);
@@ -572,7 +573,7 @@ int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t 
     HC(hipMemset(GF.kc, 0, kvb)); HC(hipMemset(GF.vc, 0, kvb));
     GF.ko_host = (uint16_t *)malloc(kob);
     HC(hipMalloc(&GF.qkv, (size_t)maxtok * 3072 * 4)); HC(hipMalloc(&GF.att, (size_t)maxtok * MH * 4));
-    HC(hipMalloc(&GF.sc, (size_t)maxtok * 16 * ctx * 4)); HC(hipMalloc(&GF.inv, (size_t)maxtok * 16 * 4));
+    HC(hipMalloc(&GF.sc, (size_t)maxtok * 16 * ctx * 4)); HC(hipMalloc(&GF.inv, (size_t)maxtok * 16 * 4)); HC(hipMalloc(&GF.mx, (size_t)maxtok * 16 * 4));
     for (int L = 0; L < 24; L++) {
         if (set_router(L, router + (size_t)L * MNE * MH)) return -1;
         LayerW &lw = S.layers[L];
@@ -609,11 +610,17 @@ static int gfull_attn_launch(int L, int glob) {
         k_dense<DENSE_W><<<dim3(3072 / (64 * DENSE_W), (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, 3072, w.qx, w.qsx, w.qsumx, GF.qkv);
     })) return -1;
     if (launch(MMOE_K_QKN, [&] {
-        k_qkn<<<dim3(nb, 24), 64, 0, S.st>>>(GF.qkv, pos0, glob, nwl + 4096, nwl + 4224, GF.cs, kcl, vcl, kol);
+        k_qkn<<<nb, 256, 0, S.st>>>(GF.qkv, pos0, glob, nwl + 4096, nwl + 4224, GF.cs, kcl, vcl, kol, GF.mx);
     })) return -1;
-    if (launch(MMOE_K_ATT_SCORES, [&] { k_att_scores<<<nb * 4, 256, 0, S.st>>>(GF.qkv, pos0, glob, win, kcl, GF.sc, ctx); })) return -1;
-    if (launch(MMOE_K_ATT_SOFTMAX, [&] { k_att_softmax<<<nb * 16, 64, 0, S.st>>>(pos0, glob, win, GF.sc, GF.inv, ctx); })) return -1;
-    if (launch(MMOE_K_ATT_PV, [&] { k_att_pv<<<nb * 4, 512, 0, S.st>>>(pos0, glob, win, GF.sc, GF.inv, vcl, GF.att, ctx); })) return -1;
+    int span = glob ? pos0 + nb : std::min(pos0 + nb, win + AT_SC_NB);   // positions one token group can see
+    if (launch(MMOE_K_ATT_SCORES, [&] {
+        k_att_scores<AT_SC_NB><<<dim3((nb + AT_SC_NB - 1) / AT_SC_NB * 4, (span + 63) / 64), 64, 0, S.st>>>(GF.qkv, nb, pos0, glob, win, kcl, GF.sc, GF.mx, ctx);
+    })) return -1;
+    if (launch(MMOE_K_ATT_SOFTMAX, [&] { k_att_softmax<<<nb, 256, 0, S.st>>>(pos0, glob, win, GF.sc, GF.mx, GF.inv, ctx); })) return -1;
+    if (launch(MMOE_K_ATT_PV, [&] {   // small chunks: fewer tokens per workgroup, more workgroups
+        if (nb >= 1024) k_att_pv<4><<<(nb + 3) / 4 * 4, 256, 0, S.st>>>(nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
+        else k_att_pv<2><<<(nb + 1) / 2 * 4, 256, 0, S.st>>>(nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
+    })) return -1;
     if (stage_quant_x(w, GF.att, nb)) return -1;
     return launch(MMOE_K_DENSE, [&] {
         k_dense<DENSE_W, true><<<dim3(MH / (64 * DENSE_W), (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + (g + 1) * 3, DN.drbs + (g + 1) * 4, DN.n[g + 1], nb, MH, w.qx, w.qsx, w.qsumx, w.x);
