@@ -587,6 +587,7 @@ int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t 
 }
 // a new chunk: nb hidden vectors (embeddings) at positions pos0..
 void gfull_begin(const float *x, int nb, int pos0) {
+    S.gfull_nb = 0;   // a rejected chunk leaves no chunk: gfull_attn / gfull_moe then report it
     if (!S.gfull || nb < 1 || nb > S.main.maxtok) { seterr("gfull_begin: not set up or nb %d out of range", nb); return; }
     if (GF.ready && (nb > GF.maxtok || pos0 < 0 || pos0 + nb > GF.ctx)) { seterr("gfull_begin: positions %d..%d past ctx %d", pos0, pos0 + nb - 1, GF.ctx); return; }
     S.gfull_nb = nb; GF.pos0 = pos0;
@@ -644,7 +645,7 @@ double gfull_attn(int L, int glob, float *rl) {
 }
 // gpu_pre.m:508-566: asynchronous; adds each token's weighted expert outputs into the device hidden state
 void gfull_moe(int nu, const uint32_t *loc, const int *regs, const int *ustart, const int *ptok, const float *pw, const int *tp) {
-    if (!S.gfull) { seterr("gfull_moe: gfull state not set up"); return; }
+    if (!S.gfull || !S.gfull_nb) { seterr("gfull_moe: gfull state not set up (gfull_begin)"); return; }
     ExpPtr ep[MNE];
     if (nu < 1 || nu > MNE) { seterr("gfull_moe: nu %d", nu); return; }
     if (resolve_loc(loc, regs, nu, ep)) return;
@@ -841,6 +842,7 @@ int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order) {
 int mmoe_gfull_stack(int L0, int nl) {
     if (ctx_ready()) return -1;
     if (L0 < 0 || nl < 1 || L0 + nl > 24) { seterr("mmoe_gfull_stack: layers %d..%d outside 0..23", L0, L0 + nl - 1); return -1; }
+    if (!GF.ready || !S.gfull_nb) { seterr("mmoe_gfull_stack: gfull_init / gfull_begin first"); return -1; }
     for (int L = L0; L < L0 + nl; L++) {
         if (!S.layers[L].tab) { seterr("mmoe_gfull_stack: layer %d has no experts (mmoe_set_layer)", L); return -1; }
         if (gfull_attn_launch(L, (L % 4) == 3)) return -1;
@@ -908,7 +910,7 @@ int mmoe_gfull_setup(int maxtok) {
 }
 // The router stage of gfull_attn (gpu_full.metal rms + rtr): hn = rmsnorm(x, post_ln[L]), rl = router logits
 int mmoe_gfull_post_norm(int L, float *rl) {
-    if (!S.gfull || L < 0 || L >= NLMAX || !S.layers[L].router) { seterr("mmoe_gfull_post_norm: not set up / layer %d", L); return -1; }
+    if (!S.gfull || !S.gfull_nb || L < 0 || L >= NLMAX || !S.layers[L].router) { seterr("mmoe_gfull_post_norm: not set up (gfull_begin) / layer %d", L); return -1; }
     Work &w = S.main; int nb = S.gfull_nb;
     const uint16_t *pw = S.layers[L].post_ln;
     if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(w.x, pw, w.hn, nb); })) return -1;

@@ -39,7 +39,7 @@ def gfull_model():
             lib.gpre_dense_add(2 * L, M.ptr(packed), M.ptr(s), packed.shape[0], H)
         packed, s = al.mats["o"]
         lib.gpre_dense_add(2 * L + 1, M.ptr(packed), M.ptr(s), packed.shape[0], H)
-    M.check(lib.gpre_dense_done(MAXTOK), "gpre_dense_done")
+    M.check(lib.gpre_dense_done(2048), "gpre_dense_done")
     rng = np.random.default_rng(SEED + 41)
     post = [(np.asarray(rng.uniform(0.5, 1.5, H), np.float32).view(np.uint32) >> 16).astype(np.uint16) for _ in range(2)]
     routers = [M.synth_router(SEED, L, 0) for L in range(2)]
@@ -51,11 +51,11 @@ def gfull_model():
         router_all[L] = routers[L % 2]
     cs = O.rope_table(CTX)
     M.check(lib.gfull_init(CTX, MAXTOK, O.WIN, M.ptr(norms), M.ptr(router_all), M.ptr(cs)), "gfull_init")
-    return lib, layers, post, routers, cs
+    return lib, layers, post, routers, cs, norms, router_all
 
 
 def test_gfull_attn_matches_oracle(gfull_model):
-    lib, layers, post, routers, cs = gfull_model
+    lib, layers, post, routers, cs = gfull_model[:5]
     rng = np.random.default_rng(SEED + 42)
     kc = {L: np.zeros((CTX, 512), np.uint16) for L, _ in LAYERS}
     vc = {L: np.zeros((CTX, 512), np.uint16) for L, _ in LAYERS}
@@ -93,7 +93,7 @@ def test_gfull_whole_layers(gfull_model):
     the card's logits, gfull_moe; two chunks through layers 0 (local) and 3 (global). As maple.c's GFULL_CHECK
     (maple.c:940-1000) each layer is checked from the card's own input: the oracle's attention half, then its
     MoE block on rmsnorm(x, post_ln) with the same top-8."""
-    lib, layers, post, routers, cs = gfull_model
+    lib, layers, post, routers, cs = gfull_model[:5]
     blocks = [HostLayer(SEED, k) for k in range(2)]                  # experts of even / odd layers
     rids = [lib.gpre_region(M.ptr(h.blk), h.blk.nbytes) for h in blocks]
     assert min(rids) >= 0, lib.mmoe_last_error()
@@ -136,7 +136,7 @@ def test_gfull_stack_on_device(gfull_model):
     per layer with no host step between them. Layers 0..3 (3 is global) one at a time from the card's own input,
     against the oracle's attention half followed by its MoE block; chunks of 5 tokens (the decode kernels) and
     of 256 tokens at positions past the window."""
-    lib, layers, post, routers, cs = gfull_model
+    lib, layers, post, routers, cs = gfull_model[:5]
     blocks = [HostLayer(SEED, k) for k in range(2)]
     for L in range(4):
         M.register_layer(L, blocks[L % 2].blk, routers[L % 2], post[L % 2])
@@ -165,3 +165,31 @@ def test_gfull_stack_on_device(gfull_model):
             print(f"  top-8 equal {np.array_equal(top, o['top'])}, x bit-exact {np.array_equal(xg, xo)}, relmax {e:.1e}", flush=True)
             assert np.array_equal(np.sort(top, 1), np.sort(o["top"], 1))
             assert e <= 1e-5
+
+
+def test_gfull_attn_large_chunk(gfull_model):
+    """A 1030-token chunk (chunks of >= 1024 tokens use the 4-token groups of the weighted-sum kernel; 1030 leaves
+    a partial group) on a fresh 2048-token set-up, local and global layer, against the oracle."""
+    lib, layers, post, routers, cs, norms, router_all = gfull_model
+    ctx = 2048
+    cs = O.rope_table(ctx)
+    M.check(lib.gfull_init(ctx, 2048, O.WIN, M.ptr(norms), M.ptr(router_all), M.ptr(cs)), "gfull_init 2048")
+    rng = np.random.default_rng(SEED + 45)
+    nb, pos0 = 1030, 0
+    x0 = rng.standard_normal((nb, H)).astype(np.float32)
+    lib.gfull_begin(M.ptr(x0), nb, pos0)
+    assert not lib.mmoe_last_error().startswith(b"gfull_begin"), lib.mmoe_last_error()
+    for L, glob in LAYERS:
+        print(f"\n  nb={nb} layer {L} glob={glob}", flush=True)
+        lib.gfull_write_x(M.ptr(x0))
+        rl = np.empty((nb, 256), np.float32)
+        assert lib.gfull_attn(L, glob, M.ptr(rl)) >= 0, lib.mmoe_last_error()
+        x = np.empty((nb, H), np.float32)
+        kop = C.c_void_p()
+        lib.gfull_read(M.ptr(x), C.addressof(kop))
+        ko = np.ctypeslib.as_array((C.c_uint16 * (24 * 2048 * 1024)).from_address(kop.value)).reshape(24, 2048, 1024)[L, :nb]
+        kc = np.zeros((ctx, 512), np.uint16); vc = np.zeros((ctx, 512), np.uint16)
+        xo, ko_o, _ = O.attn_chunk(layers[L % 2], x0, pos0, glob, kc, vc, cs)
+        nx = int((x.view(np.uint32) != xo.view(np.uint32)).sum())
+        print(f"  differing: k/v {int((ko != ko_o).sum())}, x {nx}", flush=True)
+        assert np.array_equal(ko, ko_o) and nx == 0
