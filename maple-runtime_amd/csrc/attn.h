@@ -123,6 +123,7 @@ __global__ void __launch_bounds__(64) k_att_scores(const float *__restrict__ qkv
                 for (int l = 0; l < 8; l++) a[bi][j][l] = __builtin_fmaf(kf[l], qb[bi][j * AT_HD + d8 * 8 + l], a[bi][j][l]);
     }
     const float scale = 1.0f / sqrtf((float)AT_HD);
+    float mv[NB * 4];   // the 4 NB scores of this position, -1e30 outside a token's window
 #pragma unroll
     for (int bi = 0; bi < NB; bi++) {
         int pb = pos0 + b0 + bi, lb = att_lo(pb, glob, win);
@@ -131,10 +132,33 @@ __global__ void __launch_bounds__(64) k_att_scores(const float *__restrict__ qkv
         for (int j = 0; j < 4; j++) {
             float v = hsum8(a[bi][j]) * scale;
             if (in) sc[((size_t)(b0 + bi) * 16 + kvh * 4 + j) * ctx + p - lb] = v;
-            float m = wave_max(in ? v : -1e30f);
-            if (tid == 0 && bi < nbt) atomic_max_f32(mx + (b0 + bi) * 16 + kvh * 4 + j, m);
+            mv[bi * 4 + j] = in ? v : -1e30f;
         }
     }
+    // the maxima of the 8 rows (NB = 2) over the wave at once: lane-half swaps across lane bits 32 and 16 put
+    // row k of both halves into one register pair (the lower half keeps rows 0..h-1, the upper rows h..2h-1),
+    // then a rotation by 8 within 16-lane rows; then the maximum over each aligned group of 8 lanes
+    static_assert(NB == 2, "the row-maximum exchange is written for 8 rows");
+    int lane = tid & 63;
+    float m4[4], m2[2];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mv[k]), __float_as_uint(mv[4 + k]), false, false);
+        m4[k] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+        auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(m4[k]), __float_as_uint(m4[2 + k]), false, false);
+        m2[k] = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+    }
+    float t0 = fmaxf(m2[0], __int_as_float(dpp<0x128>(__float_as_int(m2[0]))));   // row_ror:8: lane i gets lane i ^ 8
+    float t1 = fmaxf(m2[1], __int_as_float(dpp<0x128>(__float_as_int(m2[1]))));
+    float m = (lane & 8) ? t1 : t0;
+    int r = ((lane >> 5) & 1) * 4 + ((lane >> 4) & 1) * 2 + ((lane >> 3) & 1);
+    m = fmaxf(m, __int_as_float(dpp<0xB1>(__float_as_int(m))));    // quad xor 1
+    m = fmaxf(m, __int_as_float(dpp<0x4E>(__float_as_int(m))));    // quad xor 2
+    m = fmaxf(m, __int_as_float(dpp<0x12C>(__float_as_int(m))));   // row_ror:12: lane i gets lane i + 4 of its 16-lane row
+    if ((lane & 7) == 0 && (r >> 2) < nbt) atomic_max_f32(mx + (b0 + (r >> 2)) * 16 + kvh * 4 + (r & 3), m);
 }
 
 // Softmax sums of the 16 rows (heads) of token b, one workgroup per token: p = exp(s - max) (max from
