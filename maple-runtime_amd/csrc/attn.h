@@ -196,16 +196,16 @@ __global__ void __launch_bounds__(256) k_att_softmax(int pos0, int glob, int win
 }
 
 // Output of a group of NB consecutive tokens for key/value head kvh (block = (group, kvh), groups with the
-// longest windows first): wave j is query head kvh * 4 + j, lane l dims 2l and 2l + 1. Per run of AT_PVCH
-// positions the weights w = exp(s - max) * inv of the group's tokens are staged in LDS (0 outside a token's window; the
+// longest windows first): wave j is query head kvh * 4 + j, lane l dims 2l and 2l + 1. Per run of positions
+// (512 / NB, at most 128) the weights w = exp(s - max) * inv of the group's tokens are staged in LDS (0 outside a token's window; the
 // next run's are loaded into registers while the current one is consumed) and each output is the FMA chain over
 // positions of w * v, into att[b][2048].
-#define AT_PVCH 128
 template <int NB>
 __global__ void __launch_bounds__(256) k_att_pv(int nb, int pos0, int glob, int win, const float *__restrict__ sc,
                                                 const float *__restrict__ mx, const float *__restrict__ inv, const __half *__restrict__ vc,
                                                 float *__restrict__ att, int ctx) {
-    constexpr int PER = 4 * NB * AT_PVCH / 256;   // staged weights per thread
+    constexpr int AT_PVCH = NB >= 4 ? 512 / NB : 128;   // positions per staged run
+    constexpr int PER = 4 * NB * AT_PVCH / 256;       // staged weights per thread (8, or 4 for NB = 2)
     __shared__ __attribute__((aligned(16))) float wl[4][AT_PVCH][NB];
     int ngrp = (nb + NB - 1) / NB;
     int grp = ngrp - 1 - (int)(blockIdx.x >> 2), kvh = blockIdx.x & 3;

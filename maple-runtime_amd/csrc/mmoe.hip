@@ -619,7 +619,7 @@ static int gfull_attn_launch(int L, int glob) {
     })) return -1;
     if (launch(MMOE_K_ATT_SOFTMAX, [&] { k_att_softmax<<<nb, 256, 0, S.st>>>(pos0, glob, win, GF.sc, GF.mx, GF.inv, ctx); })) return -1;
     if (launch(MMOE_K_ATT_PV, [&] {   // small chunks: fewer tokens per workgroup, more workgroups
-        if (nb >= 1024) k_att_pv<4><<<(nb + 3) / 4 * 4, 256, 0, S.st>>>(nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
+        if (nb > 256) k_att_pv<4><<<(nb + 3) / 4 * 4, 256, 0, S.st>>>(nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
         else k_att_pv<2><<<(nb + 1) / 2 * 4, 256, 0, S.st>>>(nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
     })) return -1;
     if (stage_quant_x(w, GF.att, nb)) return -1;

@@ -167,15 +167,16 @@ def test_gfull_stack_on_device(gfull_model):
             assert e <= 1e-5
 
 
-def test_gfull_attn_large_chunk(gfull_model):
-    """A 1030-token chunk (chunks of >= 1024 tokens use the 4-token groups of the weighted-sum kernel; 1030 leaves
-    a partial group) on a fresh 2048-token set-up, local and global layer, against the oracle."""
+@pytest.mark.parametrize("nb,pos0", [(1030, 0), (602, 700)])
+def test_gfull_attn_large_chunk(gfull_model, nb, pos0):
+    """Chunks of 1030 tokens at position 0 and 602 tokens at 700 (above 256 tokens the weighted-sum kernel takes
+    4-token groups; both sizes leave a partial group) on a fresh 2048-position set-up, local and global layer,
+    against the oracle."""
     lib, layers, post, routers, cs, norms, router_all = gfull_model
     ctx = 2048
     cs = O.rope_table(ctx)
     M.check(lib.gfull_init(ctx, 2048, O.WIN, M.ptr(norms), M.ptr(router_all), M.ptr(cs)), "gfull_init 2048")
-    rng = np.random.default_rng(SEED + 45)
-    nb, pos0 = 1030, 0
+    rng = np.random.default_rng(SEED + 45 + nb)
     x0 = rng.standard_normal((nb, H)).astype(np.float32)
     lib.gfull_begin(M.ptr(x0), nb, pos0)
     assert not lib.mmoe_last_error().startswith(b"gfull_begin"), lib.mmoe_last_error()
@@ -188,7 +189,7 @@ def test_gfull_attn_large_chunk(gfull_model):
         kop = C.c_void_p()
         lib.gfull_read(M.ptr(x), C.addressof(kop))
         ko = np.ctypeslib.as_array((C.c_uint16 * (24 * 2048 * 1024)).from_address(kop.value)).reshape(24, 2048, 1024)[L, :nb]
-        kc = np.zeros((ctx, 512), np.uint16); vc = np.zeros((ctx, 512), np.uint16)
+        kc = np.zeros((ctx, 512), np.uint16); vc = np.zeros((ctx, 512), np.uint16)   # positions before pos0: zeros on both sides
         xo, ko_o, _ = O.attn_chunk(layers[L % 2], x0, pos0, glob, kc, vc, cs)
         nx = int((x.view(np.uint32) != xo.view(np.uint32)).sum())
         print(f"  differing: k/v {int((ko != ko_o).sum())}, x {nx}", flush=True)
