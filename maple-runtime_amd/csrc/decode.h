@@ -177,17 +177,19 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     __shared__ int qsum_l[DEC_MAXTOK];
     __shared__ int sums[2][8][DEC_MAXTOK];
     __shared__ float sgu[2][8];
-    __shared__ ExpPtr tab[MNE];
+    __shared__ __attribute__((aligned(16))) ExpPtr tab[MNE];
     int t = threadIdx.x, wv = t >> 6, l = t & 63;
     DEC_TS(18, blockIdx.x == 3 && blockIdx.y == 1);
-    ExpPtr my = layer_tab[t];                         // the layer's expert table, stored to LDS after top-8
+    static_assert(sizeof(ExpPtr) == 48, "ExpPtr: 6 pointers");
+    const v4i *ltp = (const v4i *)(layer_tab + t);   // the layer's expert table, stored to LDS after top-8 (three
+    v4i my0 = ltp[0], my1 = ltp[1], my2 = ltp[2];     // vectors: held as a struct it went to scratch memory)
 
     // top-8 of every token and the int8 quantisation (maple.c:908-909 prep) of every token, spread over waves
     for (int it = wv; it < 2 * nb; it += 4) {
         if (it < nb) topk_wave(rl + (size_t)it * MNE, E[wv], l, R.top + it * MTOPK, R.tw + it * MTOPK);
         else quant_wave<MH, DEC_GS - 128>(hn + (size_t)(it - nb) * MH, l, qs_l[it - nb], &qsv_l[it - nb], &qsum_l[it - nb]);
     }
-    tab[t] = my;
+    { v4i *tp4 = (v4i *)(tab + t); tp4[0] = my0; tp4[1] = my1; tp4[2] = my2; }
     __syncthreads();
     DEC_TS(19, blockIdx.x == 3 && blockIdx.y == 1);
     dec_group_block(nb, R);
