@@ -56,14 +56,23 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
     int l = threadIdx.x, j = l % NCH, e = blockIdx.x * (64 / NCH) + l / NCH;
     DEC_SPAN(0);
     DEC_TS(2, blockIdx.x == 5);
+    // token 0's x and the norm weights first, the router weights after them: loads return in issue order, so
+    // the norm need not wait for the router weights (the scheduling barrier keeps that order)
+    float4 x0[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) x0[i] = *(const float4 *)(x + 4 * l + 256 * i);
+    uint2 pw[8];                                      // post_ln at columns 4l + 256i + 0..3
+#pragma unroll
+    for (int i = 0; i < 8; i++) pw[i] = (do_norm && post_ln) ? *(const uint2 *)(post_ln + 4 * l + 256 * i) : make_uint2(0x3f803f80u, 0x3f803f80u);
+    __builtin_amdgcn_sched_barrier(0);
     const gptr_u4 *wp = (const gptr_u4 *)(wc + ((size_t)e * NCH + j) * LEN);
     v4i wv[LEN / 8];
 #pragma unroll
     for (int i = 0; i < LEN / 8; i++) wv[i] = wp[i];
-    float lw[32];                                     // post_ln at columns 4l + 256i + 0..3
+    float lw[32];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        uint2 pv = (do_norm && post_ln) ? *(const uint2 *)(post_ln + 4 * l + 256 * i) : make_uint2(0x3f803f80u, 0x3f803f80u);
+        uint2 pv = pw[i];
         lw[4 * i] = bf16f(pv.x & 0xffff); lw[4 * i + 1] = bf16f(pv.x >> 16); lw[4 * i + 2] = bf16f(pv.y & 0xffff); lw[4 * i + 3] = bf16f(pv.y >> 16);
     }
     float bv = bias && j == 0 ? bias[e] : 0.0f;
@@ -72,7 +81,7 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
         float v[32]; double ss = 0.0;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            float4 f = *(const float4 *)(xb + 4 * l + 256 * i);
+            float4 f = b == 0 ? x0[i] : *(const float4 *)(xb + 4 * l + 256 * i);
             v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
         }
         if (do_norm) {
@@ -141,11 +150,23 @@ __device__ void dec_group_block(int nb, DecRoute &R) {
     int t = threadIdx.x, P = nb * MTOPK;
     if (t < 64) {                                     // one wave, lane i = pair i (P <= 64)
         int i = t, e = i < P ? R.top[i] : 0x7fffffff, cl = 0, ce = 0;
-        for (int j = 0; j < P; j++) { int ej = R.top[j]; cl += ej < e; ce += (j < i) & (ej == e); }
+        for (int j0 = 0; j0 < P; j0 += MTOPK) {       // P is a multiple of 8: 8 LDS reads issued together
+            int ej[MTOPK];
+#pragma unroll
+            for (int k = 0; k < MTOPK; k++) ej[k] = R.top[j0 + k];
+#pragma unroll
+            for (int k = 0; k < MTOPK; k++) { cl += ej[k] < e; ce += (j0 + k < i) & (ej[k] == e); }
+        }
         bool first = i < P && ce == 0;
         unsigned long long fm = __ballot(first);
         int du = 0;
-        for (int j = 0; j < P; j++) du += (int)((fm >> j) & 1) & (R.top[j] < e);
+        for (int j0 = 0; j0 < P; j0 += MTOPK) {
+            int ej[MTOPK];
+#pragma unroll
+            for (int k = 0; k < MTOPK; k++) ej[k] = R.top[j0 + k];
+#pragma unroll
+            for (int k = 0; k < MTOPK; k++) du += (int)((fm >> (j0 + k)) & 1) & (ej[k] < e);
+        }
         int slot = cl + ce;                           // experts ascending, tokens ascending within one
         if (first) { R.ue[du] = e; R.ustart[du] = cl; }
         if (i == 0) { R.nu = popc64(fm); R.ustart[popc64(fm)] = P; }
@@ -283,13 +304,26 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
     ActChunk c0;
     act_load(act, 2 * wv + (l >> 5), l, c0);          // first act vectors, issued before anything else
     int nu = plan->nu;
-    const uint8_t *dcp[DEC_DU]; const float *dsp[DEC_DU];
-#pragma unroll
-    for (int k = 0; k < DEC_DU; k++) { int u = wv + 4 * k; dcp[k] = eptr[u].dc; dsp[k] = eptr[u].ds; }
+    // expert pointers through scalar loads (the wave index made provably uniform), so the code loads that use
+    // them wait on those loads only and not on the act loads issued before
+    int wvu = __builtin_amdgcn_readfirstlane(wv);
     v4i cv[DEC_DU]; float sd[DEC_DU];
+    // the first two experts of the wave (all of them for one token, nu <= 8) unconditionally, a slot past nu
+    // reading expert 0's rows instead (never used), so the pointer and code loads are issued back to back
+    const uint8_t *dc0 = eptr[0].dc; const float *ds0 = eptr[0].ds;
 #pragma unroll
-    for (int k = 0; k < DEC_DU; k++)
-        if (wv + 4 * k < nu) { cv[k] = *(const gptr_u4 *)(dcp[k] + (size_t)row * (MFF / 4) + sl * 16); sd[k] = dsp[k][row]; }
+    for (int k = 0; k < 2; k++) {   // entry and plan->nu loaded together, the pointer picked after
+        const uint8_t *dc = eptr[wvu + 4 * k].dc; const float *ds = eptr[wvu + 4 * k].ds;
+        bool live = wvu + 4 * k < nu;
+        dc = live ? dc : dc0; ds = live ? ds : ds0;
+        cv[k] = *(const gptr_u4 *)(dc + (size_t)row * (MFF / 4) + sl * 16); sd[k] = ds[row];
+    }
+#pragma unroll
+    for (int k = 2; k < DEC_DU; k++)
+        if (wvu + 4 * k < nu) {
+            const ExpPtr &ep = eptr[wvu + 4 * k];
+            cv[k] = *(const gptr_u4 *)(ep.dc + (size_t)row * (MFF / 4) + sl * 16); sd[k] = ep.ds[row];
+        }
     for (int k = 0; k < nb; k++) {
         int a = 8 * k + 2 * wv + (l >> 5);
         if (k > 0) act_load(act, a, l, c0);
