@@ -202,15 +202,29 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
     __shared__ double red[NORM ? 256 : 1];
     __shared__ float kk;
     int tid = threadIdx.x, b = blockIdx.y, j = tid % NCH, e = blockIdx.x * (256 / NCH) + tid / NCH;
+    const float *xr = in + (size_t)b * MH;
+    float xv[8];
+    uint32_t pw[8];   // bf16 bits, one per register (no packing between the loads and the barrier)
+    if (NORM) {   // the token's x and norm weights first: loads return in issue order, so the norm need not
+#pragma unroll    // wait for the router weights issued after them (the scheduling barrier keeps that order)
+        for (int i = 0; i < 8; i++) xv[i] = xr[tid + i * 256];
+        if (post_ln) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) pw[i] = post_ln[tid + i * 256];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) pw[i] = 0x3f80;   // bf16 1.0
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
     const gptr_u4 *wp = (const gptr_u4 *)(wc + ((size_t)e * NCH + j) * LEN);
     v4i wv[16];
 #pragma unroll
     for (int q = 0; q < 16; q++) wv[q] = wp[q];
-    const float *xr = in + (size_t)b * MH;
     if (NORM) {
-        float v[8]; double sq = 0.0;
+        double sq = 0.0;
 #pragma unroll
-        for (int i = 0; i < 8; i++) { v[i] = xr[tid + i * 256]; sq += (double)v[i] * (double)v[i]; }
+        for (int i = 0; i < 8; i++) sq += (double)xv[i] * (double)xv[i];
         red[tid] = sq;
         __syncthreads();
         for (int o = 128; o > 0; o >>= 1) { if (tid < o) red[tid] += red[tid + o]; __syncthreads(); }
@@ -220,8 +234,8 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             int c = tid + i * 256;
-            float wn = post_ln ? bf16f(post_ln[c]) : 1.0f;
-            float h = v[i] * k * wn;
+            float wn = __uint_as_float(pw[i] << 16);
+            float h = xv[i] * k * wn;
             hc[(c % NCH) * HP + c / NCH] = h;
             if (blockIdx.x == 0) hn_out[(size_t)b * MH + c] = h;
         }
