@@ -307,6 +307,21 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
     // expert pointers through scalar loads (the wave index made provably uniform), so the code loads that use
     // them wait on those loads only and not on the act loads issued before
     int wvu = __builtin_amdgcn_readfirstlane(wv);
+    // the combine's inputs (thread (token, row) < nb * 8): the hidden-state value and the token's 8 pair ids and
+    // weights, loaded now so the combine at the end waits for nothing
+    int cb = t >> 3, cr8 = t & 7, ca[MTOPK]; float cw[MTOPK], cx = 0.0f;
+    float *cxp = x + (size_t)cb * MH + r0 + cr8;
+    if (t < nb * 8) {
+        cx = *cxp;
+#pragma unroll
+        for (int jj = 0; jj < MTOPK; jj++) {
+            ca[jj] = (mode & 2) ? sp[cb * MTOPK + jj] : tp[cb * MTOPK + jj];
+            cw[jj] = (mode & 2) ? tw[cb * MTOPK + jj] : uw[ca[jj]];
+        }
+    }
+    int us0[2], us1[2];   // ustart of the wave's first two experts (scalar loads; clamped like the pointers)
+#pragma unroll
+    for (int k = 0; k < 2; k++) { us0[k] = plan->ustart[wvu + 4 * k]; us1[k] = plan->ustart[wvu + 4 * k + 1]; }
     v4i cv[DEC_DU]; float sd[DEC_DU];
     // the first two experts of the wave (all of them for one token, nu <= 8) unconditionally, a slot past nu
     // reading expert 0's rows instead (never used), so the pointer and code loads are issued back to back
@@ -338,11 +353,11 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
         }
 #pragma unroll
     for (int k = 0; k < DEC_DU; k++) {
-        int u = wv + 4 * k;
+        int u = wvu + 4 * k;
         if (u >= nu) break;
         uint32_t cd[16];
         decode4((uint32_t)cv[k].x, cd); decode4((uint32_t)cv[k].y, cd + 4); decode4((uint32_t)cv[k].z, cd + 8); decode4((uint32_t)cv[k].w, cd + 12);
-        int a0 = plan->ustart[u], a1 = plan->ustart[u + 1];
+        int a0 = k < 2 ? us0[k] : plan->ustart[u], a1 = k < 2 ? us1[k] : plan->ustart[u + 1];
         for (int a = a0; a < a1; a++) {
             const uint32_t *qd = (const uint32_t *)(&qa[a][(sl >> 1) * DEC_GS + (sl & 1) * 64]);
             int acc = dot16(cd, qd, 0);
@@ -359,16 +374,11 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
     __syncthreads();
     DEC_TS(36, blockIdx.x == 7);
     if (t < nb * 8) {
-        int b = t >> 3, r8 = t & 7;
-        float *xp = x + (size_t)b * MH + r0 + r8;
-        float acc = (mode & 1) ? *xp : 0.0f;
-        for (int j = 0; j < MTOPK; j++) {
-            int a = (mode & 2) ? sp[b * MTOPK + j] : tp[b * MTOPK + j];
-            float wgt = (mode & 2) ? tw[b * MTOPK + j] : uw[a];
-            acc = __builtin_fmaf(wgt, Dl[a][r8], acc);
-        }
-        if (mode & 4) acc = *xp + acc;
-        *xp = acc;
+        float acc = (mode & 1) ? cx : 0.0f;
+#pragma unroll
+        for (int jj = 0; jj < MTOPK; jj++) acc = __builtin_fmaf(cw[jj], Dl[ca[jj]][cr8], acc);
+        if (mode & 4) acc = cx + acc;
+        *cxp = acc;
     }
     DEC_TS(37, blockIdx.x == 7);
 }
