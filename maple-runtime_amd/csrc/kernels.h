@@ -1663,23 +1663,54 @@ __global__ void __launch_bounds__(256) k_combine16(const int16_t *__restrict__ d
         for (int i = 0; i < 8; i++) acc[i] = 0.0f;
     }
     __syncthreads();
-    uint4 dv[MTOPK];
+    // the 8 pairs in two groups of 4, each group's loads issued together (the barrier keeps the second group's
+    // loads from being hoisted: about 80 VGPRs, so three waves share a SIMD instead of one)
 #pragma unroll
-    for (int j = 0; j < MTOPK; j++) dv[j] = *(const uint4 *)(down + (size_t)sa[j] * MH + c);
+    for (int jg = 0; jg < MTOPK; jg += 4) {
+        uint4 dv[4];
+        float4 s0[4], s1[4];
 #pragma unroll
-    for (int j = 0; j < MTOPK; j++) {
-        const float *ds = sds[j] + c;
-        float4 s0 = *(const float4 *)ds, s1 = *(const float4 *)(ds + 4);
-        float sdv[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
-        uint32_t wd[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
-        float qs = sq[j], wgt = sw[j];
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            int d = (int16_t)(wd[i >> 1] >> (16 * (i & 1)));
-            if (d == -32768) d = dov[(size_t)sa[j] * MH + c + i];
-            float D = (float)d * qs * sdv[i];
-            acc[i] = __builtin_fmaf(wgt, D, acc[i]);
+        for (int jj = 0; jj < 4; jj++) {
+            dv[jj] = *(const uint4 *)(down + (size_t)sa[jg + jj] * MH + c);
+            const float *ds = sds[jg + jj] + c;
+            s0[jj] = *(const float4 *)ds; s1[jj] = *(const float4 *)(ds + 4);
         }
+        bool ovf = false;   // any -32768 marker (its d is in dov): rare, handled by a compact loop
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) {
+            uint32_t w4[4] = {dv[jj].x, dv[jj].y, dv[jj].z, dv[jj].w};
+#pragma unroll
+            for (int k = 0; k < 4; k++) ovf |= ((w4[k] & 0xffffu) == 0x8000u) | ((w4[k] >> 16) == 0x8000u);
+        }
+        if (!ovf) {
+#pragma unroll
+            for (int jj = 0; jj < 4; jj++) {
+                int j = jg + jj;
+                float sdv[8] = {s0[jj].x, s0[jj].y, s0[jj].z, s0[jj].w, s1[jj].x, s1[jj].y, s1[jj].z, s1[jj].w};
+                uint32_t wd[4] = {dv[jj].x, dv[jj].y, dv[jj].z, dv[jj].w};
+                float qs = sq[j], wgt = sw[j];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    int d = (int16_t)(wd[i >> 1] >> (16 * (i & 1)));
+                    acc[i] = __builtin_fmaf(wgt, (float)d * qs * sdv[i], acc[i]);
+                }
+            }
+        } else {   // the same operations in the same order, reading the int16 and scale values again
+#pragma unroll 1
+            for (int jj = 0; jj < 4; jj++) {
+                int j = jg + jj;
+                const int16_t *dr = down + (size_t)sa[j] * MH + c;
+                const float *ds = sds[j] + c;
+                float qs = sq[j], wgt = sw[j];
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    int d = dr[i];
+                    if (d == -32768) d = dov[(size_t)sa[j] * MH + c + i];
+                    acc[i] = __builtin_fmaf(wgt, (float)d * qs * ds[i], acc[i]);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
     }
     if (mode & 4) {
         float4 x0 = *(const float4 *)xp, x1 = *(const float4 *)(xp + 4);

@@ -295,3 +295,39 @@ def test_full_size_tokens_independent(zipf_layer, T):
         print(f"\n  T={T}: halves and sample bit-exact; sample vs oracle bit-exact {np.array_equal(xf[idx], xo)}")
     finally:
         M.check(lib.mmoe_set_debug(1), "debug on")
+
+
+def test_combine_int16_overflow():
+    """Down results past int16 (the -32768 marker and the int32 side buffer): expert 5 of a layer gets gate, up and
+    down codes all +1 and a large router bias, so every token routes to it; with positive inputs its gate and up
+    clamp at 7, every act value quantises to 127 and each down sum is 512 x 127 = 65024. Checks off (int16 down
+    results into k_combine16): x against the oracle."""
+    lib = M.lib()
+    M.check(lib.mmoe_init(2048), "mmoe_init")
+    L, e = 7, 5
+    blk = M.synth_layer_block(SEED, L)
+    base = e * M.EXPERT_BYTES
+    for m in (0, 2, 4):   # gate codes, up codes, down codes: bytes 0xAA = four codes 2 (w = +1)
+        off = base + M.EXPERT_OFFS[m]
+        blk[off:off + 262144] = 0xAA
+    router = M.synth_router(SEED, L, 0)
+    rid = M.register_layer(L, blk, router)
+    bias = np.zeros(256, np.float32); bias[e] = 100.0
+    M.check(lib.mmoe_set_bias(L, M.ptr(bias)), "bias")
+    M.check(lib.mmoe_set_debug(0), "debug off")
+    try:
+        nb = 256
+        rng = np.random.default_rng(SEED + 5)
+        hn = np.abs(rng.standard_normal((nb, 2048))).astype(np.float32)
+        x = rng.standard_normal((nb, 2048)).astype(np.float32)
+        xg = run_gpu(L, hn, x, M.ORDER_BATCH)
+        xo = x.copy()
+        o = O.moe_batch(hn, router, O.experts_table(blk), xo, bias=bias, want=("top", "qa", "dn_i32"))
+        assert (o["top"] == e).any(axis=1).all(), "every token routes to the all-ones expert"
+        big = int((np.abs(o["dn_i32"].astype(np.int64) - o["qa"].astype(np.int64).sum(1, keepdims=True)) > 32767).sum())
+        print(f"\n  down sums past int16: {big}; x bit-exact {np.array_equal(xg, xo)}, relmax {relmax(xg - x, xo - x):.1e}")
+        assert big > 0
+        assert relmax(xg - x, xo - x) <= TOL
+    finally:
+        M.check(lib.mmoe_set_debug(1), "debug on")
+        M.check(lib.mmoe_set_bias(L, None), "bias off")
