@@ -209,7 +209,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(json.dumps({"error": "this build measures one GPU only: the MoE path of one MI355X; "
-                                   "multi-GPU sharding is a design note (DESIGN.md), run with --gpus 1"}))
+                                   "multi-GPU sharding is a design note only; run with --gpus 1"}))
         sys.exit(2)
     lib = M.lib()
     M.check(lib.mmoe_init(2048), "mmoe_init")

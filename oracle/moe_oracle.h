@@ -130,7 +130,7 @@ void mo_moe_step(const float *hn, const uint16_t *router, const float *bias, con
 void mo_experts_grouped(const float *hn, int nb, int nu, const mo_expert *ex, const int32_t *ustart,
                         const int32_t *utok, const float *uw, const int32_t *tp, float *y, mo_trace *tr);
 
-/* ---- attention half of a layer (SURVEY §8f-4; maple.c step_batch CPU path, 706-724) ----
+/* ---- attention half of a layer (maple.c step_batch CPU path, 706-724) ----
  * Pinning: mo_rope / mo_f16 bit-exact against maple.c's rope / to_f16 (oracle/_ref); mo_attend and
  * mo_attn_chunk within 1e-6 of maple.c's attend_group / step_batch (its -ffast-math build vectorises the
  * softmax loop with libmvec's expf; this restatement fixes one order, with mo_exp). */
