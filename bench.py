@@ -184,9 +184,17 @@ def full_prefill(lib, rids, args):
             f"kernel time attention half {att:.2f} ms, MoE {tot - att:.2f} ms")
         for k, (tt, n) in sorted(fk.items(), key=lambda kv: -kv[1][0]):
             log(f"  {k:12s} {tt / n * 1e3:8.2f} us avg x {n}")
+        # scores and weighted sum: 16 heads x 128 dims x (window length) fp32 FMAs per token each, in maple.c's
+        # order (no MFMA); averaged over the 24 layers (every fourth global, the rest a 512-position window)
+        pos = np.arange(pos0, pos0 + T)
+        win_len = {0: np.minimum(pos, 512) + 1, 1: pos + 1}
+        fma = sum(16 * 128 * int(win_len[int(L % 4 == 3)].sum()) for L in range(NL)) / NL
+        fma_peak = 256 * 4 * 16 * 2.4e9   # fp32 FMA without packed operations
+        frac = {k: round(fma / (fk[k][0] / fk[k][1] * 1e-3) / fma_peak, 4) for k in ("att_scores", "att_pv") if k in fk}
         key = "first_chunk" if pos0 == 0 else "second_chunk"
         out[key] = dict(pos0=pos0, value=round(T / fms * 1e3, 1), ms_per_chunk=round(fms, 3),
                         attention_ms=round(att, 3), moe_ms=round(tot - att, 3),
+                        attention_fma_per_layer=int(fma), attention_frac_fp32_fma_peak=frac,
                         kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in fk.items()})
     lib.gfull_read(None, None)
     return out, dense
