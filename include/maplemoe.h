@@ -84,7 +84,8 @@ int mmoe_dense_reset(void);
  * head norms, rope unless glob, cache, causal attention over the window win (all positions when glob), o,
  * x += o), then post-norm and the router: rl gets nb x 256 logits; synchronous, returns device seconds (-1.0 on
  * error). gfull_moe adds the experts of the host's grouping into x (asynchronous). gfull_read waits, copies x
- * back and sets *ko to the chunk's fp16 k | v of every layer ([24][gfull_maxtok()][1024]). Results: k, v, x
+ * back and sets *ko to the chunk's fp16 k | v of every layer ([24][gfull_maxtok()][1024]; rows 0..nb-1 of each
+ * layer are the chunk's, the rest are not refreshed). Results: k, v, x
  * after attention and the logits equal maple.c's CPU statements bit for bit. */
 int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t *router, const float *cs);
 void gfull_begin(const float *x, int nb, int pos0);

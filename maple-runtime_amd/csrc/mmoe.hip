@@ -659,7 +659,11 @@ void gfull_read(float *x, const uint16_t **ko) {
     if (x && S.gfull) HCV(hipMemcpy(x, S.main.x, (size_t)S.gfull_nb * MH * 4, hipMemcpyDeviceToHost));
     if (ko) {
         *ko = NULL;
-        if (GF.ready) { HCV(hipMemcpy(GF.ko_host, GF.ko, (size_t)24 * GF.maxtok * 1024 * 2, hipMemcpyDeviceToHost)); *ko = GF.ko_host; }
+        if (GF.ready) {   // the chunk's nb rows of every layer only (the [24][maxtok][1024] layout is kept)
+            size_t pitch = (size_t)GF.maxtok * 1024 * 2, rows = (size_t)(S.gfull_nb ? S.gfull_nb : GF.maxtok) * 1024 * 2;
+            HCV(hipMemcpy2D(GF.ko_host, pitch, GF.ko, pitch, rows, 24, hipMemcpyDeviceToHost));
+            *ko = GF.ko_host;
+        }
     }
 }
 void gfull_write_x(const float *x) {
