@@ -402,13 +402,14 @@ double gpre_moe(const float *x, int nb, int nu, const uint32_t *loc, const int *
     if (nu < 1 || nu > MNE || resolve_loc(loc, regs, nu, ep)) { if (nu < 1 || nu > MNE) seterr("gpre_moe: nu %d", nu); return -1.0; }
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { seterr("gpre_moe: event"); return -1.0; }
+    auto fail = [&] { (void)hipEventDestroy(a); (void)hipEventDestroy(b); return -1.0; };
     (void)hipEventRecord(a, S.st);
-    if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_moe: copy x"); return -1.0; }
-    if (experts_host_grouping(w, nb, nu, ep, ustart, ptok, pw, tp)) return -1.0;
-    if (stage_combine(w, nb, w.x, MMOE_COMBINE_OVERWRITE)) return -1.0;
+    if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_moe: copy x"); return fail(); }
+    if (experts_host_grouping(w, nb, nu, ep, ustart, ptok, pw, tp)) return fail();
+    if (stage_combine(w, nb, w.x, MMOE_COMBINE_OVERWRITE)) return fail();
     (void)hipEventRecord(b, S.st);
     if (hipMemcpyAsync(y, w.x, (size_t)nb * MH * 4, hipMemcpyDeviceToHost, S.st) != hipSuccess || hipStreamSynchronize(S.st) != hipSuccess) {
-        seterr("gpre_moe: %s", hipGetErrorString(hipGetLastError())); return -1.0;
+        seterr("gpre_moe: %s", hipGetErrorString(hipGetLastError())); return fail();
     }
     float ms = 0; (void)hipEventElapsedTime(&ms, a, b);
     (void)hipEventDestroy(a); (void)hipEventDestroy(b);
@@ -513,15 +514,16 @@ double gpre_dense(int g, const float *x, int nb, float *y) {
     int ys = DN.rows[g], nrb = ys / (64 * DENSE_W);
     hipEvent_t a, b;
     if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { seterr("gpre_dense: event"); return -1.0; }
+    auto fail = [&] { (void)hipEventDestroy(a); (void)hipEventDestroy(b); return -1.0; };
     (void)hipEventRecord(a, S.st);
-    if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_dense: copy x"); return -1.0; }
-    if (stage_quant_x(w, w.hn, nb)) return -1.0;
+    if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_dense: copy x"); return fail(); }
+    if (stage_quant_x(w, w.hn, nb)) return fail();
     if (launch(MMOE_K_DENSE, [&] {
             k_dense<DENSE_W><<<dim3(nrb, (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, ys, w.qx, w.qsx, w.qsumx, DN.y);
-        })) return -1.0;
+        })) return fail();
     (void)hipEventRecord(b, S.st);
     if (hipMemcpyAsync(y, DN.y, (size_t)nb * ys * 4, hipMemcpyDeviceToHost, S.st) != hipSuccess || hipStreamSynchronize(S.st) != hipSuccess) {
-        seterr("gpre_dense: %s", hipGetErrorString(hipGetLastError())); return -1.0;
+        seterr("gpre_dense: %s", hipGetErrorString(hipGetLastError())); return fail();
     }
     float ms = 0; (void)hipEventElapsedTime(&ms, a, b);
     (void)hipEventDestroy(a); (void)hipEventDestroy(b);

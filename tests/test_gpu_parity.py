@@ -297,6 +297,37 @@ def test_full_size_tokens_independent(zipf_layer, T):
         M.check(lib.mmoe_set_debug(1), "debug on")
 
 
+def test_rejects_sizes_outside_capacity(layer0):
+    """Sizes outside what mmoe_init / gpux_init allocated are refused on the host with an error and no device
+    work (maple.c never calls these hooks with an empty chunk; the refusal is this library's contract), and
+    the library stays usable: a valid call afterwards still matches the oracle."""
+    lib = M.lib()
+    x, hn = normed_hidden(SEED, 902, 2)
+    x_in = x.copy()
+    for nb in (0, -1, 2049):
+        assert lib.mmoe_moe(0, M.ptr(hn), nb, M.ptr(x), M.ORDER_BATCH) == -1
+        assert b"outside" in lib.mmoe_last_error(), lib.mmoe_last_error()
+    assert lib.mmoe_moe(-1, M.ptr(hn), 2, M.ptr(x), M.ORDER_BATCH) == -1
+    assert lib.mmoe_moe(64, M.ptr(hn), 2, M.ptr(x), M.ORDER_BATCH) == -1      # past the 64 layer slots
+    assert np.array_equal(x, x_in), "a refused call wrote the hidden state"
+    # gpre_moe: an empty chunk, and a pair whose token lies outside the chunk
+    ustart = np.array([0, 8], np.int32); utok = np.zeros(8, np.int32); uw = np.full(8, 0.125, np.float32)
+    tp = np.tile(np.arange(8, dtype=np.int32), 2)
+    loc = M.block_loc(0, [5]); regs = np.array([layer0.rid, -1, -1, -1], np.int32)
+    y = np.zeros((2, 2048), np.float32)
+    assert lib.gpre_moe(M.ptr(hn), 0, 1, M.ptr(loc), M.ptr(regs), None, M.ptr(ustart), M.ptr(utok), M.ptr(uw),
+                        M.ptr(tp), M.ptr(y)) < 0
+    bad = utok.copy(); bad[3] = 2
+    assert lib.gpre_moe(M.ptr(hn), 2, 1, M.ptr(loc), M.ptr(regs), None, M.ptr(ustart), M.ptr(bad), M.ptr(uw),
+                        M.ptr(tp), M.ptr(y)) < 0
+    assert b"ptok" in lib.mmoe_last_error(), lib.mmoe_last_error()
+    assert not y.any(), "a refused gpre_moe wrote its output"
+    # gpux_begin: no slots
+    assert not lib.gpux_begin(0, M.ptr(hn[0]), 0, M.ptr(np.zeros(1, np.int32)))
+    # still usable
+    compare_layer(layer0, 4, M.ORDER_BATCH)
+
+
 def test_combine_int16_overflow():
     """Down results past int16 (the -32768 marker and the int32 side buffer): expert 5 of a layer gets gate, up and
     down codes all +1 and a large router bias, so every token routes to it; with positive inputs its gate and up
