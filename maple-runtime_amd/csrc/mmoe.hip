@@ -462,6 +462,7 @@ void gpre_dense_add(int g, const uint8_t *codes, const float *scales, int rows, 
 
 int gpre_dense_done(int maxtok) {
     if (ctx_ready()) return -1;
+    if (DN.ready) { seterr("gpre_dense_done: the projections are already on the card (mmoe_dense_reset first)"); return -1; }
     if (DN.bad) { seterr("gpre_dense_add: a matrix was not 256k x 2048 (or more than 3 per group)"); fprintf(stderr, "maplemoe: %s\n", mmoe_last_error()); return -1; }
     if (DN.host.empty() || maxtok < 1 || maxtok > 2048 || maxtok > S.main.maxtok) {
         seterr("gpre_dense_done: nothing added, or maxtok %d outside 1..%d (gpre_init)", maxtok, S.main.maxtok);
@@ -561,11 +562,12 @@ int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t 
     if (ctx < 1 || maxtok < 1 || maxtok > S.main.maxtok || maxtok > DN.maxtok || win < 0 || !norms || !router || !cs) {
         seterr("gfull_init: ctx %d / maxtok %d (context %d) / win %d", ctx, maxtok, S.main.maxtok, win); return -1;
     }
-    if (GF.ready) {   // a second set-up replaces the first
-        HC(hipFree(GF.nw)); HC(hipFree(GF.cs)); HC(hipFree(GF.kc)); HC(hipFree(GF.vc)); HC(hipFree(GF.ko));
-        HC(hipFree(GF.qkv)); HC(hipFree(GF.att)); HC(hipFree(GF.sc)); HC(hipFree(GF.inv)); HC(hipFree(GF.mx)); free(GF.ko_host);
-        GF.ready = 0;
-    }
+    // a second set-up replaces the first; buffers of a set-up that failed part way are released here too
+    GF.ready = 0;
+    void **dbuf[] = {(void **)&GF.nw, (void **)&GF.cs, (void **)&GF.kc, (void **)&GF.vc, (void **)&GF.ko,
+                     (void **)&GF.qkv, (void **)&GF.att, (void **)&GF.sc, (void **)&GF.inv, (void **)&GF.mx};
+    for (void **pp : dbuf) if (*pp) { HC(hipFree(*pp)); *pp = nullptr; }
+    free(GF.ko_host); GF.ko_host = nullptr;
     std::vector<uint16_t> nw((size_t)24 * GF_NWL);
     for (size_t i = 0; i < nw.size(); i++) { uint32_t u; memcpy(&u, &norms[i], 4); nw[i] = (uint16_t)(u >> 16); }
     HC(hipMalloc(&GF.nw, nw.size() * 2)); HC(hipMemcpy(GF.nw, nw.data(), nw.size() * 2, hipMemcpyHostToDevice));
@@ -574,6 +576,7 @@ int gfull_init(int ctx, int maxtok, int win, const float *norms, const uint16_t 
     HC(hipMalloc(&GF.kc, kvb)); HC(hipMalloc(&GF.vc, kvb)); HC(hipMalloc(&GF.ko, kob));
     HC(hipMemset(GF.kc, 0, kvb)); HC(hipMemset(GF.vc, 0, kvb));
     GF.ko_host = (uint16_t *)malloc(kob);
+    if (!GF.ko_host) { seterr("gfull_init: %zu bytes of host memory", kob); return -1; }
     HC(hipMalloc(&GF.qkv, (size_t)maxtok * 3072 * 4)); HC(hipMalloc(&GF.att, (size_t)maxtok * MH * 4));
     HC(hipMalloc(&GF.sc, (size_t)maxtok * 16 * ctx * 4)); HC(hipMalloc(&GF.inv, (size_t)maxtok * 16 * 4)); HC(hipMalloc(&GF.mx, (size_t)maxtok * 16 * 4));
     for (int L = 0; L < 24; L++) {

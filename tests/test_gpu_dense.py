@@ -63,3 +63,5 @@ def test_gpre_dense_matches_cpu_projections():
     assert lib.gpre_dense(5, None, 1, None) < 0                              # empty group
     lib.gpre_dense_add(0, M.ptr(mats[0][0][0]), M.ptr(mats[0][0][2]), 2048, 2048)
     assert b"after gpre_dense_done" in lib.mmoe_last_error()
+    assert lib.gpre_dense_done(256) == -1                                   # a second upload needs a reset
+    assert b"already" in lib.mmoe_last_error()
