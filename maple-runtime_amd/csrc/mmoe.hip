@@ -685,7 +685,11 @@ int gpux_init(int layers, int slots) {
     if (layers < 1 || layers > NLMAX || slots < 1 || slots > 256) { seterr("gpux_init: layers %d / slots %d out of range", layers, slots); return -1; }
     if (!S.dec.maxtok && work_alloc(S.dec, MMOE_GPUX_MAXTOK)) return -1;
     if (work_debug(S.dec, S.debug)) return -1;
-    if (S.gx_mem) HC(hipFree(S.gx_mem));
+    if (S.gx_mem) {   // a second set-up replaces the first (its slots are gone until uploaded again)
+        uint8_t *old = S.gx_mem;
+        S.gx_mem = nullptr; S.gx_layers = S.gx_slots = 0;
+        HC(hipFree(old));
+    }
     HC(hipMalloc(&S.gx_mem, (size_t)layers * slots * EXPERT_BYTES));
     S.gx_layers = layers; S.gx_slots = slots;
     return 0;

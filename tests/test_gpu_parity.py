@@ -175,6 +175,15 @@ def test_gpux(layer0):
         qa, qsa, qsuma = O.prep(act)
         d = np.array([np.float32(np.float32(o.mo_dot_i32(O._p(dc[r]), O._p(qa), 512) - qsuma) * qsa) * ds[r] for r in range(2048)], np.float32)
         assert relmax(out[k], d) <= TOL
+    # a second gpux_init replaces the slots: upload one expert again and the hit gives the same output
+    M.check(lib.gpux_init(2, 4), "gpux_init again")
+    lib.gpux_upload(1, 2, *[M.ptr(a) for a in M.expert_views(layer0.blk, experts[4])])
+    h = lib.gpux_begin(1, M.ptr(hn[0]), 1, M.ptr(np.array([2], np.int32)))
+    assert h, lib.mmoe_last_error()
+    again = np.zeros((1, 2048), np.float32)
+    lib.gpux_end(h, M.ptr(again), 1)
+    assert np.array_equal(again[0], out[0]), "slot 4 before and slot 2 after the second gpux_init differ"
+    assert not lib.gpux_begin(1, M.ptr(hn[0]), 1, M.ptr(np.array([4], np.int32)))   # past the 4 slots now
 
 
 @pytest.mark.parametrize("nb", [1, 5, 8])
