@@ -126,7 +126,9 @@ int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order);
 int mmoe_rmsnorm_dev(const float *d_x, const uint16_t *d_w, int nb, float *d_out);
 /* nl stacked MoE layers: for L in L0..L0+nl-1: hn = rmsnorm(x, post_ln[L]); x += MoE_L(hn). */
 int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order);
-/* The same captured once into a HIP graph, then replayed `replays` times; mmoe_graph_reset drops it. */
+/* The same captured once into a HIP graph, then replayed `replays` times; mmoe_graph_reset drops it. A call
+ * with other arguments captures anew. The graph holds the device buffers it was captured with: after
+ * mmoe_set_layer or mmoe_set_bias of its layers, call mmoe_graph_reset. Profiling must be off. */
 int mmoe_stack_graph(int L0, int nl, float *d_x, int nb, int order, int replays);
 int mmoe_graph_reset(void);
 /* Router stage of gfull_attn (gpu_full.metal:12-27 rms, 169-209 rtr) on the gfull hidden state:

@@ -134,6 +134,7 @@ static struct {
     hipEvent_t pe[2];
     double prof_ms[MMOE_PROF_NKERNELS]; long prof_n[MMOE_PROF_NKERNELS];
     hipGraphExec_t graph = nullptr;
+    struct { int L0, nl, nb, order; float *x; } gkey = {};   // the arguments the graph was captured with
     int ncu = 256;             // compute units of the device (persistent grids)
 } S;
 
@@ -867,6 +868,10 @@ int mmoe_gfull_stack(int L0, int nl) {
 // Capture mmoe_stack_dev into a HIP graph and replay it (launch-bound decode). Profiling must be off.
 int mmoe_stack_graph(int L0, int nl, float *d_x, int nb, int order, int replays) {
     if (S.prof) { seterr("mmoe_stack_graph: profiling is on"); return -1; }
+    if (replays < 0) { seterr("mmoe_stack_graph: replays %d", replays); return -1; }
+    // the graph holds its arguments: other arguments need a new capture
+    if (S.graph && (S.gkey.L0 != L0 || S.gkey.nl != nl || S.gkey.x != d_x || S.gkey.nb != nb || S.gkey.order != order))
+        if (mmoe_graph_reset()) return -1;
     if (!S.graph) {
         hipGraph_t g;
         HC(hipStreamBeginCapture(S.st, hipStreamCaptureModeThreadLocal));
@@ -875,6 +880,7 @@ int mmoe_stack_graph(int L0, int nl, float *d_x, int nb, int order, int replays)
         if (rc || e != hipSuccess) { seterr("graph capture failed: %s", hipGetErrorString(e)); return -1; }
         HC(hipGraphInstantiate(&S.graph, g, nullptr, nullptr, 0));
         HC(hipGraphDestroy(g));
+        S.gkey = {L0, nl, nb, order, d_x};
     }
     for (int i = 0; i < replays; i++) HC(hipGraphLaunch(S.graph, S.st));
     return 0;

@@ -232,6 +232,33 @@ def test_stack_decode(layer0):
         assert relmax(xg - x0, xo - x0) <= TOL
 
 
+def test_stack_graph_replays_match_eager(layer0):
+    """mmoe_stack_graph (the HIP-graph replay the decode benchmarks time) against mmoe_stack_dev: three replays
+    in a row, each with eager work of another shape in between, every replay bit-identical to the eager step.
+    The second case changes the arguments, so the library must capture a new graph, not replay the old one.
+    Runs after test_stack_decode, which set layers 0-2 with their norm weights."""
+    lib = M.lib()
+    M.check(lib.mmoe_graph_reset(), "graph reset")
+    xo, ho = normed_hidden(SEED, 903, 8)
+    for nb, order in [(1, M.ORDER_STEP), (64, M.ORDER_BATCH)]:
+        x0 = M.synth_hidden(SEED, 400 + nb, nb)
+        d_e = lib.mmoe_dev_alloc(x0.nbytes); d_g = lib.mmoe_dev_alloc(x0.nbytes)
+        M.check(lib.mmoe_h2d(d_e, M.ptr(x0), x0.nbytes), "h2d"); M.check(lib.mmoe_h2d(d_g, M.ptr(x0), x0.nbytes), "h2d")
+        xe = np.empty_like(x0); xg = np.empty_like(x0)
+        try:
+            for r in range(3):
+                M.check(lib.mmoe_stack_dev(0, 3, d_e, nb, order), "stack eager")
+                M.check(lib.mmoe_d2h(M.ptr(xe), d_e, x0.nbytes), "d2h")
+                run_gpu(0, ho, xo, M.ORDER_BATCH)                            # other work between replays
+                M.check(lib.mmoe_stack_graph(0, 3, d_g, nb, order, 1), "stack graph")
+                M.check(lib.mmoe_d2h(M.ptr(xg), d_g, x0.nbytes), "d2h")
+                assert np.array_equal(xg.view(np.int32), xe.view(np.int32)), f"nb {nb} replay {r} differs from eager"
+            print(f"\n  graph nb={nb}: 3 replays bit-identical to the eager steps")
+        finally:
+            M.check(lib.mmoe_graph_reset(), "graph reset")   # before its buffers go
+            lib.mmoe_dev_free(d_e); lib.mmoe_dev_free(d_g)
+
+
 def test_moe_batch_mfma_router(layer0):
     """Batches of >= 128 tokens with the bf16-MFMA router and exact refinement of each token's candidates."""
     lib = M.lib()
