@@ -573,7 +573,7 @@ __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, 
 }
 
 // Top-8 and the int8 quantisation of the MoE input (maple.c:909-923 and 908 prep) of 4 tokens per block,
-// one wave per token; adds each token's 8 experts to hist (per chunk of 64 tokens) when hist is given.
+// one wave per token, blocks (x, 0) the top-8 and blocks (x, 1) the quantisation; adds each token's 8 experts to hist (per chunk of 64 tokens) when hist is given.
 __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl, const float *__restrict__ hn, int nb,
                                                     int *__restrict__ top, float *__restrict__ tw, int8_t *__restrict__ qx,
                                                     float *__restrict__ qsx, int *__restrict__ qsumx, int *__restrict__ hist);
@@ -743,9 +743,12 @@ __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl
     int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
     int b = blockIdx.x * 4 + wv;
     if (b >= nb) return;  // whole wave exits together
-    int ek = topk_wave(rl + (size_t)b * MNE, E[wv], l, top + b * MTOPK, tw + b * MTOPK);
-    if (hist && l < MTOPK) atomicAdd(&hist[(b >> 6) * MNE + ek], 1);   // per-chunk expert counts for k_group
-    quant_wave<MH>(hn + (size_t)b * MH, l, qx + (size_t)b * MH, qsx + b, qsumx + b);
+    if (blockIdx.y == 0) {   // grid y = 2: the top-8 and the quantisation of a token run in different blocks
+        int ek = topk_wave(rl + (size_t)b * MNE, E[wv], l, top + b * MTOPK, tw + b * MTOPK);
+        if (hist && l < MTOPK) atomicAdd(&hist[(b >> 6) * MNE + ek], 1);   // per-chunk expert counts for k_group
+    } else {
+        quant_wave<MH>(hn + (size_t)b * MH, l, qx + (size_t)b * MH, qsx + b, qsumx + b);
+    }
 }
 
 // Exact top-8 from approximate logits (k_router_mfma), in two kernels before k_topk_quant.

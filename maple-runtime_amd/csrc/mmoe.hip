@@ -207,7 +207,7 @@ static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) 
                 k_chain<<<dim3((nb + 3) / 4, 2), 256, 0, S.st>>>(d_hn, nb, lw.rc8, lw.bias, w.cand, w.ncand, w.rl);
             })) return -1;
     }
-    if (launch(MMOE_K_TOPK, [&] { k_topk_quant<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
+    if (launch(MMOE_K_TOPK, [&] { k_topk_quant<<<dim3((nb + 3) / 4, 2), 256, 0, S.st>>>(w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
     w.hist_used = nch * MNE;   // cleared by this call's combine
     return launch(MMOE_K_GROUP, [&] {
         k_group<<<nch, 512, 0, S.st>>>(w.hist, nb, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles, w.eu, w.top, w.tw, w.utok, w.uw,
