@@ -127,10 +127,13 @@ int mmoe_rmsnorm_dev(const float *d_x, const uint16_t *d_w, int nb, float *d_out
 /* nl stacked MoE layers: for L in L0..L0+nl-1: hn = rmsnorm(x, post_ln[L]); x += MoE_L(hn). */
 int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order);
 /* The same captured once into a HIP graph, then replayed `replays` times; mmoe_graph_reset drops it. A call
- * with other arguments captures anew. The graph holds the device buffers it was captured with: after
- * mmoe_set_layer or mmoe_set_bias of its layers, call mmoe_graph_reset. Profiling must be off. */
+ * with other arguments captures anew. The graph holds the kernels and device buffers it was captured with, so
+ * every setter that changes them (mmoe_set_layer, mmoe_set_bias, mmoe_set_debug, mmoe_set_decode_path,
+ * mmoe_set_router_mode, gfull_init) drops it first. Profiling must be off. mmoe_graph_held: 1 while a
+ * captured graph is kept, else 0. */
 int mmoe_stack_graph(int L0, int nl, float *d_x, int nb, int order, int replays);
 int mmoe_graph_reset(void);
+int mmoe_graph_held(void);
 /* Router stage of gfull_attn (gpu_full.metal:12-27 rms, 169-209 rtr) on the gfull hidden state:
  * hn = rmsnorm(x, post_ln[L]), rl[nb][256] = router logits (copied to the host if rl != NULL). */
 int mmoe_gfull_setup(int maxtok);

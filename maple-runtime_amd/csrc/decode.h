@@ -16,14 +16,6 @@
 #pragma once
 #include "kernels.h"
 
-#ifdef DEC_TIMING   // development instrumentation: per-phase timestamps of one block per kernel
-#define DEC_TS(i, cond) do { if ((cond) && threadIdx.x == 0) dec_ts[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#define DEC_SPAN(i) do { if (threadIdx.x == 0) { unsigned long long ts_ = __builtin_amdgcn_s_memrealtime(); atomicMin(&dec_ts[i], ts_); atomicMax(&dec_ts[i + 1], ts_); } } while (0)
-#else
-#define DEC_TS(i, cond) do {} while (0)
-#define DEC_SPAN(i) do {} while (0)
-#endif
-
 #define DEC_MAXTOK 8
 #define DEC_MAXP (DEC_MAXTOK * MTOPK)  // 64 pairs
 #define DEC_GS 144                      // LDS bytes per 128-column group of int8 vectors (16 bytes padding)
@@ -54,8 +46,6 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
     constexpr int LEN = MH / NCH;                     // chain length
     __shared__ __attribute__((aligned(16))) float hs[NCH * (LEN + DEC_HP)];
     int l = threadIdx.x, j = l % NCH, e = blockIdx.x * (64 / NCH) + l / NCH;
-    DEC_SPAN(0);
-    DEC_TS(2, blockIdx.x == 5);
     // token 0's x and the norm weights first, the router weights after them: loads return in issue order, so
     // the norm need not wait for the router weights (the scheduling barrier keeps that order)
     float4 x0[8];
@@ -94,7 +84,6 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
 #pragma unroll
             for (int i = 0; i < 32; i++) v[i] = v[i] * k * lw[i];
         }
-        DEC_TS(3, blockIdx.x == 5);
         __syncthreads();                              // previous token's chains are done with hs
 #pragma unroll
         for (int i = 0; i < 32; i++) { int c = 4 * l + 256 * (i >> 2) + (i & 3); hs[(c % NCH) * (LEN + DEC_HP) + c / NCH] = v[i]; }
@@ -103,7 +92,6 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
             for (int i = 0; i < 8; i++) *(float4 *)(hn + (size_t)b * MH + 4 * l + 256 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
         __syncthreads();
         const float *hc = hs + j * (LEN + DEC_HP);
-        DEC_TS(4, blockIdx.x == 5);
         float acc = 0.0f;
 #pragma unroll
         for (int i = 0; i < LEN / 8; i++) {
@@ -127,8 +115,6 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
             rl[(size_t)b * MNE + e] = r;
         }
     }
-    DEC_TS(5, blockIdx.x == 5);
-    DEC_SPAN(0);
 }
 
 // wc[e][j][m] = w[e][j + NCH*m]
@@ -200,7 +186,6 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     __shared__ float sgu[2][8];
     __shared__ __attribute__((aligned(16))) ExpPtr tab[MNE];
     int t = threadIdx.x, wv = t >> 6, l = t & 63;
-    DEC_TS(18, blockIdx.x == 3 && blockIdx.y == 1);
     static_assert(sizeof(ExpPtr) == 48, "ExpPtr: 6 pointers");
     const v4i *ltp = (const v4i *)(layer_tab + t);   // the layer's expert table, stored to LDS after top-8 (three
     v4i my0 = ltp[0], my1 = ltp[1], my2 = ltp[2];     // vectors: held as a struct it went to scratch memory)
@@ -212,9 +197,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     }
     { v4i *tp4 = (v4i *)(tab + t); tp4[0] = my0; tp4[1] = my1; tp4[2] = my2; }
     __syncthreads();
-    DEC_TS(19, blockIdx.x == 3 && blockIdx.y == 1);
     dec_group_block(nb, R);
-    DEC_TS(20, blockIdx.x == 3 && blockIdx.y == 1);
     int u = blockIdx.y;
     bool pub = blockIdx.x == 0 && blockIdx.y == 0;
     if (u >= R.nu && !pub) return;                    // whole block
@@ -239,10 +222,6 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     uint32_t cwd[8] = {(uint32_t)c0.x, (uint32_t)c0.y, (uint32_t)c0.z, (uint32_t)c0.w, (uint32_t)c1.x, (uint32_t)c1.y, (uint32_t)c1.z, (uint32_t)c1.w};
 #pragma unroll
     for (int k = 0; k < 8; k++) decode4(cwd[k], cd + 4 * k);
-#ifdef DEC_TIMING
-    if (cd[31] == 0xffffffffu) dec_ts[63] = 1;      // forces the code loads before the next stamp
-#endif
-    DEC_TS(21, blockIdx.x == 3 && blockIdx.y == 1);
     int a0 = R.ustart[u], n = R.ustart[u + 1] - a0;
     for (int i = 0; i < n; i++) {
         int tok = R.utok[a0 + i];
@@ -255,7 +234,6 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     }
     if (t < 16) sgu[t >> 3][t & 7] = srow;
     __syncthreads();
-    DEC_TS(22, blockIdx.x == 3 && blockIdx.y == 1);
     if (t < n * 8) {
         int i = t >> 3, r8 = t & 7, a = a0 + i, tok = R.utok[a];
         float qs = qsv_l[tok]; int qsum = qsum_l[tok];
@@ -267,7 +245,6 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
         act[(size_t)a * MFF + r0 + r8] = g / (1.0f + dexp(-g)) * uu;
         if (dbg) { dbg[(size_t)a * 2 * MFF + r0 + r8] = ag; dbg[(size_t)a * 2 * MFF + MFF + r0 + r8] = au; }
     }
-    DEC_TS(23, blockIdx.x == 3 && blockIdx.y == 1);
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -300,7 +277,6 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
     __shared__ int qsuma[DEC_MAXP];
     int t = threadIdx.x, wv = t >> 6, l = t & 63, rr = l >> 3, sl = l & 7;
     int r0 = blockIdx.x * 8, row = r0 + rr;
-    DEC_TS(34, blockIdx.x == 7);
     ActChunk c0;
     act_load(act, 2 * wv + (l >> 5), l, c0);          // first act vectors, issued before anything else
     int nu = plan->nu;
@@ -345,7 +321,6 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
         quant_half<DEC_GS>(c0.v, l, qa[a], &qsa[a], &qsuma[a]);
     }
     __syncthreads();
-    DEC_TS(35, blockIdx.x == 7);
     if (blockIdx.x == 0)
         for (int a = wv; a < nb * MTOPK; a += 4) {
             if (l < MFF / 16) *(uint4 *)(qa_out + (size_t)a * MFF + l * 16) = *(const uint4 *)(&qa[a][(l >> 3) * DEC_GS + (l & 7) * 16]);
@@ -366,13 +341,11 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
             if (sl == 0) {
                 float d = (float)(acc - qsuma[a]) * qsa[a] * sd[k];
                 Dl[a][rr] = d;
-                down[(size_t)a * MH + row] = d;
-                if (dbg) dbg[(size_t)a * MH + row] = acc;
+                if (dbg) { down[(size_t)a * MH + row] = d; dbg[(size_t)a * MH + row] = acc; }   // checks only
             }
         }
     }
     __syncthreads();
-    DEC_TS(36, blockIdx.x == 7);
     if (t < nb * 8) {
         float acc = (mode & 1) ? cx : 0.0f;
 #pragma unroll
@@ -380,5 +353,4 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
         if (mode & 4) acc = cx + acc;
         *cxp = acc;
     }
-    DEC_TS(37, blockIdx.x == 7);
 }

@@ -501,26 +501,18 @@ __global__ void __launch_bounds__(256) k_router_l1max(const uint16_t *__restrict
 // p / (sum of picked, in pick order, + 1e-20). Also writes slot -> expert (top) and weight (tw).
 // =====================================================================================================
 // One wave, one token: rl_row[256] -> top[8], tw[8] (written by lane 0). E = 256 floats of LDS scratch.
-#ifdef DEC_TIMING
-__device__ unsigned long long dec_ts[64];
-#define TK_TS(i) do { if (blockIdx.x == 3 && blockIdx.y == 1 && l == 0) dec_ts[i] = __builtin_amdgcn_s_memrealtime(); } while (0)
-#else
-#define TK_TS(i) do {} while (0)
-#endif
 // One wave, one token: rl_row[256] -> top[8], tw[8] (and lane l returns the expert of slot l % 8).
 // E = 256 floats of LDS scratch. Selection: p >= 0, so key = p_bits + 1 orders like p, and 0 marks a picked expert. Each of the 8 rounds
 // takes the largest key (lane-local over 4, DPP within 16-lane rows, the 4 row results as scalars), then the
 // lowest expert index holding it (ballots in index order: e = l + 64 i), which is the pick order of maple.c's
 // repeated strict-> scans, ties included.
 __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
-    TK_TS(40); TK_TS(41);
     float lg[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) lg[i] = r[l + 64 * i];
     float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
     mx = wave_max(mx);
     mx = fmaxf(mx, -1e30f);  // maple.c starts its max at -1e30
-    TK_TS(42);
 #pragma unroll
     for (int i = 0; i < 4; i++) { lg[i] = dexp(lg[i] - mx); E[l + 64 * i] = lg[i]; }
     __builtin_amdgcn_wave_barrier();
@@ -537,7 +529,6 @@ __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, 
 #pragma unroll
     for (int i = 0; i < 8; i++) pv[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), i));
     float sum = hsum8(pv);
-    TK_TS(43);
     uint32_t key[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) key[i] = __float_as_uint(lg[i] / sum) + 1u;
@@ -561,7 +552,6 @@ __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, 
             key[0] = i == 0 ? 0u : key[0]; key[1] = i == 1 ? 0u : key[1]; key[2] = i == 2 ? 0u : key[2]; key[3] = i == 3 ? 0u : key[3];
         }
     }
-    TK_TS(44); TK_TS(45);
     if (l == 0) {
 #pragma unroll
         for (int k = 0; k < MTOPK; k++) { top[k] = ek[k]; tw[k] = pk[k] / (tsum + 1e-20f); }

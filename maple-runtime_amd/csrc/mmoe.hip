@@ -2,10 +2,11 @@
 //
 // Exports, with maple.c's own C signatures (maple.c:247-272), the entry points maple.c links against when
 // built with -DGPU_HEAD: gpre_* (experts of a prompt chunk and the dense q/k/v/o projections), gfull_*
-// (device-resident hidden state), gpux_* (decode experts) and gpu_head_*. Those outside the built scope (the
-// output head, attention) return the failure value maple.c already handles by falling back to its CPU code. New mmoe_* entry points run the whole layer on the device:
-// router logits, softmax/top-8, grouping, int8 quantisation, gate/up + SiLU, re-quantisation, down and the
-// combine (declared in include/maplemoe.h).
+// (device-resident hidden state and the attention half of a layer), gpux_* (decode experts) and gpu_head_*.
+// The output head is outside the built scope: gpu_head_init returns the failure value maple.c handles by
+// keeping the head on its CPU. New mmoe_* entry points run the whole MoE layer on the device: router logits,
+// softmax/top-8, grouping, int8 quantisation, gate/up + SiLU, re-quantisation, down and the combine
+// (declared in include/maplemoe.h).
 //
 // One global context, like the reference (gpu_pre.m keeps file-scope state); not thread-safe; all work is
 // queued on one default-priority HIP stream owned by the library.
@@ -173,7 +174,8 @@ static int tile_tn(int np) { return np >= 2048 ? 64 : 16; }
 
 // Router logits of nb tokens (d_hn) with layer L's router; order 0 = batch (maple.c:853-889), 1 = step (bf_row)
 static bool S_router_exact = true;    // large batches: exact chain GEMM (else MFMA logits + exact refinement)
-static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
+// exact_only: never the approximate large-batch router (callers that hand the logits themselves to the host)
+static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bool exact_only = false) {
     LayerW &lw = S.layers[L];
     w.refine = false;
     if (!lw.router) { seterr("layer %d has no router (mmoe_set_layer)", L); return -1; }
@@ -187,7 +189,7 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order) {
         if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { k_router_chains<8, true><<<dim3(MNE * 8 / 256, nb), 256, 0, S.st>>>(w.norm_x, nb, lw.rc8, lw.bias, w.rl, w.norm_w, hn_w); });
         return launch(MMOE_K_ROUTER, [&] { k_router_chains<8><<<dim3(MNE * 8 / 256, nb), 256, 0, S.st>>>(d_hn, nb, lw.rc8, lw.bias, w.rl); });
     }
-    if (S_router_exact)
+    if (S_router_exact || exact_only)
         return launch(MMOE_K_ROUTER, [&] { k_router_gemm<4><<<dim3((nb + 15) / 16, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
     // approximate logits on the bf16 MFMA; k_cand + k_chain make the top-8 exact
     w.refine = true;
@@ -309,9 +311,14 @@ static int moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) {
     int np = nb * MTOPK, tn = tile_tn(np);
     LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = d_hn; LAST.dec = 0;
     if (stage_router(w, L, d_hn, nb, order)) return -1;
-    if (stage_route_group(w, L, nb, tn, d_hn)) return -1;
-    if (stage_experts(w, np, MNE, tn, true)) return -1;
-    return stage_combine(w, nb, d_x, order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH);
+    int rc = stage_route_group(w, L, nb, tn, d_hn);
+    if (!rc) rc = stage_experts(w, np, MNE, tn, true);
+    if (!rc) rc = stage_combine(w, nb, d_x, order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH);
+    if (rc && w.hist_used) {   // a stage failed before the combine cleared the expert counts: clear them here
+        (void)hipMemsetAsync(w.hist, 0, (size_t)w.hist_used * sizeof(int), S.st);
+        w.hist_used = 0;
+    }
+    return rc;
 }
 
 // Experts for a host-given grouping (gpre_moe, gfull_moe, gpux): ustart[nu+1], ptok, pw, tp on the host,
@@ -377,13 +384,19 @@ int gpre_region(const void *p, size_t len) {
     if (S.regions.size() >= MMOE_MAXREG) { seterr("gpre_region: more than %d regions", MMOE_MAXREG); return -1; }
     uint8_t *d = nullptr;
     HC(hipMalloc(&d, len));
-    hipEvent_t a, b; HC(hipEventCreate(&a)); HC(hipEventCreate(&b));
-    HC(hipEventRecord(a, S.st));
-    HC(hipMemcpyAsync(d, p, len, hipMemcpyHostToDevice, S.st));
-    HC(hipEventRecord(b, S.st));
-    HC(hipEventSynchronize(b));
-    float ms = 0; HC(hipEventElapsedTime(&ms, a, b)); S.t_region += ms * 1e-3;
-    HC(hipEventDestroy(a)); HC(hipEventDestroy(b));
+    hipEvent_t a = nullptr, b = nullptr;
+    float ms = 0;
+    hipError_t e = hipEventCreate(&a);
+    if (e == hipSuccess) e = hipEventCreate(&b);
+    if (e == hipSuccess) e = hipEventRecord(a, S.st);
+    if (e == hipSuccess) e = hipMemcpyAsync(d, p, len, hipMemcpyHostToDevice, S.st);
+    if (e == hipSuccess) e = hipEventRecord(b, S.st);
+    if (e == hipSuccess) e = hipEventSynchronize(b);
+    if (e == hipSuccess) e = hipEventElapsedTime(&ms, a, b);
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    if (e != hipSuccess) { (void)hipFree(d); seterr("gpre_region: copy into HBM: %s", hipGetErrorString(e)); return -1; }
+    S.t_region += ms * 1e-3;
     S.regions.push_back(Region{p, len, d});
     return (int)S.regions.size() - 1;
 }
@@ -759,10 +772,13 @@ int mmoe_init(int maxtok) {
 }
 
 // Small batches take the three-kernel decode path unless switched off (tests compare both paths).
-int mmoe_set_router_mode(int exact) { S_router_exact = exact != 0; return 0; }
-int mmoe_set_decode_path(int on) { S_dec_enabled = on != 0; return 0; }
+// Every setter below changes what a captured graph holds (kernels, pointers it passes): each drops the graph
+// before the change, so the next mmoe_stack_graph captures again and no replay touches freed memory.
+int mmoe_set_router_mode(int exact) { if (mmoe_graph_reset()) return -1; S_router_exact = exact != 0; return 0; }
+int mmoe_set_decode_path(int on) { if (mmoe_graph_reset()) return -1; S_dec_enabled = on != 0; return 0; }
 
 int mmoe_set_debug(int on) {
+    if (mmoe_graph_reset()) return -1;
     S.debug = on != 0;
     if (S.main.maxtok && work_debug(S.main, S.debug)) return -1;
     if (S.dec.maxtok && work_debug(S.dec, S.debug)) return -1;
@@ -772,6 +788,7 @@ int mmoe_set_debug(int on) {
 int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *router, const uint16_t *post_ln) {
     if (ctx_ready()) return -1;
     if (L < 0 || L >= NLMAX) { seterr("mmoe_set_layer: layer %d outside 0..%d", L, NLMAX - 1); return -1; }
+    if (mmoe_graph_reset()) return -1;
     LayerW &lw = S.layers[L];
     ExpPtr ep[MNE];
     if (resolve_loc(loc, regs, MNE, ep)) return -1;
@@ -788,6 +805,7 @@ int mmoe_set_layer(int L, const uint32_t *loc, const int *regs, const uint16_t *
 // Layer L's router (bf16 [256][2048]) into HBM with its chain-major copies (both orders, and fp32 for the
 // tiled batch router) and the bound the MFMA router option uses.
 static int set_router(int L, const uint16_t *router) {
+    if (mmoe_graph_reset()) return -1;
     LayerW &lw = S.layers[L];
     if (!lw.router) HC(hipMalloc(&lw.router, (size_t)MNE * MH * 2));
     HC(hipMemcpy(lw.router, router, (size_t)MNE * MH * 2, hipMemcpyHostToDevice));
@@ -807,6 +825,7 @@ static int set_router(int L, const uint16_t *router) {
 int mmoe_set_bias(int L, const float *bias) {
     if (ctx_ready()) return -1;
     if (L < 0 || L >= NLMAX) { seterr("mmoe_set_bias: layer %d", L); return -1; }
+    if (mmoe_graph_reset()) return -1;
     LayerW &lw = S.layers[L];
     if (!bias) { if (lw.bias) HC(hipFree(lw.bias)); lw.bias = nullptr; return 0; }
     if (!lw.bias) HC(hipMalloc(&lw.bias, MNE * 4));
@@ -877,15 +896,23 @@ int mmoe_stack_graph(int L0, int nl, float *d_x, int nb, int order, int replays)
         HC(hipStreamBeginCapture(S.st, hipStreamCaptureModeThreadLocal));
         int rc = mmoe_stack_dev(L0, nl, d_x, nb, order);
         hipError_t e = hipStreamEndCapture(S.st, &g);
-        if (rc || e != hipSuccess) { seterr("graph capture failed: %s", hipGetErrorString(e)); return -1; }
+        if (rc || e != hipSuccess) {
+            if (e == hipSuccess) (void)hipGraphDestroy(g);
+            if (!rc) seterr("graph capture failed: %s", hipGetErrorString(e));
+            return -1;
+        }
         HC(hipGraphInstantiate(&S.graph, g, nullptr, nullptr, 0));
         HC(hipGraphDestroy(g));
-        S.gkey = {L0, nl, nb, order, d_x};
+        S.gkey = {L0, nl, nb, order, d_x};   // setters that change what a capture holds drop the graph
     }
     for (int i = 0; i < replays; i++) HC(hipGraphLaunch(S.graph, S.st));
     return 0;
 }
-int mmoe_graph_reset(void) { if (S.graph) { HC(hipGraphExecDestroy(S.graph)); S.graph = nullptr; } return 0; }
+int mmoe_graph_reset(void) {
+    if (S.graph) { hipGraphExec_t g = S.graph; S.graph = nullptr; HC(hipGraphExecDestroy(g)); }
+    return 0;
+}
+int mmoe_graph_held(void) { return S.graph != nullptr; }
 
 // Intermediate results of the last main-context call (debug/test access)
 int mmoe_read(int what, void *dst, size_t bytes) {
@@ -933,7 +960,8 @@ int mmoe_gfull_post_norm(int L, float *rl) {
     Work &w = S.main; int nb = S.gfull_nb;
     const uint16_t *pw = S.layers[L].post_ln;
     if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(w.x, pw, w.hn, nb); })) return -1;
-    if (stage_router(w, L, w.hn, nb, MMOE_ORDER_BATCH)) return -1;
+    // exact chains whatever the router mode: maple.c takes these logits as they are (its own softmax/top-8)
+    if (stage_router(w, L, w.hn, nb, MMOE_ORDER_BATCH, true)) return -1;
     if (rl) { HC(hipMemcpyAsync(rl, w.rl, (size_t)nb * MNE * 4, hipMemcpyDeviceToHost, S.st)); HC(hipStreamSynchronize(S.st)); }
     return 0;
 }
@@ -1021,13 +1049,3 @@ int mmoe_device_info(char *name, int len, int *cus, int *clock_khz) {
 
 }  // extern "C"
 
-#ifdef DEC_TIMING
-extern "C" int mmoe_dec_ts(unsigned long long *out, int reset) {
-    if (reset) {
-        unsigned long long h[64];
-        for (int i = 0; i < 64; i++) h[i] = (i % 16 == 0) ? ~0ull : 0ull;
-        return hipMemcpyToSymbol(HIP_SYMBOL(dec_ts), h, sizeof h) == hipSuccess ? 0 : -1;
-    }
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(dec_ts), 64 * 8) == hipSuccess ? 0 : -1;
-}
-#endif

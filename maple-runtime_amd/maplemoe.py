@@ -57,7 +57,7 @@ def _declare(L):
         "mmoe_init": (i, [i]), "mmoe_set_layer": (i, [i, vp, vp, vp, vp]), "mmoe_set_bias": (i, [i, vp]),
         "mmoe_moe": (i, [i, vp, i, vp, i]), "mmoe_moe_dev": (i, [i, vp, i, vp, i]),
         "mmoe_rmsnorm_dev": (i, [vp, vp, i, vp]), "mmoe_stack_dev": (i, [i, i, vp, i, i]),
-        "mmoe_stack_graph": (i, [i, i, vp, i, i, i]), "mmoe_graph_reset": (i, []),
+        "mmoe_stack_graph": (i, [i, i, vp, i, i, i]), "mmoe_graph_reset": (i, []), "mmoe_graph_held": (i, []),
         "mmoe_gfull_setup": (i, [i]), "mmoe_gfull_post_norm": (i, [i, vp]), "mmoe_gfull_stack": (i, [i, i]),
         "mmoe_read": (i, [i, vp, sz]), "mmoe_set_debug": (i, [i]), "mmoe_set_decode_path": (i, [i]), "mmoe_set_router_mode": (i, [i]), "mmoe_last_error": (C.c_char_p, []),
         "mmoe_dev_alloc": (vp, [sz]), "mmoe_dev_free": (i, [vp]), "mmoe_h2d": (i, [vp, vp, sz]),
