@@ -32,6 +32,7 @@ class Trace(C.Structure):
 
 _or = None
 _ref = None
+_ref_native = None
 
 
 def oracle():
@@ -63,14 +64,21 @@ def ref_available():
     return os.path.exists(os.path.join(HERE, "_ref", "libmaple_ref.so"))
 
 
-def ref():
-    """maple.c compiled from /root/reference (oracle/Makefile `ref`)."""
-    global _ref
-    if _ref is None:
-        path = os.path.join(HERE, "_ref", "libmaple_ref.so")
+def ref(native=False):
+    """maple.c compiled from /root/reference (oracle/Makefile `ref`): -mavx2 -mfma -mf16c (the reference's
+    AVX2 target), or native=True: its documented -march=native build on the build host."""
+    global _ref, _ref_native
+    lib = _ref_native if native else _ref
+    if lib is None:
+        name = "libmaple_ref_native.so" if native else "libmaple_ref.so"
+        path = os.path.join(HERE, "_ref", name)
         if not os.path.exists(path):
-            raise RuntimeError("oracle/_ref/libmaple_ref.so not built (make -C oracle ref)")
-        _ref = C.CDLL(path)
+            raise RuntimeError(f"oracle/_ref/{name} not built (make -C oracle ref)")
+        lib = C.CDLL(path)
+        if native:
+            _ref_native = lib
+        else:
+            _ref = lib
         vp, i = C.c_void_p, C.c_int
         for n, r, a in [("ref_set_threads", i, [i]), ("ref_set_router", None, [i, vp]),
                         ("ref_set_expert", None, [i, i, vp, vp, vp, vp, vp, vp]),
@@ -79,13 +87,13 @@ def ref():
                         ("ref_topk", None, [vp, i, vp, vp]), ("ref_group", i, [vp, vp, i, vp, vp, vp, vp, vp, vp]),
                         ("ref_rmsnorm", None, [vp, vp, i, vp]), ("ref_act", None, [vp, vp, vp, i]),
                         ("ref_moe_batch", None, [i, vp, i, vp] + [vp] * 14),
-                        ("ref_moe_step", None, [i, vp, vp, vp, vp, vp, vp, vp]), ("ref_now", C.c_double, []),
+                        ("ref_moe_step", None, [i, vp, vp, vp, vp, vp, vp, vp]), ("ref_now", C.c_double, []), ("ref_set_bias", None, [vp]),
                         ("ref_ctx", i, []), ("ref_rope", None, [vp, i]), ("ref_f16", None, [vp, vp, i]),
                         ("ref_cs", None, [i, vp]), ("ref_set_attn", None, [i] + [vp] * 11),
                         ("ref_cache", None, [i, i, vp, vp, i]), ("ref_attn_chunk", None, [i, i, vp, i, i, vp])]:
-            f = getattr(_ref, n)
+            f = getattr(lib, n)
             f.restype, f.argtypes = r, a
-    return _ref
+    return lib
 
 
 # ------------------------------------------------------------------ oracle wrappers

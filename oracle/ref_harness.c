@@ -158,6 +158,12 @@ void ref_act(const float *G, const float *U, float *act, int n) {
     FAST_LEAVE;
 }
 
+/* Optional per-expert logit bias for ref_moe_batch (NULL: none). Not a maple.c feature: the Zipf-skewed
+ * workload adds it to each logit after the router dot, as the oracle's mo_router_batch
+ * and the library do (one fp32 addition). */
+static const float *REF_BIAS;
+void ref_set_bias(const float *bias) { REF_BIAS = bias; }
+
 /* The MoE block of step_batch (maple.c:733-755, 824-834) for layer L: hn[nb][2048] post-norm input,
  * x[nb][2048] updated in place. Optional outputs as in the oracle's mo_trace (NULL = skip). */
 void ref_moe_batch(int L, const float *hn, int nb, float *x, float *rl_out, int32_t *top_out, float *tw_out,
@@ -168,6 +174,7 @@ void ref_moe_batch(int L, const float *hn, int nb, float *x, float *rl_out, int3
     memcpy(HNB, hn, sizeof(float) * (size_t)nb * H);
     for (int b = 0; b < nb; b++) prep(&VHB[b], HNB[b], H);
     if (nb <= 32) run(job_route_small, NULL, NE); else run(job_route_multi, NULL, (nb + 7) / 8);
+    if (REF_BIAS) for (int b = 0; b < nb; b++) for (int e = 0; e < NE; e++) RLG[b][e] = RLG[b][e] + REF_BIAS[e];
     if (rl_out) memcpy(rl_out, RLG, sizeof(float) * (size_t)nb * NE);
     run(job_topk, NULL, nb);
     if (top_out) memcpy(top_out, TOPB, sizeof(int) * (size_t)nb * TOPK);

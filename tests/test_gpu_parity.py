@@ -398,3 +398,22 @@ def test_combine_int16_overflow():
     finally:
         M.check(lib.mmoe_set_debug(1), "debug on")
         M.check(lib.mmoe_set_bias(L, None), "bias off")
+
+
+def test_flip_token_matches_oracle(layer0):
+    """the golden token whose re-quantised act maple.c's AVX2 build rounds across an int8 boundary (a tie within
+    an ulp, tests/test_golden.py): the card equals the oracle bit for bit, and differs from maple.c's AVX2 output
+    in exactly that one value, which maple.c's -march=native build rounds as the card does"""
+    from test_golden import flip_inputs
+    f, hl, hn = flip_inputs()
+    assert hl.L == 0 and np.array_equal(hl.router, layer0.router)
+    for dec in (1, 0):                                   # the decode kernels and the grouped-GEMM kernels
+        M.check(M.lib().mmoe_set_decode_path(dec), "decode path")
+        xg = run_gpu(0, hn, np.zeros((1, 2048), np.float32), M.ORDER_BATCH)
+        xo = np.zeros((1, 2048), np.float32)
+        o = O.moe_batch(hn, hl.router, hl.table, xo, want=("top", "act", "qa"))
+        qa = M.mfma_to_natural(M.read("QA", (8, 512), np.int8), 512)
+        assert np.array_equal(qa, o["qa"]) and np.array_equal(xg.view(np.int32), xo.view(np.int32))
+        assert int((qa != f["avx2_qa"]).sum()) == 1 and np.array_equal(qa, f["native_qa"])
+        assert relmax(xg, f["native_xout"]) <= TOL
+    M.lib().mmoe_set_decode_path(1)
