@@ -20,6 +20,7 @@
 #define MMOE_MAXTOK 2048      /* largest chunk (maple.c:413 BMAX) */
 #define MMOE_MAXREG 64        /* regions (gpu_pre.m:21 MAXREG) */
 #define MMOE_GPUX_MAXTOK 64   /* vectors per gpux call (maple.c:322 MAXSEQ) */
+#define MMOE_NOALLOC_MAXTOK 64   /* tokens per mmoe_moe_dev_noalloc call (its fixed scratch) */
 
 /* ============================ Part 1: maple.c:247-272 ============================ */
 
@@ -122,6 +123,13 @@ int mmoe_set_bias(int L, const float *bias);
 int mmoe_moe(int L, const float *hn, int nb, float *x, int order);
 /* The same on device pointers, queued on the library stream (mmoe_stream) without waiting. */
 int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order);
+/* No counterpart in the reference. For callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc): mmoe_moe_dev for nb <= MMOE_NOALLOC_MAXTOK
+ * tokens whose work buffers all live in a fixed 7 MiB static device array of the library (set up when the
+ * library context is, by mmoe_init / mmoe_set_layer; held until the process ends). The call allocates and
+ * frees nothing; larger nb is refused with -1. Every call on the GPU shares that scratch: calls that overlap
+ * on one GPU (from several host threads) race. Results equal mmoe_moe_dev's. */
+int mmoe_moe_dev_noalloc(int L, const float *d_hn, int nb, float *d_x, int order);
 /* maple.c:398-402 rmsnorm on device pointers; d_w bf16[2048] or NULL (unit weight). */
 int mmoe_rmsnorm_dev(const float *d_x, const uint16_t *d_w, int nb, float *d_out);
 /* nl stacked MoE layers: for L in L0..L0+nl-1: hn = rmsnorm(x, post_ln[L]); x += MoE_L(hn). */

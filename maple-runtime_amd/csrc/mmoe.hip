@@ -73,41 +73,20 @@ struct Work {
     float *hmax = nullptr;          // max |hn| per token
     int *cand = nullptr, *ncand = nullptr;   // refinement candidates [T][RG_MAXC], counts [T]
     bool refine = false;            // the last router call left approximate logits for k_cand / k_chain
-    unsigned *counters = nullptr;   // [0] routing, [64 + u] per used expert: last-block-done counters (self-resetting)
 };
 
-static int work_alloc(Work &w, int maxtok) {
-    if (maxtok < 1 || maxtok > MMOE_MAXTOK) { seterr("maxtok %d outside 1..%d", maxtok, MMOE_MAXTOK); return -1; }
-    w.maxtok = maxtok; w.maxp = maxtok * MTOPK;
-    int nch = (maxtok + 63) / 64;
-    size_t T = maxtok, P = w.maxp;
-    HC(hipMalloc(&w.hn, T * MH * 4)); HC(hipMalloc(&w.x, T * MH * 4)); HC(hipMalloc(&w.rl, T * MNE * 4));
-    HC(hipMalloc(&w.top, T * MTOPK * 4)); HC(hipMalloc(&w.tw, T * MTOPK * 4));
-    HC(hipMalloc(&w.hist, (size_t)nch * MNE * 4));
-    HC(hipMemset(w.hist, 0, (size_t)nch * MNE * 4));   // the combine after k_group clears what it used
-    HC(hipMalloc(&w.plan, sizeof(Plan))); HC(hipMalloc(&w.tiles, sizeof(Tile) * ((size_t)w.maxp / 16 + MNE + 8))); HC(hipMalloc(&w.eptr, MNE * sizeof(ExpPtr)));
-    HC(hipMalloc(&w.utok, P * 4)); HC(hipMalloc(&w.uw, P * 4)); HC(hipMalloc(&w.tp, P * 4)); HC(hipMalloc(&w.sp, P * 4));
-    HC(hipMalloc(&w.ustart, (MNE + 1) * 4));
-    HC(hipMalloc(&w.qx, T * MH)); HC(hipMalloc(&w.qsx, T * 4)); HC(hipMalloc(&w.qsumx, T * 4));
-    HC(hipMalloc(&w.act, P * MFF * 4)); HC(hipMalloc(&w.qa, P * MFF)); HC(hipMalloc(&w.qsa, P * 4)); HC(hipMalloc(&w.qsuma, P * 4));
-    HC(hipMalloc(&w.down, P * MH * 4));
-    HC(hipMalloc(&w.dov, P * MH * 4));
-    HC(hipMalloc(&w.eu, MNE * 4)); HC(hipMalloc(&w.pu, P * 4));
-    HC(hipMalloc(&w.hs, 2 * T * MH * 2)); HC(hipMalloc(&w.hmax, T * 4)); HC(hipMalloc(&w.rpart, 4 * T * MNE * 4));
-    HC(hipMalloc(&w.cand, T * RG_MAXC * 4)); HC(hipMalloc(&w.ncand, T * 4));
-    HC(hipMalloc(&w.counters, (64 + MNE) * sizeof(unsigned)));
-    HC(hipMemset(w.counters, 0, (64 + MNE) * sizeof(unsigned)));
+// Where a Work set's buffers come from: hipMalloc (c == nullptr) or a fixed device span carved in order
+// (the no-alloc entry point's static scratch).
+struct Carve { uint8_t *base = nullptr; size_t used = 0, cap = 0; };
+template <typename T> static int wbuf(T *&p, size_t bytes, Carve *c) {
+    if (!c) { HC(hipMalloc(&p, bytes)); return 0; }
+    size_t o = (c->used + 255) / 256 * 256;
+    if (o + bytes > c->cap) { seterr("scratch of %zu bytes too small (%zu needed)", c->cap, o + bytes); return -1; }
+    p = (T *)(c->base + o);
+    c->used = o + bytes;
     return 0;
 }
-
-static int work_debug(Work &w, int on) {
-    if (on && !w.dbg_gu) {
-        HC(hipMalloc(&w.dbg_gu, (size_t)w.maxp * 2 * MFF * 4));
-        HC(hipMalloc(&w.dbg_dn, (size_t)w.maxp * MH * 4));
-    }
-    if (!on && w.dbg_gu) { HC(hipFree(w.dbg_gu)); HC(hipFree(w.dbg_dn)); w.dbg_gu = w.dbg_dn = nullptr; }
-    return 0;
-}
+__global__ void k_fill_zero(int *p, int n) { int i = blockIdx.x * 256 + threadIdx.x; if (i < n) p[i] = 0; }
 
 // ------------------------------------------------------------------------------------------------------
 // Global state
@@ -120,6 +99,8 @@ static struct {
     hipStream_t st = nullptr;
     Work main;                 // gpre / gfull / mmoe
     Work dec;                  // gpux
+    Work na;                   // mmoe_moe_dev_noalloc: carved from `scratch` (its device address in na_ptr)
+    uint8_t *na_ptr = nullptr;
     bool debug = false;
     std::vector<Region> regions;
     LayerW layers[NLMAX];
@@ -139,6 +120,49 @@ static struct {
     int ncu = 256;             // compute units of the device (persistent grids)
 } S;
 
+// small (carved sets): at most 64 tokens, so only the decode and 16-token-tile paths run: no int16 down side
+// buffer (2048+ pairs only), no approximate-router buffers (512+ tokens), no host-side hidden state copy.
+static int work_alloc(Work &w, int maxtok, Carve *c = nullptr) {
+    if (maxtok < 1 || maxtok > MMOE_MAXTOK || (c && maxtok > 64)) { seterr("maxtok %d outside 1..%d", maxtok, c ? 64 : MMOE_MAXTOK); return -1; }
+    w.maxtok = maxtok; w.maxp = maxtok * MTOPK;
+    int nch = (maxtok + 63) / 64;
+    size_t T = maxtok, P = w.maxp;
+    if (wbuf(w.hn, T * MH * 4, c) || wbuf(w.rl, T * MNE * 4, c) || wbuf(w.top, T * MTOPK * 4, c) ||
+        wbuf(w.tw, T * MTOPK * 4, c) || wbuf(w.hist, (size_t)nch * MNE * 4, c) || wbuf(w.plan, sizeof(Plan), c) ||
+        wbuf(w.tiles, sizeof(Tile) * ((size_t)w.maxp / 16 + MNE + 8), c) || wbuf(w.eptr, MNE * sizeof(ExpPtr), c) ||
+        wbuf(w.utok, P * 4, c) || wbuf(w.uw, P * 4, c) || wbuf(w.tp, P * 4, c) || wbuf(w.sp, P * 4, c) ||
+        wbuf(w.ustart, (MNE + 1) * 4, c) || wbuf(w.qx, T * MH, c) || wbuf(w.qsx, T * 4, c) || wbuf(w.qsumx, T * 4, c) ||
+        wbuf(w.act, P * MFF * 4, c) || wbuf(w.qa, P * MFF, c) || wbuf(w.qsa, P * 4, c) || wbuf(w.qsuma, P * 4, c) ||
+        wbuf(w.down, P * MH * 4, c) || wbuf(w.eu, MNE * 4, c) || wbuf(w.pu, P * 4, c))
+        return -1;
+    // the per-chunk expert counts start at zero; the combine after k_group clears what it used
+    k_fill_zero<<<(nch * MNE + 255) / 256, 256, 0, S.st>>>(w.hist, nch * MNE);
+    HC(hipGetLastError());
+    if (c) return 0;
+    HC(hipMalloc(&w.x, T * MH * 4));
+    HC(hipMalloc(&w.dov, P * MH * 4));
+    HC(hipMalloc(&w.hs, 2 * T * MH * 2)); HC(hipMalloc(&w.hmax, T * 4)); HC(hipMalloc(&w.rpart, 4 * T * MNE * 4));
+    HC(hipMalloc(&w.cand, T * RG_MAXC * 4)); HC(hipMalloc(&w.ncand, T * 4));
+    HC(hipStreamSynchronize(S.st));
+    return 0;
+}
+
+static int work_debug(Work &w, int on) {
+    if (on && !w.dbg_gu) {
+        HC(hipMalloc(&w.dbg_gu, (size_t)w.maxp * 2 * MFF * 4));
+        HC(hipMalloc(&w.dbg_dn, (size_t)w.maxp * MH * 4));
+    }
+    if (!on && w.dbg_gu) { HC(hipFree(w.dbg_gu)); HC(hipFree(w.dbg_dn)); w.dbg_gu = w.dbg_dn = nullptr; }
+    return 0;
+}
+
+// Work buffers of mmoe_moe_dev_noalloc, for callers that cannot allocate (see that entry point): a fixed device
+// array, held by the device the library runs on until the process ends. Host code never passes the array's
+// name to a kernel or a copy: it stands for a host-side shadow there. The device address comes from
+// hipGetSymbolAddress once, in ctx_ready, and every use goes through S.na_ptr.
+#define NOALLOC_SCRATCH_BYTES (7u << 20)
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
 static int ctx_ready() {
     if (S.ready) return 0;
     int n = 0;
@@ -148,6 +172,13 @@ static int ctx_ready() {
     HC(hipEventCreate(&S.gx_ev));
     int dev = 0; HC(hipGetDevice(&dev));
     HC(hipDeviceGetAttribute(&S.ncu, hipDeviceAttributeMultiprocessorCount, dev));
+    // the no-alloc work set: carved from the static scratch of this device (one device per process here)
+    void *sp = nullptr;
+    HC(hipGetSymbolAddress(&sp, HIP_SYMBOL(scratch)));
+    S.na_ptr = (uint8_t *)sp;
+    Carve c{S.na_ptr, 0, NOALLOC_SCRATCH_BYTES};
+    if (work_alloc(S.na, MMOE_NOALLOC_MAXTOK, &c)) return -1;
+    HC(hipStreamSynchronize(S.st));
     S.ready = true;
     return 0;
 }
@@ -288,8 +319,7 @@ static int launch_dec_down(Work &w, int nb, float *d_x, int order) {
     int mode = order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH;
     return launch(MMOE_K_DOWN, [&] { k_dec_down<<<MH / 8, 256, 0, S.st>>>(w.plan, w.eptr, w.act, w.qa, w.qsa, w.qsuma, w.tp, w.sp, w.uw, w.tw, nb, d_x, mode, w.down, dd); });
 }
-static int moe_dec(int L, const float *in, int do_norm, int nb, float *d_x, int order) {
-    Work &w = S.main;
+static int moe_dec(Work &w, int L, const float *in, int do_norm, int nb, float *d_x, int order) {
     LayerW &lw = S.layers[L];
     LAST.w = &w; LAST.np = nb * MTOPK; LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = nullptr; LAST.dec = 1; LAST.x = d_x;
     const uint16_t *pln = do_norm ? lw.post_ln : nullptr;
@@ -302,12 +332,11 @@ static int moe_dec(int L, const float *in, int do_norm, int nb, float *d_x, int 
     return launch_dec_down(w, nb, d_x, order);
 }
 
-// Whole MoE layer on device buffers: x[b] += MoE_L(hn[b])
-static int moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) {
-    Work &w = S.main;
+// Whole MoE layer on device buffers: x[b] += MoE_L(hn[b]), with the work set w (no allocation here)
+static int moe_dev(Work &w, int L, const float *d_hn, int nb, float *d_x, int order) {
     if (nb < 1 || nb > w.maxtok) { seterr("nb %d outside 1..%d (mmoe_init)", nb, w.maxtok); return -1; }
     if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("layer %d not set (mmoe_set_layer)", L); return -1; }
-    if (nb <= DEC_MAXTOK && S_dec_enabled) return moe_dec(L, d_hn, 0, nb, d_x, order);
+    if (nb <= DEC_MAXTOK && S_dec_enabled) return moe_dec(w, L, d_hn, 0, nb, d_x, order);
     int np = nb * MTOPK, tn = tile_tn(np);
     LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = d_hn; LAST.dec = 0;
     if (stage_router(w, L, d_hn, nb, order)) return -1;
@@ -839,13 +868,21 @@ int mmoe_moe(int L, const float *hn, int nb, float *x, int order) {
     if (nb < 1 || nb > w.maxtok) { seterr("mmoe_moe: nb %d outside 1..%d", nb, w.maxtok); return -1; }
     HC(hipMemcpyAsync(w.hn, hn, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st));
     HC(hipMemcpyAsync(w.x, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st));
-    if (moe_dev(L, w.hn, nb, w.x, order)) return -1;
+    if (moe_dev(w, L, w.hn, nb, w.x, order)) return -1;
     HC(hipMemcpyAsync(x, w.x, (size_t)nb * MH * 4, hipMemcpyDeviceToHost, S.st));
     HC(hipStreamSynchronize(S.st));
     return 0;
 }
 
-int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) { return moe_dev(L, d_hn, nb, d_x, order); }
+int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) { return moe_dev(S.main, L, d_hn, nb, d_x, order); }
+
+// mmoe_moe_dev for batches of up to MMOE_NOALLOC_MAXTOK tokens with every work buffer in the library's static
+// scratch: no allocation of any kind. Calls on one device share that scratch (and queue on one stream).
+int mmoe_moe_dev_noalloc(int L, const float *d_hn, int nb, float *d_x, int order) {
+    if (!S.ready || !S.na.maxtok) { seterr("mmoe_moe_dev_noalloc: set the layers up first (mmoe_set_layer)"); return -1; }
+    if (nb < 1 || nb > MMOE_NOALLOC_MAXTOK) { seterr("mmoe_moe_dev_noalloc: nb %d outside 1..%d (the fixed scratch)", nb, MMOE_NOALLOC_MAXTOK); return -1; }
+    return moe_dev(S.na, L, d_hn, nb, d_x, order);
+}
 
 int mmoe_rmsnorm_dev(const float *d_x, const uint16_t *d_w, int nb, float *d_out) {
     if (ctx_ready()) return -1;
@@ -857,17 +894,17 @@ int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order) {
     if (!w.maxtok || nb < 1 || nb > w.maxtok) { seterr("mmoe_stack_dev: nb %d outside capacity %d", nb, w.maxtok); return -1; }
     for (int L = L0; L < L0 + nl; L++) {
         if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("mmoe_stack_dev: layer %d not set", L); return -1; }
-        if (nb <= DEC_MAXTOK && S_dec_enabled) { if (moe_dec(L, d_x, 1, nb, d_x, order)) return -1; continue; }
+        if (nb <= DEC_MAXTOK && S_dec_enabled) { if (moe_dec(w, L, d_x, 1, nb, d_x, order)) return -1; continue; }
         const uint16_t *pw = S.layers[L].post_ln;
         if (order == MMOE_ORDER_STEP || nb < 512) {   // the chain router forms hn itself (no rmsnorm launch)
             w.norm_x = d_x; w.norm_w = pw;
-            int rc = moe_dev(L, w.hn, nb, d_x, order);
+            int rc = moe_dev(w, L, w.hn, nb, d_x, order);
             w.norm_x = nullptr; w.norm_w = nullptr;
             if (rc) return -1;
             continue;
         }
         if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(d_x, pw, w.hn, nb); })) return -1;
-        if (moe_dev(L, w.hn, nb, d_x, order)) return -1;
+        if (moe_dev(w, L, w.hn, nb, d_x, order)) return -1;
     }
     return 0;
 }
