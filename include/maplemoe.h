@@ -178,9 +178,11 @@ int mmoe_read(int what, void *dst, size_t bytes);
 int mmoe_set_debug(int on);
 /* Batches of <= 8 tokens use three fused decode kernels (default on); off = the grouped-GEMM path. */
 int mmoe_set_decode_path(int on);
-/* Router of batches of >= 128 tokens in batch order: 1 (default) = exact fp32 FMA chains for every logit;
- * 0 = bf16 MFMA logits with the experts near each token's top 8 recomputed exactly (top-8 indices and their
- * logits stay maple.c's; the other logits and the softmax weights are within 1e-5). */
+/* Router of batches of >= 512 tokens in batch order: 0 (default) = bf16 MFMA logits on the input split into
+ * three exact bf16 parts, with every expert that a rounding bound cannot exclude from a token's top 8 recomputed
+ * in maple.c's exact chain order (top-8 indices and their logits stay maple.c's; the other logits, and through
+ * the softmax sum the weights, differ by about 1e-7); 1 = exact fp32 FMA chains for every logit. gfull_attn's
+ * logits, which maple.c consumes itself, always use the exact chains. */
 int mmoe_set_router_mode(int exact);
 const char *mmoe_last_error(void);
 

@@ -4,7 +4,7 @@
 // throughput: 8 experts of one token are 6.4 MB of codes, less than what the GPU keeps in flight. What costs
 // time is the number of dependent steps, so the layer is three launches and no block waits for another
 // inside a launch (device-scope fences that would publish data between blocks flush L2 on this part):
-//   k_dec_route   rmsnorm (optional) + router logits in maple.c's FMA-chain order, from a chain-major copy
+//   k_dec_route   rmsnorm (optional) + router logits in maple.c's FMA-chain order, from a chain-order copy
 //                 of the router so every thread issues all its loads at once
 //   k_dec_gateup  every block first repeats the small routing step (softmax/top-8 and the grouping of
 //                 maple.c:924-938 for <= 8 tokens, the int8 quantisation of its tokens), then computes its
@@ -34,7 +34,8 @@ __device__ __forceinline__ void decode4(uint32_t w, uint32_t *o) {
 // ---------------------------------------------------------------------------------------------------------
 // Router logits. One wave per block, 64/NCH experts per block (grid = MNE*NCH/64), lane = (expert, chain j):
 // chain j of expert e runs over columns j, j+NCH, ... (NCH = 16: maple.c:146-157, step; NCH = 8:
-// maple.c:853-889, batch). wc is the router in chain-major order, wc[e][j][m] = w[e][j + NCH*m]; a lane
+// maple.c:853-889, batch). wc is the router in chain order (k_router_chainmajor: word q of chain j holds its steps
+// 8q .. 8q+7, the words q of an expert's NCH chains side by side); a lane
 // issues all loads of its chain at kernel start and keeps them in registers for every token. hn sits in
 // LDS in the same chain-major order (padded against bank conflicts). do_norm: hn = rmsnorm(x, post_ln)
 // (maple.c:398-402, as k_rmsnorm), else hn = x. Block 0 writes hn.
@@ -55,10 +56,10 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
 #pragma unroll
     for (int i = 0; i < 8; i++) pw[i] = (do_norm && post_ln) ? *(const uint2 *)(post_ln + 4 * l + 256 * i) : make_uint2(0x3f803f80u, 0x3f803f80u);
     __builtin_amdgcn_sched_barrier(0);
-    const gptr_u4 *wp = (const gptr_u4 *)(wc + ((size_t)e * NCH + j) * LEN);
+    const gptr_u4 *wp = (const gptr_u4 *)(wc + (size_t)e * MH + j * 8);   // 16 bytes i of the chain at wp[i * NCH]
     v4i wv[LEN / 8];
 #pragma unroll
-    for (int i = 0; i < LEN / 8; i++) wv[i] = wp[i];
+    for (int i = 0; i < LEN / 8; i++) wv[i] = wp[i * NCH];
     float lw[32];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -117,12 +118,15 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
     }
 }
 
-// wc[e][j][m] = w[e][j + NCH*m]
+// The router in chain order for the kernels that run maple.c's FMA chains (NCH chains per expert, chain j over
+// columns j, j + NCH, j + 2 NCH, ...): wc[e][q][j][t] = w[e][j + NCH (8 q + t)]. Steps 8q .. 8q+7 of chain j are
+// one 16-byte word, and the words of step group q of all NCH chains are contiguous, so when lane j of a group of
+// NCH lanes loads its chain's word q, the group reads NCH x 16 contiguous bytes.
 template <int NCH>
 __global__ void k_router_chainmajor(const uint16_t *__restrict__ w, uint16_t *__restrict__ wc) {
     int i = blockIdx.x * 256 + threadIdx.x;      // over 256 * 2048 elements of wc
-    int e = i / MH, r = i % MH, j = r / (MH / NCH), m = r % (MH / NCH);
-    wc[i] = w[(size_t)e * MH + j + NCH * m];
+    int e = i / MH, r = i % MH, q = r / (NCH * 8), j = (r / 8) % NCH, t = r % 8;
+    wc[i] = w[(size_t)e * MH + j + NCH * (8 * q + t)];
 }
 
 // Grouping of the nb <= 8 tokens' top-8 (R.top) by one wave of the block, the counting sort of

@@ -187,7 +187,8 @@ __device__ __forceinline__ float hsum8(const float *v) {
 
 // Mid-size batches: one thread per (expert, chain) of one token, block = 256/NCH experts of token
 // blockIdx.y. The token's row sits in LDS chain-major (hc[j][m] = hn[j + NCH m]) and the router comes from
-// its chain-major copy (wc[e][j][m] = w[e][j + NCH m]), so a chain reads contiguous memory; its loads are
+// its chain-order copy (wc[e][q][j][t] = w[e][j + NCH (8 q + t)], k_router_chainmajor), so the NCH lanes of an
+// expert read NCH x 16 contiguous bytes per load; its loads are
 // issued 16 at a time ahead of the FMAs. Chain j runs over columns j, j + NCH, ... with fma(w, x, acc); the
 // chains are then folded as described above (NCH = 16: chain j + chain j+8 first).
 // NORM: `in` is the hidden state x and the block first forms hn = rmsnorm(x, post_ln) for its token with
@@ -217,10 +218,10 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    const gptr_u4 *wp = (const gptr_u4 *)(wc + ((size_t)e * NCH + j) * LEN);
+    const gptr_u4 *wp = (const gptr_u4 *)(wc + (size_t)e * MH + j * 8);   // 16 bytes q of the chain at wp[q * NCH]
     v4i wv[16];
 #pragma unroll
-    for (int q = 0; q < 16; q++) wv[q] = wp[q];
+    for (int q = 0; q < 16; q++) wv[q] = wp[q * NCH];
     if (NORM) {
         double sq = 0.0;
 #pragma unroll
@@ -255,7 +256,7 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
     for (int half = 0; half < LEN / 128; half++) {
         if (half > 0) {
 #pragma unroll
-            for (int q = 0; q < 16; q++) wv[q] = wp[half * 16 + q];
+            for (int q = 0; q < 16; q++) wv[q] = wp[(half * 16 + q) * NCH];
         }
 #pragma unroll
         for (int q = 0; q < 16; q++) {
@@ -379,69 +380,60 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ h
     }
 }
 
-// Large batches, approximate logits on the bf16 MFMA + exact refinement (k_cand, k_chain).
-// hn is split into two bf16 parts, h = h1 + h2 + r (h1 the top 8 significant bits by truncation, h2 the top 8
-// of what is left; both subtractions are exact and |r| <= 2^-15 |h|). The router is bf16 already, so every
-// product w * h_i is exact in fp32 and only the fp32 accumulation of the MFMA and the dropped r contribute
-// to the difference from maple.c's chain result L, bounded in k_cand.
-__global__ void __launch_bounds__(256) k_split2(const float *__restrict__ hn, int nb, uint16_t *__restrict__ hs,
-                                                float *__restrict__ hmax) {
-    int wv = threadIdx.x >> 6, l = threadIdx.x & 63, b = blockIdx.x * 4 + wv;
-    if (b >= nb) return;
-    const float *xr = hn + (size_t)b * MH;
-    float4 f[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) f[i] = *(const float4 *)(xr + (l + 64 * i) * 4);
-    float mx = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        float v[4] = {f[i].x, f[i].y, f[i].z, f[i].w};
-        uint32_t h1[4], h2[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            mx = fmaxf(mx, fabsf(v[u]));
-            uint32_t b1 = __float_as_uint(v[u]) & 0xffff0000u;
-            float r1 = v[u] - __uint_as_float(b1);
-            h1[u] = b1 >> 16; h2[u] = __float_as_uint(r1) >> 16;
-        }
-        int c = (l + 64 * i) * 4;
-        *(uint2 *)(hs + (size_t)b * MH + c) = make_uint2(h1[0] | (h1[1] << 16), h1[2] | (h1[3] << 16));
-        *(uint2 *)(hs + ((size_t)nb + b) * MH + c) = make_uint2(h2[0] | (h2[1] << 16), h2[2] | (h2[3] << 16));
-    }
-    mx = wave_max(mx);
-    if (l == 0) hmax[b] = mx;
-}
-
-// Partial logits on v_mfma_f32_32x32x16_bf16: P[q][b][e] = sum over columns [512 q, 512 q + 512) of
-// w[e][c] * (h1 + h2)[b][c]. Block: 64 experts x 64 tokens x one column quarter q (grid.z), 4 waves, wave
+// Large batches, approximate logits on the bf16 MFMA + exact refinement (k_refine_topk).
+// Each fp32 input h is split into three bf16 parts by truncation: h1 = the top 8 significant bits of h,
+// h2 = the top 8 of h - h1, h3 = the top 8 of what is left. Both subtractions are exact and the three parts
+// hold all 24 significant bits, so h = h1 + h2 + h3 exactly (for |h| above 2^-110; the MoE input is RMS-normed).
+// The router is bf16 already, so every product w * h_i is exact in fp32: only the fp32 accumulation of the MFMA
+// makes the approximate logit A differ from maple.c's chain result L, bounded in k_refine_topk.
+//
+// Partial logits on v_mfma_f32_32x32x16_bf16: P[q][b][e] = sum over columns [512 q, 512 q + 512) and the three
+// parts of w[e][c] * h_i[b][c], accumulated per chunk of 64 columns from zero (the 192 products of a chunk) and
+// the 8 chunk sums added in order, which keeps the rounding bound of k_refine_topk small. Block: 64 experts x 64 tokens x one column quarter q (grid.z), 4 waves, wave
 // (we, wt) owns the 32 x 32 output fragment (we, wt). Columns advance in chunks of 64: the router chunk
-// (64 x 64 bf16) and the two input parts (2 x 64 x 64 bf16) are read with coalesced 16-byte loads into
-// registers two chunks ahead, then stored to LDS (rows padded to 72 bf16). k_cand adds the 4 partials.
+// (64 x 64 bf16) and the input chunk (64 x 64 fp32) are read with coalesced 16-byte loads into registers two
+// chunks ahead, then stored to LDS (the input as its three bf16 parts; rows padded to 72 bf16).
 #define RM_KC 64
 #define RM_LR 72
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-__global__ void __launch_bounds__(256) k_router_mfma(const uint16_t *__restrict__ w, const uint16_t *__restrict__ hs, int nb,
+__device__ __forceinline__ void split3(v4i f0, v4i f1, v4i &p1, v4i &p2, v4i &p3) {
+    uint32_t v[8] = {(uint32_t)f0.x, (uint32_t)f0.y, (uint32_t)f0.z, (uint32_t)f0.w,
+                     (uint32_t)f1.x, (uint32_t)f1.y, (uint32_t)f1.z, (uint32_t)f1.w};
+    uint32_t a[8], b[8], c[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        uint32_t b1 = v[u] & 0xffff0000u;
+        float r1 = __uint_as_float(v[u]) - __uint_as_float(b1);
+        uint32_t b2 = __float_as_uint(r1) & 0xffff0000u;
+        float r2 = r1 - __uint_as_float(b2);
+        a[u] = b1 >> 16; b[u] = b2 >> 16; c[u] = __float_as_uint(r2) >> 16;
+    }
+    p1 = v4i{(int)(a[0] | a[1] << 16), (int)(a[2] | a[3] << 16), (int)(a[4] | a[5] << 16), (int)(a[6] | a[7] << 16)};
+    p2 = v4i{(int)(b[0] | b[1] << 16), (int)(b[2] | b[3] << 16), (int)(b[4] | b[5] << 16), (int)(b[6] | b[7] << 16)};
+    p3 = v4i{(int)(c[0] | c[1] << 16), (int)(c[2] | c[3] << 16), (int)(c[4] | c[5] << 16), (int)(c[6] | c[7] << 16)};
+}
+__global__ void __launch_bounds__(256) k_router_mfma(const uint16_t *__restrict__ w, const float *__restrict__ hn, int nb,
                                                      float *__restrict__ P) {
     __shared__ __attribute__((aligned(16))) uint16_t ws[64 * RM_LR];
-    __shared__ __attribute__((aligned(16))) uint16_t hsl[2][64 * RM_LR];
+    __shared__ __attribute__((aligned(16))) uint16_t hsl[3][64 * RM_LR];
     int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, r = l & 31, kg = l >> 5;
     int we = wv >> 1, wt = wv & 1;
     int e0 = blockIdx.y * 64, t0 = blockIdx.x * 64, kq = blockIdx.z * (MH / 4);
-    int srow = tid >> 3, spc = tid & 7;          // staging: row srow + 32 i, 16-byte piece spc of the chunk
-    const uint16_t *wsrc[2], *hsrc[2][2];
+    int srow = tid >> 3, spc = tid & 7;          // staging: row srow + 32 i, 8-column piece spc of the chunk
+    const uint16_t *wsrc[2]; const float *hsrc[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         wsrc[i] = w + (size_t)(e0 + srow + 32 * i) * MH + kq + spc * 8;
-#pragma unroll
-        for (int sp = 0; sp < 2; sp++) hsrc[sp][i] = hs + ((size_t)sp * nb + min(t0 + srow + 32 * i, nb - 1)) * MH + kq + spc * 8;
+        hsrc[i] = hn + (size_t)min(t0 + srow + 32 * i, nb - 1) * MH + kq + spc * 8;
     }
-    v4i rw[2][2], rh[2][2][2];                   // [ring][row half] / [ring][part][row half]
+    v4i rw[2][2], rh[2][2][2];                   // [ring][row half] / [ring][row half][16-byte half]
 #define RM_LOAD(q_, k_)                                                                              \
     {                                                                                                \
         _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
             rw[q_][i] = *(const gptr_u4 *)(wsrc[i] + (k_));                                          \
-            _Pragma("unroll") for (int sp = 0; sp < 2; sp++) rh[q_][sp][i] = *(const gptr_u4 *)(hsrc[sp][i] + (k_)); \
+            rh[q_][i][0] = *(const gptr_u4 *)(hsrc[i] + (k_));                                       \
+            rh[q_][i][1] = *(const gptr_u4 *)(hsrc[i] + (k_) + 4);                                   \
         }                                                                                            \
     }
     RM_LOAD(0, 0);
@@ -449,27 +441,34 @@ __global__ void __launch_bounds__(256) k_router_mfma(const uint16_t *__restrict_
     f32x16 acc;
 #pragma unroll
     for (int i = 0; i < 16; i++) acc[i] = 0.0f;
-#pragma unroll
+#pragma unroll 2
     for (int ck = 0; ck < MH / 4 / RM_KC; ck++) {
         const int q = ck & 1;
         __syncthreads();
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            *(v4i *)(&ws[(srow + 32 * i) * RM_LR + spc * 8]) = rw[q][i];
-#pragma unroll
-            for (int sp = 0; sp < 2; sp++) *(v4i *)(&hsl[sp][(srow + 32 * i) * RM_LR + spc * 8]) = rh[q][sp][i];
+            int o = (srow + 32 * i) * RM_LR + spc * 8;
+            *(v4i *)(&ws[o]) = rw[q][i];
+            v4i p1, p2, p3;
+            split3(rh[q][i][0], rh[q][i][1], p1, p2, p3);
+            *(v4i *)(&hsl[0][o]) = p1; *(v4i *)(&hsl[1][o]) = p2; *(v4i *)(&hsl[2][o]) = p3;
         }
         __syncthreads();
         if (ck + 2 < MH / 4 / RM_KC) RM_LOAD(q, (ck + 2) * RM_KC);
+        f32x16 cacc;   // the chunk's own sum from zero, added to acc after: 192 products per accumulation
+#pragma unroll
+        for (int i = 0; i < 16; i++) cacc[i] = 0.0f;
 #pragma unroll
         for (int kk = 0; kk < RM_KC; kk += 16) {
             bf16x8 av = *(const bf16x8 *)(&ws[(we * 32 + r) * RM_LR + kk + kg * 8]);
 #pragma unroll
-            for (int sp = 0; sp < 2; sp++) {
+            for (int sp = 0; sp < 3; sp++) {
                 bf16x8 bv = *(const bf16x8 *)(&hsl[sp][(wt * 32 + r) * RM_LR + kk + kg * 8]);
-                acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, acc, 0, 0, 0);
+                cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, cacc, 0, 0, 0);
             }
         }
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[i] = acc[i] + cacc[i];
     }
 #undef RM_LOAD
     // D: register i -> expert row (i/4)*8 + kg*4 + i%4 of the fragment, token column r
@@ -741,34 +740,58 @@ __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl
     }
 }
 
-// Exact top-8 from approximate logits (k_router_mfma), in two kernels before k_topk_quant.
-// |A - L| <= RG_ERRK * max|h_b| * max_e sum_c |w_ec| = err_b bounds the gap between the MFMA logit A and
-// maple.c's chain logit L: 2 * 2048 fp32 accumulations on the MFMA side and 256 + 3 on the chain side, each
-// at most one rounding of 2^-24 times the running magnitude (at most sum |w h|), plus the dropped input
-// remainder (2^-15 = 512 x 2^-24 of |h|), 4867 x 2^-24 x sum |w h| in all; times 1.01 for the bf16 parts and
-// 2 for safety. Every expert with A >= a8 - 2 err_b (a8 = the 8th largest A) is a candidate and gets its exact
-// chain logit in maple.c's batch order; no other expert can reach the top 8 of the exact logits, because the 8
-// experts with A >= a8 have L >= a8 - err_b while the rest have L < a8 - err_b. The softmax/top-8 of
-// k_topk_quant then runs on the row of exact (candidates) and approximate (the rest) logits, so the picks and
-// their order are maple.c's; p, and so tw, differ only through the softmax sum's approximate small terms.
-#define RG_ERRK (2.0f * 4867.0f * 1.01f / 16777216.0f)
-#define RG_MAXC 32   // candidates per token resolved by the chain kernel; more than that: all 256 experts
-// k_cand: one wave per token: candidate list cand[b][0..nc) (ascending expert), nc in ncand[b]
-// A = (P0 + P1) + (P2 + P3) + bias is written to rl; k_chain then overwrites the candidates' entries.
-__global__ void __launch_bounds__(256) k_cand(const float *__restrict__ P, int nb, const float *__restrict__ bias,
-                                              const float *__restrict__ hmax, const float *__restrict__ w1max,
-                                              float *__restrict__ rl, int *__restrict__ cand, int *__restrict__ ncand) {
+// Exact top-8 from the approximate logits of k_router_mfma, fused with the softmax/top-8 of the token.
+// |A - L| <= RG_ERRK * max|h_b| * max_e sum_c |w_ec| = err_b bounds the gap between the MFMA logit A and maple.c's
+// chain logit L. On the MFMA side a product of a column and an input part is exact and passes through at most
+// 192 roundings inside its chunk's accumulation (every one of the chunk's 3 x 64 products rounded on its own,
+// the worst case for the MFMA's internal sums), 8 for the chunk sums of its quarter, 3 for the quarter partials
+// and 1 for the bias; on the chain side through 256 FMAs and 3 hsum additions. Each rounding is at most 2^-24
+// times the running magnitude (at most sum |w h|): 463 x 2^-24 x sum |w h| in all; times 1.01 for the margin of
+// w1max's own float sum and the parts' sum of magnitudes, and 2 for safety. Every expert with A >= a8 - 2 err_b (a8 = the 8th largest A) is a candidate and gets its exact chain
+// logit in maple.c's batch order; no other expert can reach the top 8 of the exact logits, because the 8
+// experts with A >= a8 have L >= a8 - err_b while the rest have L < a8 - err_b. The softmax/top-8 then runs on
+// the row of exact (candidates) and approximate (the rest) logits, so the picks and their order are maple.c's;
+// p, and so tw, differ only through the softmax sum's approximate small terms.
+#define RG_ERRK (2.0f * 463.0f * 1.01f / 16777216.0f)
+#define RT_HP 260    // LDS floats per chain of the staged input (256 + 4 against bank conflicts)
+// One wave per token, 4 tokens per block (grid = ceil(nb / 4)); the tokens' int8 quantisation is k_quant, a
+// launch of its own (blocks of this kernel hold many registers). The input row sits in LDS chain-major
+// (hc[j][m] = hn[j + 8m]); lane = (candidate slot l / 8, chain l % 8), so 8 candidates are resolved per pass,
+// each lane's 256-long FMA chain reading the router's chain-order copy (k_router_chainmajor, NCH = 8) with all
+// 32 of its 16-byte loads issued before the FMAs. Writes rl (exact for candidates, else approximate), top, tw
+// and the per-chunk expert counts for k_group.
+__global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P, const float *__restrict__ hn, int nb,
+                                                     const uint16_t *__restrict__ wc8, const float *__restrict__ bias,
+                                                     const float *__restrict__ w1max, float *__restrict__ rl,
+                                                     int *__restrict__ top, float *__restrict__ tw, int *__restrict__ hist) {
+    __shared__ __attribute__((aligned(16))) float hsc[4][8 * RT_HP];
+    __shared__ float row[4][MNE], E[4][MNE];
+    __shared__ int cand[4][MNE];
     int wv = threadIdx.x >> 6, l = threadIdx.x & 63, b = blockIdx.x * 4 + wv;
-    if (b >= nb) return;
+    if (b >= nb) return;   // whole wave; no block-wide barrier below
+    const float *xr = hn + (size_t)b * MH;
+    float4 f[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) f[i] = *(const float4 *)(xr + (l + 64 * i) * 4);
     float a[4];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         size_t o = (size_t)b * MNE + l + 64 * i, qs = (size_t)nb * MNE;
         float v = (P[o] + P[o + qs]) + (P[o + 2 * qs] + P[o + 3 * qs]);
         if (bias) v = v + bias[l + 64 * i];
-        a[i] = v; rl[o] = v;
+        a[i] = v;
     }
-    float err = RG_ERRK * hmax[b] * w1max[0];
+    float *hc = &hsc[wv][0];
+    float hm = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        int c = (l + 64 * i) * 4;
+        float v4[4] = {f[i].x, f[i].y, f[i].z, f[i].w};
+#pragma unroll
+        for (int u = 0; u < 4; u++) { hc[((c + u) & 7) * RT_HP + ((c + u) >> 3)] = v4[u]; hm = fmaxf(hm, fabsf(v4[u])); }
+    }
+    hm = wave_max(hm);
+    // a8: the 8th largest approximate logit (8 rounds of the wave maximum, lowest index first)
     float rem[4] = {a[0], a[1], a[2], a[3]}, a8 = 0.0f;
     for (int k = 0; k < MTOPK; k++) {
         float m = wave_max(fmaxf(fmaxf(rem[0], rem[1]), fmaxf(rem[2], rem[3])));
@@ -777,62 +800,38 @@ __global__ void __launch_bounds__(256) k_cand(const float *__restrict__ P, int n
         int e = m0 ? __ffsll((long long)m0) - 1 : m1 ? 64 + __ffsll((long long)m1) - 1 : m2 ? 128 + __ffsll((long long)m2) - 1 : 192 + __ffsll((long long)m3) - 1;
         if (l == (e & 63)) { int i = e >> 6; rem[0] = i == 0 ? -INFINITY : rem[0]; rem[1] = i == 1 ? -INFINITY : rem[1]; rem[2] = i == 2 ? -INFINITY : rem[2]; rem[3] = i == 3 ? -INFINITY : rem[3]; }
     }
-    float thr = a8 - 2.0f * err;
+    float thr = a8 - 2.0f * (RG_ERRK * hm * w1max[0]);
     int nc = 0;
     unsigned long long lanemask = (1ull << l) - 1ull;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
+        row[wv][l + 64 * i] = a[i];
         bool c = a[i] >= thr;
         unsigned long long m = __ballot(c);
-        int pos = nc + popc64(m & lanemask);
-        if (c && pos < RG_MAXC) cand[(size_t)b * RG_MAXC + pos] = l + 64 * i;
+        if (c) cand[wv][nc + popc64(m & lanemask)] = l + 64 * i;
         nc += popc64(m);
     }
-    if (l == 0) ncand[b] = nc;
-}
-// k_chain: exact chain logits (maple.c:870-889 order, 8 chains over columns j + 8m, hsum8, + bias) of the
-// candidates, written over the approximate logits. Block = 4 tokens x 8 candidate slots x 8 chains; grid.y
-// = RG_MAXC / 8 groups of candidate slots (tokens with more than RG_MAXC candidates: every expert, all groups
-// striding over 256). wc8 = router chain-major (wc8[e][j][m] = w[e][j + 8 m]).
-__global__ void __launch_bounds__(256) k_chain(const float *__restrict__ hn, int nb, const uint16_t *__restrict__ wc8,
-                                               const float *__restrict__ bias, const int *__restrict__ cand,
-                                               const int *__restrict__ ncand, float *__restrict__ rl) {
-    __shared__ __attribute__((aligned(16))) float hsc[4][8][260];
-    int tid = threadIdx.x, tk = tid >> 6, l = tid & 63, j = l & 7, slot = l >> 3;
-    int b = blockIdx.x * 4 + tk;
-    bool live = b < nb;
-    int bb = live ? b : nb - 1;
-    const float *xr = hn + (size_t)bb * MH;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        int c = (l + 64 * i) * 4;
-        float4 f = *(const float4 *)(xr + c);
-        hsc[tk][(c & 7) + 0][c >> 3] = f.x; hsc[tk][(c & 7) + 1][c >> 3] = f.y;
-        hsc[tk][(c & 7) + 2][c >> 3] = f.z; hsc[tk][(c & 7) + 3][c >> 3] = f.w;
-    }
-    __syncthreads();
-    if (!live) return;
-    int nc = ncand[b];
-    bool all = nc > RG_MAXC;
-    int n = all ? MNE : nc;
-    // slots of this block: blockIdx.y * 8 + slot, + gridDim.y * 8, ... (one round unless every expert is needed)
-    for (int c0 = blockIdx.y * 8; c0 < n; c0 += gridDim.y * 8) {   // c0 is uniform over the wave
-        int ci = c0 + slot;
-        bool on = ci < n;
-        int e = all ? (on ? ci : 0) : cand[(size_t)b * RG_MAXC + (on ? ci : 0)];
-        const gptr_u4 *wp = (const gptr_u4 *)(wc8 + ((size_t)e * 8 + j) * 256);
-        const float *hc = &hsc[tk][j][0];
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    // exact chain logits of the candidates, 8 per pass (nc is at least 8 and at most 256)
+    int slot = l >> 3, j = l & 7;
+    const float *hj = hc + j * RT_HP;
+    for (int c0 = 0; c0 < nc; c0 += 8) {   // c0 and nc are uniform over the wave
+        bool on = c0 + slot < nc;
+        int e = cand[wv][on ? c0 + slot : 0];
+        const gptr_u4 *wp = (const gptr_u4 *)(wc8 + (size_t)e * MH + j * 8);   // 16 bytes q of the chain at wp[q * 8]
         float acc = 0.0f;
-#pragma unroll 1
-        for (int mb = 0; mb < 4; mb++) {
-            v4i wq[8];
 #pragma unroll
-            for (int q = 0; q < 8; q++) wq[q] = wp[mb * 8 + q];
+        for (int hb = 0; hb < 2; hb++) {   // the chain's weights in two halves of 16 x 16 bytes (registers)
+            v4i wq[16];
 #pragma unroll
-            for (int q = 0; q < 8; q++) {
-                float4 h0 = *(const float4 *)(hc + mb * 64 + q * 8), h1 = *(const float4 *)(hc + mb * 64 + q * 8 + 4);
-                v4i wv = wq[q];
-                uint32_t q0 = (uint32_t)wv.x, q1 = (uint32_t)wv.y, q2 = (uint32_t)wv.z, q3 = (uint32_t)wv.w;
+            for (int q = 0; q < 16; q++) wq[q] = wp[(hb * 16 + q) * 8];
+#pragma unroll
+            for (int q16 = 0; q16 < 16; q16++) {
+                int q = hb * 16 + q16;
+                if ((q & 1) == 0) __builtin_amdgcn_sched_barrier(0);   // two steps per scheduling region (registers)
+                float4 h0 = *(const float4 *)(hj + q * 8), h1 = *(const float4 *)(hj + q * 8 + 4);
+                uint32_t q0 = (uint32_t)wq[q16].x, q1 = (uint32_t)wq[q16].y, q2 = (uint32_t)wq[q16].z, q3 = (uint32_t)wq[q16].w;
                 acc = __builtin_fmaf(__uint_as_float(q0 << 16), h0.x, acc); acc = __builtin_fmaf(__uint_as_float(q0 & 0xffff0000u), h0.y, acc);
                 acc = __builtin_fmaf(__uint_as_float(q1 << 16), h0.z, acc); acc = __builtin_fmaf(__uint_as_float(q1 & 0xffff0000u), h0.w, acc);
                 acc = __builtin_fmaf(__uint_as_float(q2 << 16), h1.x, acc); acc = __builtin_fmaf(__uint_as_float(q2 & 0xffff0000u), h1.y, acc);
@@ -843,11 +842,17 @@ __global__ void __launch_bounds__(256) k_chain(const float *__restrict__ hn, int
 #pragma unroll
         for (int i = 0; i < 8; i++) s8[i] = __shfl(acc, (l & ~7) + i, 64);
         if (j == 0 && on) {
-            float r = hsum8(s8);
-            if (bias) r = r + bias[e];
-            rl[(size_t)b * MNE + e] = r;
+            float rv = hsum8(s8);
+            if (bias) rv = rv + bias[e];
+            row[wv][e] = rv;
         }
     }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+    for (int i = 0; i < 4; i++) rl[(size_t)b * MNE + l + 64 * i] = row[wv][l + 64 * i];
+    int ek = topk_wave(&row[wv][0], E[wv], l, top + b * MTOPK, tw + b * MTOPK);
+    if (hist && l < MTOPK) atomicAdd(&hist[(b >> 6) * MNE + ek], 1);   // per-chunk expert counts for k_group
 }
 
 // Quantisation of two FF-long (512) vectors by one wave, as quant_wave: lanes 0-31 hold one vector, lanes

@@ -16,6 +16,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <unistd.h>
+#include <tuple>
 #include <vector>
 #include "kernels.h"
 #include "decode.h"
@@ -68,11 +69,8 @@ struct Work {
     int hist_used = 0;              // entries of hist the device grouping filled; the combine clears them
     const float *norm_x = nullptr;  // set by mmoe_stack_dev: the router normalises this x into hn (post_ln norm_w)
     const uint16_t *norm_w = nullptr;
-    uint16_t *hs = nullptr;         // MoE input split into 2 bf16 parts [2][T][2048] (approximate router)
-    float *rpart = nullptr;         // partial router logits [4][T][256]
-    float *hmax = nullptr;          // max |hn| per token
-    int *cand = nullptr, *ncand = nullptr;   // refinement candidates [T][RG_MAXC], counts [T]
-    bool refine = false;            // the last router call left approximate logits for k_cand / k_chain
+    float *rpart = nullptr;         // partial router logits [4][T][256] (approximate router)
+    bool refine = false;            // the last router call left approximate logits for k_refine_topk
 };
 
 // Where a Work set's buffers come from: hipMalloc (c == nullptr) or a fixed device span carved in order
@@ -120,6 +118,23 @@ static struct {
     int ncu = 256;             // compute units of the device (persistent grids)
 } S;
 
+// Kernel launch on the library stream. The arguments are converted to the kernel's parameter types and passed
+// by address (hipLaunchKernel). While a launch() profiles, the dispatch itself carries start/stop events
+// (hipExtLaunchKernel): their interval is the kernel's execution on the device, the duration rocprofv3 reports,
+// without the extra barrier packets that events recorded around the launch would add.
+static hipEvent_t g_ke[2];          // set by launch() while profiling, else null
+static hipError_t g_klerr = hipSuccess;
+template <typename... P, typename... A>
+static void kl(void (*f)(P...), dim3 g, dim3 b, size_t shm, A &&...a) {
+    static_assert(sizeof...(P) == sizeof...(A), "kernel argument count");
+    std::tuple<P...> v(static_cast<P>(a)...);
+    void *ptr[sizeof...(P)];
+    std::apply([&](auto &...x) { int i = 0; ((ptr[i++] = (void *)&x), ...); }, v);
+    hipError_t e = g_ke[0] ? hipExtLaunchKernel((const void *)f, g, b, ptr, shm, S.st, g_ke[0], g_ke[1], 0)
+                           : hipLaunchKernel((const void *)f, g, b, ptr, shm, S.st);
+    if (e != hipSuccess) g_klerr = e;
+}
+
 // small (carved sets): at most 64 tokens, so only the decode and 16-token-tile paths run: no int16 down side
 // buffer (2048+ pairs only), no approximate-router buffers (512+ tokens), no host-side hidden state copy.
 static int work_alloc(Work &w, int maxtok, Carve *c = nullptr) {
@@ -136,13 +151,12 @@ static int work_alloc(Work &w, int maxtok, Carve *c = nullptr) {
         wbuf(w.down, P * MH * 4, c) || wbuf(w.eu, MNE * 4, c) || wbuf(w.pu, P * 4, c))
         return -1;
     // the per-chunk expert counts start at zero; the combine after k_group clears what it used
-    k_fill_zero<<<(nch * MNE + 255) / 256, 256, 0, S.st>>>(w.hist, nch * MNE);
+    kl(k_fill_zero, (nch * MNE + 255) / 256, 256, 0, w.hist, nch * MNE);
     HC(hipGetLastError());
     if (c) return 0;
     HC(hipMalloc(&w.x, T * MH * 4));
     HC(hipMalloc(&w.dov, P * MH * 4));
-    HC(hipMalloc(&w.hs, 2 * T * MH * 2)); HC(hipMalloc(&w.hmax, T * 4)); HC(hipMalloc(&w.rpart, 4 * T * MNE * 4));
-    HC(hipMalloc(&w.cand, T * RG_MAXC * 4)); HC(hipMalloc(&w.ncand, T * 4));
+    HC(hipMalloc(&w.rpart, 4 * T * MNE * 4));
     HC(hipStreamSynchronize(S.st));
     return 0;
 }
@@ -183,14 +197,16 @@ static int ctx_ready() {
     return 0;
 }
 
-// Launch helper: optional per-kernel event timing on the library stream.
+// Launch helper: one kernel (f calls kl once); while profiling, its device execution time is added to kid's.
 template <typename F>
 static int launch(int kid, F &&f) {
-    if (S.prof) HC(hipEventRecord(S.pe[0], S.st));
+    g_klerr = hipSuccess;
+    if (S.prof) { g_ke[0] = S.pe[0]; g_ke[1] = S.pe[1]; }
     f();
+    g_ke[0] = g_ke[1] = nullptr;
+    if (g_klerr != hipSuccess) { seterr("kernel launch failed: %s", hipGetErrorString(g_klerr)); (void)hipGetLastError(); return -1; }
     HC(hipGetLastError());
     if (S.prof) {
-        HC(hipEventRecord(S.pe[1], S.st));
         HC(hipEventSynchronize(S.pe[1]));
         float ms = 0; HC(hipEventElapsedTime(&ms, S.pe[0], S.pe[1]));
         S.prof_ms[kid] += ms; S.prof_n[kid]++;
@@ -204,7 +220,7 @@ static int launch(int kid, F &&f) {
 static int tile_tn(int np) { return np >= 2048 ? 64 : 16; }
 
 // Router logits of nb tokens (d_hn) with layer L's router; order 0 = batch (maple.c:853-889), 1 = step (bf_row)
-static bool S_router_exact = true;    // large batches: exact chain GEMM (else MFMA logits + exact refinement)
+static bool S_router_exact = false;   // batches of 512+: MFMA logits + exact refinement (else the exact chain GEMM)
 // exact_only: never the approximate large-batch router (callers that hand the logits themselves to the host)
 static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bool exact_only = false) {
     LayerW &lw = S.layers[L];
@@ -213,43 +229,38 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bo
     // w.norm_x set (stacked path): the chain routers form hn = rmsnorm(x, post_ln) into d_hn themselves
     float *hn_w = const_cast<float *>(d_hn);
     if (order == MMOE_ORDER_STEP) {
-        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { k_router_chains<16, true><<<dim3(MNE * 16 / 256, nb), 256, 0, S.st>>>(w.norm_x, nb, lw.rc16, lw.bias, w.rl, w.norm_w, hn_w); });
-        return launch(MMOE_K_ROUTER, [&] { k_router_chains<16><<<dim3(MNE * 16 / 256, nb), 256, 0, S.st>>>(d_hn, nb, lw.rc16, lw.bias, w.rl); });
+        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16, true>, dim3(MNE * 16 / 256, nb), 256, 0, w.norm_x, nb, lw.rc16, lw.bias, w.rl, w.norm_w, hn_w); });
+        return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16>, dim3(MNE * 16 / 256, nb), 256, 0, d_hn, nb, lw.rc16, lw.bias, w.rl, nullptr, nullptr); });
     }
     if (nb < 512) {   // one block per (token, 32 experts): 8 nb blocks, router reread from L2 per token
-        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { k_router_chains<8, true><<<dim3(MNE * 8 / 256, nb), 256, 0, S.st>>>(w.norm_x, nb, lw.rc8, lw.bias, w.rl, w.norm_w, hn_w); });
-        return launch(MMOE_K_ROUTER, [&] { k_router_chains<8><<<dim3(MNE * 8 / 256, nb), 256, 0, S.st>>>(d_hn, nb, lw.rc8, lw.bias, w.rl); });
+        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<8, true>, dim3(MNE * 8 / 256, nb), 256, 0, w.norm_x, nb, lw.rc8, lw.bias, w.rl, w.norm_w, hn_w); });
+        return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<8>, dim3(MNE * 8 / 256, nb), 256, 0, d_hn, nb, lw.rc8, lw.bias, w.rl, nullptr, nullptr); });
     }
     if (S_router_exact || exact_only)
-        return launch(MMOE_K_ROUTER, [&] { k_router_gemm<4><<<dim3((nb + 15) / 16, MNE / RG_BE), 256, 0, S.st>>>(d_hn, nb, lw.rf8, lw.bias, w.rl); });
-    // approximate logits on the bf16 MFMA; k_cand + k_chain make the top-8 exact
+        return launch(MMOE_K_ROUTER, [&] { kl(k_router_gemm<4>, dim3((nb + 15) / 16, MNE / RG_BE), 256, 0, d_hn, nb, lw.rf8, lw.bias, w.rl); });
+    // approximate logits on the bf16 MFMA; k_refine_topk makes the top-8 exact
     w.refine = true;
-    return launch(MMOE_K_ROUTER, [&] {
-        k_split2<<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, w.hs, w.hmax);
-        k_router_mfma<<<dim3((nb + 63) / 64, MNE / 64, 4), 256, 0, S.st>>>(lw.router, w.hs, nb, w.rpart);
-    });
+    return launch(MMOE_K_ROUTER, [&] { kl(k_router_mfma, dim3((nb + 63) / 64, MNE / 64, 4), 256, 0, lw.router, d_hn, nb, w.rpart); });
 }
 
 // softmax/top-8, the int8 quantisation of hn and the grouping of nb tokens; eptr filled from layer L's table
 static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) {
     int nch = (nb + 63) / 64;
-    if (w.refine) {
+    if (w.refine) {   // exact logits of each token's candidates, then its softmax/top-8 (and the quantisation)
         const LayerW &lw = S.layers[L];
-        if (launch(MMOE_K_ROUTER, [&] {
-                k_cand<<<(nb + 3) / 4, 256, 0, S.st>>>(w.rpart, nb, lw.bias, w.hmax, lw.w1max, w.rl, w.cand, w.ncand);
-                k_chain<<<dim3((nb + 3) / 4, 2), 256, 0, S.st>>>(d_hn, nb, lw.rc8, lw.bias, w.cand, w.ncand, w.rl);
-            })) return -1;
-    }
-    if (launch(MMOE_K_TOPK, [&] { k_topk_quant<<<dim3((nb + 3) / 4, 2), 256, 0, S.st>>>(w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
+        if (launch(MMOE_K_TOPK, [&] { kl(k_refine_topk, (nb + 3) / 4, 256, 0, w.rpart, d_hn, nb, lw.rc8, lw.bias, lw.w1max, w.rl, w.top, w.tw, w.hist); }) ||
+            launch(MMOE_K_QUANT, [&] { kl(k_quant<MH>, (nb + 3) / 4, 256, 0, d_hn, nb, w.qx, w.qsx, w.qsumx); }))
+            return -1;
+    } else if (launch(MMOE_K_TOPK, [&] { kl(k_topk_quant, dim3((nb + 3) / 4, 2), 256, 0, w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
     w.hist_used = nch * MNE;   // cleared by this call's combine
     return launch(MMOE_K_GROUP, [&] {
-        k_group<<<nch, 512, 0, S.st>>>(w.hist, nb, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles, w.eu, w.top, w.tw, w.utok, w.uw,
+        kl(k_group, nch, 512, 0, w.hist, nb, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles, w.eu, w.top, w.tw, w.utok, w.uw,
                                        w.tp, w.sp, w.pu);
     });
 }
 
 static int stage_quant_x(Work &w, const float *d_hn, int nb) {
-    return launch(MMOE_K_QUANT, [&] { k_quant<MH><<<(nb + 3) / 4, 256, 0, S.st>>>(d_hn, nb, w.qx, w.qsx, w.qsumx); });
+    return launch(MMOE_K_QUANT, [&] { kl(k_quant<MH>, (nb + 3) / 4, 256, 0, d_hn, nb, w.qx, w.qsx, w.qsumx); });
 }
 
 // gate/up (+SiLU), act quantisation, down for np pairs under w.plan / w.eptr / w.utok
@@ -259,27 +270,27 @@ static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8)
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
     if (tn == 64) {   // checks on: int32 sums into the debug buffer; else the fp32 activation into w.act
         int nblk = (int)grid8(S.ncu * 2 < maxtiles * (MFF / 128) ? S.ncu * 2 : maxtiles * (MFF / 128));   // two persistent blocks per CU
-        if (dg) return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<false><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, dg); });
-        return launch(MMOE_K_GATEUP, [&] { k_gateup_pk<true><<<nblk, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act); });
+        if (dg) return launch(MMOE_K_GATEUP, [&] { kl(k_gateup_pk<false>, nblk, 256, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, dg); });
+        return launch(MMOE_K_GATEUP, [&] { kl(k_gateup_pk<true>, nblk, 256, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act); });
     }
-    return launch(MMOE_K_GATEUP, [&] { k_gateup<16, GU16_W, GU16_RF><<<grid8(maxtiles * (MFF / (16 * GU16_W * GU16_RF))), 64 * GU16_W, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
+    return launch(MMOE_K_GATEUP, [&] { kl(k_gateup<16, GU16_W, GU16_RF>, grid8(maxtiles * (MFF / (16 * GU16_W * GU16_RF))), 64 * GU16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
 static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
     // large batches: 4 row blocks per workgroup (half the activation staging per row); else 2 (more workgroups)
     if (tn == 64 && compact && maxtiles >= S.ncu)
-        return launch(MMOE_K_DOWN, [&] { k_down_tile<4, true><<<grid8(maxtiles * (MH / 256 / 4)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
-    if (tn == 64 && compact) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB, true><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
-    if (tn == 64) return launch(MMOE_K_DOWN, [&] { k_down_tile<DN_RPB, false><<<grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, nullptr, dd); });
-    return launch(MMOE_K_DOWN, [&] { k_down<16, DN16_W, DN16_RF><<<grid8(maxtiles * (MH / (16 * DN16_W * DN16_RF))), 64 * DN16_W, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
+        return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<4, true>, grid8(maxtiles * (MH / 256 / 4)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
+    if (tn == 64 && compact) return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<DN_RPB, true>, grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
+    if (tn == 64) return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<DN_RPB, false>, grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, nullptr, dd); });
+    return launch(MMOE_K_DOWN, [&] { kl(k_down<16, DN16_W, DN16_RF>, grid8(maxtiles * (MH / (16 * DN16_W * DN16_RF))), 64 * DN16_W, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
 }
 
 static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
     if (tn == 64) {
         // checks on: activation from the int32 sums in the debug buffer; else gate/up wrote it already
-        if (dg) return launch(MMOE_K_QUANT_ACT, [&] { k_act_quant<<<maxtiles * 8, 256, 0, S.st>>>(w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, dg, w.act, w.qa, w.qsa, w.qsuma); });
-        return launch(MMOE_K_QUANT_ACT, [&] { k_quant_act<<<(np + 7) / 8, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); });
+        if (dg) return launch(MMOE_K_QUANT_ACT, [&] { kl(k_act_quant, maxtiles * 8, 256, 0, w.plan, w.tiles, w.eptr, w.utok, w.qsx, w.qsumx, dg, w.act, w.qa, w.qsa, w.qsuma); });
+        return launch(MMOE_K_QUANT_ACT, [&] { kl(k_quant_act, (np + 7) / 8, 256, 0, w.act, np, w.qa, w.qsa, w.qsuma); });
     }
-    return launch(MMOE_K_QUANT_ACT, [&] { k_quant<MFF><<<(np + 3) / 4, 256, 0, S.st>>>(w.act, np, w.qa, w.qsa, w.qsuma); });
+    return launch(MMOE_K_QUANT_ACT, [&] { kl(k_quant<MFF>, (np + 3) / 4, 256, 0, w.act, np, w.qa, w.qsa, w.qsuma); });
 }
 // device_grouping: the grouping came from k_group (pu is valid), so the 64-token-tile path may
 // hand the down results to k_combine as int16 (not with checks on: the tests read them as fp32)
@@ -301,8 +312,8 @@ static int stage_combine(Work &w, int nb, float *d_x, int mode) {
     w.hist_used = 0;
     int *hz = hzn ? w.hist : nullptr;
     if (w.compact)
-        return launch(MMOE_K_COMBINE, [&] { k_combine16<<<nb, 256, 0, S.st>>>((const int16_t *)w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode, w.pu, w.eptr, w.qsa, w.dov, hz, hzn); });
-    return launch(MMOE_K_COMBINE, [&] { k_combine<<<(n + 255) / 256, 256, 0, S.st>>>(w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode, hz, hzn); });
+        return launch(MMOE_K_COMBINE, [&] { kl(k_combine16, nb, 256, 0, (const int16_t *)w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode, w.pu, w.eptr, w.qsa, w.dov, hz, hzn); });
+    return launch(MMOE_K_COMBINE, [&] { kl(k_combine, (n + 255) / 256, 256, 0, w.down, w.uw, w.tp, w.sp, w.tw, nb, d_x, mode, hz, hzn); });
 }
 
 // Small batches (decode): three kernels, see decode.h. in = hn (do_norm 0) or the hidden state x whose
@@ -312,21 +323,21 @@ static int launch_dec_gateup(Work &w, int nb, int L) {
     int maxu = nb * MTOPK < MNE ? nb * MTOPK : MNE;
     int *dg = S.debug ? w.dbg_gu : nullptr;
     const ExpPtr *tab = S.layers[L].tab;
-    return launch(MMOE_K_GATEUP, [&] { k_dec_gateup<<<dim3(MFF / 8, maxu), 256, 0, S.st>>>(w.rl, w.hn, nb, tab, w.top, w.tw, w.plan, w.utok, w.uw, w.tp, w.sp, w.eptr, w.qx, w.qsx, w.qsumx, w.act, dg); });
+    return launch(MMOE_K_GATEUP, [&] { kl(k_dec_gateup, dim3(MFF / 8, maxu), 256, 0, w.rl, w.hn, nb, tab, w.top, w.tw, w.plan, w.utok, w.uw, w.tp, w.sp, w.eptr, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
 static int launch_dec_down(Work &w, int nb, float *d_x, int order) {
     int *dd = S.debug ? w.dbg_dn : nullptr;
     int mode = order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH;
-    return launch(MMOE_K_DOWN, [&] { k_dec_down<<<MH / 8, 256, 0, S.st>>>(w.plan, w.eptr, w.act, w.qa, w.qsa, w.qsuma, w.tp, w.sp, w.uw, w.tw, nb, d_x, mode, w.down, dd); });
+    return launch(MMOE_K_DOWN, [&] { kl(k_dec_down, MH / 8, 256, 0, w.plan, w.eptr, w.act, w.qa, w.qsa, w.qsuma, w.tp, w.sp, w.uw, w.tw, nb, d_x, mode, w.down, dd); });
 }
 static int moe_dec(Work &w, int L, const float *in, int do_norm, int nb, float *d_x, int order) {
     LayerW &lw = S.layers[L];
     LAST.w = &w; LAST.np = nb * MTOPK; LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = nullptr; LAST.dec = 1; LAST.x = d_x;
     const uint16_t *pln = do_norm ? lw.post_ln : nullptr;
     if (order == MMOE_ORDER_STEP) {
-        if (launch(MMOE_K_ROUTER, [&] { k_dec_route<16><<<MNE * 16 / 64, 64, 0, S.st>>>(in, nb, pln, do_norm, lw.rc16, lw.bias, w.hn, w.rl); })) return -1;
+        if (launch(MMOE_K_ROUTER, [&] { kl(k_dec_route<16>, MNE * 16 / 64, 64, 0, in, nb, pln, do_norm, lw.rc16, lw.bias, w.hn, w.rl); })) return -1;
     } else {
-        if (launch(MMOE_K_ROUTER, [&] { k_dec_route<8><<<MNE * 8 / 64, 64, 0, S.st>>>(in, nb, pln, do_norm, lw.rc8, lw.bias, w.hn, w.rl); })) return -1;
+        if (launch(MMOE_K_ROUTER, [&] { kl(k_dec_route<8>, MNE * 8 / 64, 64, 0, in, nb, pln, do_norm, lw.rc8, lw.bias, w.hn, w.rl); })) return -1;
     }
     if (launch_dec_gateup(w, nb, L)) return -1;
     return launch_dec_down(w, nb, d_x, order);
@@ -366,7 +377,7 @@ static int experts_host_grouping(Work &w, int nb, int nu, const ExpPtr *eptr_h, 
     HC(hipMemcpyAsync(w.utok, ptok, sizeof(int) * np, hipMemcpyHostToDevice, S.st));
     if (pw) HC(hipMemcpyAsync(w.uw, pw, sizeof(float) * np, hipMemcpyHostToDevice, S.st));
     if (tp) HC(hipMemcpyAsync(w.tp, tp, sizeof(int) * nb * MTOPK, hipMemcpyHostToDevice, S.st));
-    if (launch(MMOE_K_GROUP, [&] { k_plan_from_ustart<<<1, 64, 0, S.st>>>(w.ustart, nu, w.plan, tn, w.tiles); })) return -1;
+    if (launch(MMOE_K_GROUP, [&] { kl(k_plan_from_ustart, 1, 64, 0, w.ustart, nu, w.plan, tn, w.tiles); })) return -1;
     if (stage_quant_x(w, w.hn, nb)) return -1;
     return stage_experts(w, np, nu, tn, false);
 }
@@ -563,7 +574,7 @@ double gpre_dense(int g, const float *x, int nb, float *y) {
     if (hipMemcpyAsync(w.hn, x, (size_t)nb * MH * 4, hipMemcpyHostToDevice, S.st) != hipSuccess) { seterr("gpre_dense: copy x"); return fail(); }
     if (stage_quant_x(w, w.hn, nb)) return fail();
     if (launch(MMOE_K_DENSE, [&] {
-            k_dense<DENSE_W><<<dim3(nrb, (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, ys, w.qx, w.qsx, w.qsumx, DN.y);
+            kl(k_dense<DENSE_W>, dim3(nrb, (nb + 63) / 64), 64 * DENSE_W, 0, DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, ys, w.qx, w.qsx, w.qsumx, DN.y);
         })) return fail();
     (void)hipEventRecord(b, S.st);
     if (hipMemcpyAsync(y, DN.y, (size_t)nb * ys * 4, hipMemcpyDeviceToHost, S.st) != hipSuccess || hipStreamSynchronize(S.st) != hipSuccess) {
@@ -653,26 +664,26 @@ static int gfull_attn_launch(int L, int glob) {
     int nb = S.gfull_nb, pos0 = GF.pos0, ctx = GF.ctx, win = GF.win, g = 2 * L;
     const uint16_t *nwl = GF.nw + (size_t)L * GF_NWL;
     __half *kcl = GF.kc + (size_t)L * ctx * 512, *vcl = GF.vc + (size_t)L * ctx * 512, *kol = GF.ko + (size_t)L * GF.maxtok * 1024;
-    if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(w.x, nwl, w.hn, nb); })) return -1;
+    if (launch(MMOE_K_RMSNORM, [&] { kl(k_rmsnorm, nb, 256, 0, w.x, nwl, w.hn, nb); })) return -1;
     if (stage_quant_x(w, w.hn, nb)) return -1;
     if (launch(MMOE_K_DENSE, [&] {
-        k_dense<DENSE_W><<<dim3(3072 / (64 * DENSE_W), (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, 3072, w.qx, w.qsx, w.qsumx, GF.qkv);
+        kl(k_dense<DENSE_W>, dim3(3072 / (64 * DENSE_W), (nb + 63) / 64), 64 * DENSE_W, 0, DN.dmat + g * 3, DN.drbs + g * 4, DN.n[g], nb, 3072, w.qx, w.qsx, w.qsumx, GF.qkv);
     })) return -1;
     if (launch(MMOE_K_QKN, [&] {
-        k_qkn<<<nb, 256, 0, S.st>>>(GF.qkv, pos0, glob, nwl + 4096, nwl + 4224, GF.cs, kcl, vcl, kol, GF.mx);
+        kl(k_qkn, nb, 256, 0, GF.qkv, pos0, glob, nwl + 4096, nwl + 4224, GF.cs, kcl, vcl, kol, GF.mx);
     })) return -1;
     int span = glob ? pos0 + nb : std::min(pos0 + nb, win + AT_SC_NB);   // positions one token group can see
     if (launch(MMOE_K_ATT_SCORES, [&] {
-        k_att_scores<AT_SC_NB><<<dim3((nb + AT_SC_NB - 1) / AT_SC_NB * 4, (span + 63) / 64), 64, 0, S.st>>>(GF.qkv, nb, pos0, glob, win, kcl, GF.sc, GF.mx, ctx);
+        kl(k_att_scores<AT_SC_NB>, dim3((nb + AT_SC_NB - 1) / AT_SC_NB * 4, (span + 63) / 64), 64, 0, GF.qkv, nb, pos0, glob, win, kcl, GF.sc, GF.mx, ctx);
     })) return -1;
-    if (launch(MMOE_K_ATT_SOFTMAX, [&] { k_att_softmax<<<nb, 256, 0, S.st>>>(pos0, glob, win, GF.sc, GF.mx, GF.inv, ctx); })) return -1;
+    if (launch(MMOE_K_ATT_SOFTMAX, [&] { kl(k_att_softmax, nb, 256, 0, pos0, glob, win, GF.sc, GF.mx, GF.inv, ctx); })) return -1;
     if (launch(MMOE_K_ATT_PV, [&] {   // small chunks: fewer tokens per workgroup, more workgroups
-        if (nb > 256) k_att_pv<4><<<(nb + 3) / 4 * 4, 256, 0, S.st>>>(nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
-        else k_att_pv<2><<<(nb + 1) / 2 * 4, 256, 0, S.st>>>(nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
+        if (nb > 256) kl(k_att_pv<4>, (nb + 3) / 4 * 4, 256, 0, nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
+        else kl(k_att_pv<2>, (nb + 1) / 2 * 4, 256, 0, nb, pos0, glob, win, GF.sc, GF.mx, GF.inv, vcl, GF.att, ctx);
     })) return -1;
     if (stage_quant_x(w, GF.att, nb)) return -1;
     return launch(MMOE_K_DENSE, [&] {
-        k_dense<DENSE_W, true><<<dim3(MH / (64 * DENSE_W), (nb + 63) / 64), 64 * DENSE_W, 0, S.st>>>(DN.dmat + (g + 1) * 3, DN.drbs + (g + 1) * 4, DN.n[g + 1], nb, MH, w.qx, w.qsx, w.qsumx, w.x);
+        kl(k_dense<DENSE_W, true>, dim3(MH / (64 * DENSE_W), (nb + 63) / 64), 64 * DENSE_W, 0, DN.dmat + (g + 1) * 3, DN.drbs + (g + 1) * 4, DN.n[g + 1], nb, MH, w.qx, w.qsx, w.qsumx, w.x);
     });
 }
 // The attention half of layer L and the router: rl gets nb x 256 logits. Synchronous; returns device seconds.
@@ -840,12 +851,12 @@ static int set_router(int L, const uint16_t *router) {
     HC(hipMemcpy(lw.router, router, (size_t)MNE * MH * 2, hipMemcpyHostToDevice));
     if (!lw.rc16) HC(hipMalloc(&lw.rc16, (size_t)MNE * MH * 2));
     if (!lw.rc8) HC(hipMalloc(&lw.rc8, (size_t)MNE * MH * 2));
-    k_router_chainmajor<16><<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rc16);
-    k_router_chainmajor<8><<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rc8);
+    kl(k_router_chainmajor<16>, MNE * MH / 256, 256, 0, lw.router, lw.rc16);
+    kl(k_router_chainmajor<8>, MNE * MH / 256, 256, 0, lw.router, lw.rc8);
     if (!lw.rf8) HC(hipMalloc(&lw.rf8, (size_t)MNE * MH * 4));
-    k_router_chain8_f32<<<MNE * MH / 256, 256, 0, S.st>>>(lw.router, lw.rf8);
+    kl(k_router_chain8_f32, MNE * MH / 256, 256, 0, lw.router, lw.rf8);
     if (!lw.w1max) HC(hipMalloc(&lw.w1max, sizeof(float)));
-    k_router_l1max<<<1, 256, 0, S.st>>>(lw.router, lw.w1max);
+    kl(k_router_l1max, 1, 256, 0, lw.router, lw.w1max);
     HC(hipGetLastError());
     HC(hipStreamSynchronize(S.st));
     return 0;
@@ -886,7 +897,7 @@ int mmoe_moe_dev_noalloc(int L, const float *d_hn, int nb, float *d_x, int order
 
 int mmoe_rmsnorm_dev(const float *d_x, const uint16_t *d_w, int nb, float *d_out) {
     if (ctx_ready()) return -1;
-    return launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(d_x, d_w, d_out, nb); });
+    return launch(MMOE_K_RMSNORM, [&] { kl(k_rmsnorm, nb, 256, 0, d_x, d_w, d_out, nb); });
 }
 
 int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order) {
@@ -903,7 +914,7 @@ int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order) {
             if (rc) return -1;
             continue;
         }
-        if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(d_x, pw, w.hn, nb); })) return -1;
+        if (launch(MMOE_K_RMSNORM, [&] { kl(k_rmsnorm, nb, 256, 0, d_x, pw, w.hn, nb); })) return -1;
         if (moe_dev(w, L, w.hn, nb, d_x, order)) return -1;
     }
     return 0;
@@ -996,7 +1007,7 @@ int mmoe_gfull_post_norm(int L, float *rl) {
     if (!S.gfull || !S.gfull_nb || L < 0 || L >= NLMAX || !S.layers[L].router) { seterr("mmoe_gfull_post_norm: not set up (gfull_begin) / layer %d", L); return -1; }
     Work &w = S.main; int nb = S.gfull_nb;
     const uint16_t *pw = S.layers[L].post_ln;
-    if (launch(MMOE_K_RMSNORM, [&] { k_rmsnorm<<<nb, 256, 0, S.st>>>(w.x, pw, w.hn, nb); })) return -1;
+    if (launch(MMOE_K_RMSNORM, [&] { kl(k_rmsnorm, nb, 256, 0, w.x, pw, w.hn, nb); })) return -1;
     // exact chains whatever the router mode: maple.c takes these logits as they are (its own softmax/top-8)
     if (stage_router(w, L, w.hn, nb, MMOE_ORDER_BATCH, true)) return -1;
     if (rl) { HC(hipMemcpyAsync(rl, w.rl, (size_t)nb * MNE * 4, hipMemcpyDeviceToHost, S.st)); HC(hipStreamSynchronize(S.st)); }
@@ -1059,7 +1070,7 @@ int mmoe_selftest_silu(uint32_t lo, uint32_t n, unsigned long long *nbad, uint32
     HC(hipMalloc(&d, sizeof(R)));
     int rc = -1;
     if (hipMemcpy(d, &h, sizeof h, hipMemcpyHostToDevice) == hipSuccess) {
-        k_selftest_silu<<<S.ncu * 16, 256, 0, S.st>>>(lo, n, &d->bad, &d->first);
+        kl(k_selftest_silu, S.ncu * 16, 256, 0, lo, n, &d->bad, &d->first);
         if (hipGetLastError() == hipSuccess && hipStreamSynchronize(S.st) == hipSuccess &&
             hipMemcpy(&h, d, sizeof h, hipMemcpyDeviceToHost) == hipSuccess) rc = 0;
     }

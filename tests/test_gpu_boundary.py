@@ -69,7 +69,7 @@ def test_setters_drop_the_graph(layer7):
     bias = np.zeros(256, np.float32)
     setters = [("mmoe_set_debug(1)", lambda: lib.mmoe_set_debug(1)), ("mmoe_set_debug(0)", lambda: lib.mmoe_set_debug(0)),
                ("mmoe_set_decode_path", lambda: lib.mmoe_set_decode_path(1)),
-               ("mmoe_set_router_mode", lambda: lib.mmoe_set_router_mode(1)),
+               ("mmoe_set_router_mode", lambda: lib.mmoe_set_router_mode(0)),
                ("mmoe_set_bias", lambda: lib.mmoe_set_bias(7, M.ptr(bias))),
                ("mmoe_set_bias(NULL)", lambda: lib.mmoe_set_bias(7, None)),
                ("mmoe_set_layer", lambda: M.register_layer(7, layer7.blk, layer7.router) and 0)]

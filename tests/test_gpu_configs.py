@@ -8,7 +8,8 @@
   a local (windowed) and a global layer, attention half and MoE block (Zipf(1.1)-biased router, as the bench).
   The oracle's attention for one token needs the cache of every earlier position: it gets the card's cache, whose
   rows are checked bit for bit on the sampled positions, then runs maple.c's chunk code for each sampled token.
-  The second chunk runs with the MFMA router option, under which gfull_attn must still return exact logits."""
+  The first chunk runs with the exact router option, the second with the default MFMA router, under which
+  gfull_attn must still return exact logits."""
 import ctypes as C
 
 import numpy as np
@@ -134,7 +135,7 @@ def config4(stack24):
     yield lib, att, blocks, post, zb, cs
     for L, _ in C4_LAYERS:
         lib.mmoe_set_bias(L, None)
-    lib.mmoe_set_router_mode(1)
+    lib.mmoe_set_router_mode(0)
 
 
 def test_config4_full_size_sampled(config4):

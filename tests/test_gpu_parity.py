@@ -108,8 +108,13 @@ def test_silu_exhaustive():
 
 
 def test_moe_batch_gemm_router(layer0):
-    # >= 512 tokens: the exact tiled fp32 router (k_router_gemm); 520 leaves a ragged last token tile
-    compare_layer(layer0, 520, M.ORDER_BATCH)
+    # >= 512 tokens with the exact router option: the tiled fp32 chains (k_router_gemm); 520 leaves a ragged
+    # last token tile
+    M.check(M.lib().mmoe_set_router_mode(1), "router mode")
+    try:
+        compare_layer(layer0, 520, M.ORDER_BATCH)
+    finally:
+        M.check(M.lib().mmoe_set_router_mode(0), "router mode")
 
 
 def test_moe_batch_tn64(layer0):
@@ -260,14 +265,14 @@ def test_stack_graph_replays_match_eager(layer0):
 
 
 def test_moe_batch_mfma_router(layer0):
-    """Batches of >= 128 tokens with the bf16-MFMA router and exact refinement of each token's candidates."""
+    """Batches of >= 512 tokens with the bf16-MFMA router (inputs split into three exact bf16 parts) and exact
+    chain logits for each token's candidates (k_refine_topk): top-8 and their logits bit-exact, the rest close."""
     lib = M.lib()
     M.check(lib.mmoe_set_router_mode(0), "router mode")
     try:
-        compare_layer(layer0, 256, M.ORDER_BATCH, " mfma router", refined=True)
-        compare_layer(layer0, 200, M.ORDER_BATCH, " mfma router", refined=True)
+        compare_layer(layer0, 520, M.ORDER_BATCH, " mfma router", refined=True)
     finally:
-        M.check(lib.mmoe_set_router_mode(1), "router mode")
+        M.check(lib.mmoe_set_router_mode(0), "router mode")
 
 
 def test_moe_batch_tn64_compact_sums(layer0):
@@ -309,10 +314,13 @@ def test_full_size_tokens_independent(zipf_layer, T):
     """BASELINE config 2 at full size (2048 Zipf-routed tokens, checks off: the int16 / fused-activation path).
     Each token's MoE output depends on that token only, and the batch combine sums a token's pairs in ascending
     expert order whatever the batch, so the full batch must reproduce, bit for bit, the rows of sub-batches run
-    alone (two halves, and a scattered 48-token sample); the sample is also checked against the oracle."""
+    alone (two halves, and a scattered 48-token sample); the sample is also checked against the oracle. Runs
+    with the exact router option, so that the 48-token sample (chain router) and the full batch share every
+    logit; test_zipf_mfma_router_matches_exact covers the default MFMA router at this size."""
     lib = M.lib()
     L = zipf_layer.L
     M.check(lib.mmoe_set_debug(0), "debug off")
+    M.check(lib.mmoe_set_router_mode(1), "router mode")
     try:
         x, hn = normed_hidden(SEED, 500 + T, T)
         xf = run_gpu(L, hn, x, M.ORDER_BATCH)
@@ -330,6 +338,7 @@ def test_full_size_tokens_independent(zipf_layer, T):
         assert relmax(xf[idx] - xsmp, xo - xsmp) <= TOL
         print(f"\n  T={T}: halves and sample bit-exact; sample vs oracle bit-exact {np.array_equal(xf[idx], xo)}")
     finally:
+        M.check(lib.mmoe_set_router_mode(0), "router mode")
         M.check(lib.mmoe_set_debug(1), "debug on")
 
 
@@ -417,3 +426,33 @@ def test_flip_token_matches_oracle(layer0):
         assert int((qa != f["avx2_qa"]).sum()) == 1 and np.array_equal(qa, f["native_qa"])
         assert relmax(xg, f["native_xout"]) <= TOL
     M.lib().mmoe_set_decode_path(1)
+
+
+def test_zipf_mfma_router_matches_exact(zipf_layer):
+    """Config 2 (2048 Zipf-routed tokens) with the MFMA router against the exact chain router: identical top-8,
+    the picked experts' logits bit for bit, tw and x within the bar; and, with the MFMA router too, each token's
+    result independent of the rest of the batch (halves bit-exact)."""
+    lib = M.lib()
+    L, T = zipf_layer.L, 2048
+    M.check(lib.mmoe_set_debug(0), "debug off")
+    x, hn = normed_hidden(SEED, 4100, T)
+    try:
+        out = {}
+        for mode in (1, 0):
+            M.check(lib.mmoe_set_router_mode(mode), "router mode")
+            xg = run_gpu(L, hn, x, M.ORDER_BATCH)
+            out[mode] = (xg, M.read("TOP", (T, 8), np.int32), M.read("TW", (T, 8), np.float32), M.read("LOGITS", (T, 256), np.float32))
+        (x1, t1, w1, r1), (x0, t0, w0, r0) = out[1], out[0]
+        assert np.array_equal(t0, t1), f"top-8 differs on {int((t0 != t1).any(1).sum())} tokens"
+        sel = np.take_along_axis(r0, t0, 1).view(np.int32), np.take_along_axis(r1, t1, 1).view(np.int32)
+        assert np.array_equal(*sel), "the picked experts' logits differ"
+        print(f"\n  mfma vs exact router: tw relmax {relmax(w0, w1):.1e}, x relmax {relmax(x0 - x, x1 - x):.1e}, "
+              f"other logits relmax {relmax(r0, r1):.1e}")
+        assert relmax(w0, w1) <= TOL and relmax(x0 - x, x1 - x) <= TOL
+        h = T // 2
+        for lo, hi in ((0, h), (h, T)):
+            xs = run_gpu(L, np.ascontiguousarray(hn[lo:hi]), np.ascontiguousarray(x[lo:hi]), M.ORDER_BATCH)
+            assert np.array_equal(xs, x0[lo:hi]), f"rows {lo}..{hi} differ from the full batch"
+    finally:
+        M.check(lib.mmoe_set_router_mode(0), "router mode")
+        M.check(lib.mmoe_set_debug(1), "debug on")
