@@ -18,7 +18,7 @@
 #include <stdint.h>
 
 #define MMOE_MAXTOK 2048      /* largest chunk (maple.c:413 BMAX) */
-#define MMOE_MAXREG 64        /* regions (gpu_pre.m:21 MAXREG) */
+#define MMOE_MAXREG 256       /* regions (gpu_pre.m:21 MAXREG is 64: a model whose layers span 3 shards needs 72) */
 #define MMOE_GPUX_MAXTOK 64   /* vectors per gpux call (maple.c:322 MAXSEQ) */
 #define MMOE_NOALLOC_MAXTOK 64   /* tokens per mmoe_moe_dev_noalloc call (its fixed scratch) */
 

@@ -76,3 +76,71 @@ def write_checkpoint(d, seed, nexp=6, gu_shards=2):
         for r in recs:
             f.write(REC.pack(*r))
     return dict(experts=experts, routers=routers, post_ln=post_ln, recs=recs)
+
+
+VOCAB, NKV, HD = 151936, 4, 128
+
+
+def pack_codes(c):
+    """codes[rows][cols] in {0,1,2} -> the packed layout of convert.py:29-33 (128-column groups of 32 bytes, byte j
+    holding columns j, j+32, j+64, j+96 at bits 0,2,4,6)"""
+    r, n = c.shape
+    g = c.reshape(r, n // 128, 4, 32).astype(np.uint8)
+    return (g[:, :, 0] | (g[:, :, 1] << 2) | (g[:, :, 2] << 4) | (g[:, :, 3] << 6)).reshape(r, n // 4)
+
+
+def write_model_checkpoint(d, seed, nexp=16, vocab_rows=4096):
+    """A whole-model directory in maple.c's format (every record at its real shape) that maple.c itself can run:
+    embeddings and lm_head share one record of VOCAB x 2048 bf16 whose first `vocab_rows` rows are random and the
+    rest a sparse (unwritten, zero) tail of the shard; 2 variants of norms, router and attention projections,
+    alternating over the layers; `nexp` distinct experts (expert e of layer L is distinct (7 e + L) % nexp).
+    Returns the number of vocabulary rows with data (prompt ids must lie below it)."""
+    os.makedirs(d, exist_ok=True)
+    rng = np.random.default_rng(seed)
+    sh = [Shard() for _ in range(9)]
+    bf = lambda a: (np.asarray(a, np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    eoff = []
+    for k in range(nexp):
+        gc = np.empty((M.FF, M.H // 4), np.uint8); gs = np.empty(M.FF, np.float32)
+        uc = np.empty((M.FF, M.H // 4), np.uint8); us = np.empty(M.FF, np.float32)
+        dc = np.empty((M.H, M.FF // 4), np.uint8); ds = np.empty(M.H, np.float32)
+        M.lib().mmoe_synth_expert(seed, 0, k, M.ptr(gc), M.ptr(gs), M.ptr(uc), M.ptr(us), M.ptr(dc), M.ptr(ds))
+        g = sh[k % 2]
+        o = (k % 2, g.put(gc), g.put(gs), g.put(uc), g.put(us), sh[2].put(dc), sh[2].put(ds))
+        eoff.append(o)
+    r_off = [sh[3].put(M.synth_router(seed, L, 0)) for L in range(2)]
+    norm = lambda n: bf(rng.uniform(0.7, 1.3, n))
+    var = []
+    for v in range(2):
+        t = {}
+        for name, rows in (("q", NE // 16 * 128), ("k", NKV * HD), ("v", NKV * HD), ("o", M.H)):
+            c = rng.choice(np.array([0, 1, 2], np.uint8), size=(rows, M.H), p=[0.3, 0.4, 0.3])
+            t[name] = (sh[4].put(pack_codes(c)), sh[4].put(rng.uniform(0.01, 0.05, rows).astype(np.float32)), rows)
+        t["in"] = sh[4].put(norm(M.H)); t["post"] = sh[4].put(norm(M.H))
+        t["qn"] = sh[4].put(norm(HD)); t["kn"] = sh[4].put(norm(HD))
+        var.append(t)
+    o_norm = sh[4].put(np.full(M.H, 0x3F80, np.uint16))
+    emb = sh[5].put(bf(rng.standard_normal((vocab_rows, M.H)) * 0.05))
+    recs = [(ord("b"), 5, emb, 0, VOCAB, M.H), (ord("b"), 5, emb, 0, VOCAB, M.H), (ord("b"), 4, o_norm, 0, 1, M.H)]
+    for L in range(NL):
+        t = var[L % 2]
+        recs += [(ord("b"), 4, t["in"], 0, 1, M.H), (ord("b"), 4, t["post"], 0, 1, M.H),
+                 (ord("b"), 4, t["qn"], 0, 1, HD), (ord("b"), 4, t["kn"], 0, 1, HD),
+                 (ord("b"), 3, r_off[L % 2], 0, NE, M.H)]
+        for name in "qkvo":
+            off, soff, rows = t[name]
+            recs.append((ord("t"), 4, off, soff, rows, M.H))
+        for e in range(NE):
+            o = eoff[distinct(L, e, nexp)]
+            recs.append((ord("t"), o[0], o[1], o[2], M.FF, M.H))
+            recs.append((ord("t"), o[0], o[3], o[4], M.FF, M.H))
+            recs.append((ord("t"), 2, o[5], o[6], M.H, M.FF))
+    for k, s_ in enumerate(sh):
+        with open(os.path.join(d, f"shard-{k + 1:05d}.bin"), "wb") as f:
+            f.write(bytes(s_.buf) if k < 6 else b"\0" * 16)
+            if k == 5:
+                f.truncate(emb + VOCAB * M.H * 2)              # the zero tail of the vocabulary, not written
+    with open(os.path.join(d, "layout.bin"), "wb") as f:
+        for r in recs:
+            f.write(REC.pack(*r))
+    return vocab_rows

@@ -17,13 +17,14 @@
 #include "maplemoe.h"
 #include "moe_oracle.h"
 
-static const uint8_t *REG_P[MMOE_MAXREG];
-static size_t REG_N[MMOE_MAXREG];
+#define STUB_MAXREG 64   /* the stand-in's own region table (gpu_pre.m:21's size) */
+static const uint8_t *REG_P[STUB_MAXREG];
+static size_t REG_N[STUB_MAXREG];
 static int NREG;
 static volatile unsigned SINK;
 
 int gpre_region(const void *p, size_t len) {
-    if (NREG >= MMOE_MAXREG) return -1;
+    if (NREG >= STUB_MAXREG) return -1;
     const uint8_t *b = (const uint8_t *)p;
     unsigned s = 0;
     for (size_t i = 0; i < len; i++) s += b[i];
