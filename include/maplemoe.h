@@ -137,7 +137,7 @@ int mmoe_stack_dev(int L0, int nl, float *d_x, int nb, int order);
 /* The same captured once into a HIP graph, then replayed `replays` times; mmoe_graph_reset drops it. A call
  * with other arguments captures anew. The graph holds the kernels and device buffers it was captured with, so
  * every setter that changes them (mmoe_set_layer, mmoe_set_bias, mmoe_set_debug, mmoe_set_decode_path,
- * mmoe_set_router_mode, gfull_init) drops it first. Profiling must be off. mmoe_graph_held: 1 while a
+ * mmoe_set_expert_path, mmoe_set_router_mode, gfull_init) drops it first. Profiling must be off. mmoe_graph_held: 1 while a
  * captured graph is kept, else 0. */
 int mmoe_stack_graph(int L0, int nl, float *d_x, int nb, int order, int replays);
 int mmoe_graph_reset(void);
@@ -178,6 +178,10 @@ int mmoe_read(int what, void *dst, size_t bytes);
 int mmoe_set_debug(int on);
 /* Batches of <= 8 tokens use three fused decode kernels (default on); off = the grouped-GEMM path. */
 int mmoe_set_decode_path(int on);
+/* Batches whose pairs are tiled by 16 (fewer than 2048 pairs, above the decode path): 1 (default) = one fused
+ * kernel per tile (gate/up, SiLU*up, act quantisation and down; the act never leaves the chip), 0 = the three
+ * separate kernels. Both give identical results. */
+int mmoe_set_expert_path(int fused);
 /* Router of batches of >= 512 tokens in batch order: 0 (default) = bf16 MFMA logits on the input split into
  * three exact bf16 parts, with every expert that a rounding bound cannot exclude from a token's top 8 recomputed
  * in maple.c's exact chain order (top-8 indices and their logits stay maple.c's; the other logits, and through

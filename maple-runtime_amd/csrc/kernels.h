@@ -1484,6 +1484,191 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
     }
 }
 
+// Whole expert per workgroup for small batches (tiles of <= 16 pairs): gate/up with SiLU*up, the int8
+// quantisation of act and down in one launch (maple.c:471-479, 498-505, 825-832). With a few pairs per expert
+// these layers stream the expert's 798,720 bytes of codes and scales and do little arithmetic, so one
+// workgroup per tile streams the whole expert through a register ring, as fast as a plain copy of the same
+// blocks; act never leaves LDS. Block = 8 waves; wave w takes gate and up rows 64w .. +64 (8 fragments of 16 rows
+// on v_mfma_i32_16x16x64_i8, operand mapping of k_gateup), then down rows 256w .. +256 in two passes of 128.
+// The code loads form 12 groups of 8 16-byte loads per lane, each group whole rows (16 rows x 512 bytes of a
+// gate and an up fragment, or 4 down fragments x 128 bytes: 8 KB contiguous per wave; reading 64 bytes of
+// many rows per group instead streamed 20% slower). The ring holds 4 groups, so the down codes are in flight
+// while gate/up finishes. LDS: the tile's int8 input (16 rows of 2048 bytes, 16-byte parts swizzled as in
+// k_gateup), reused for fp32 act; act in int8 (rows of DN_QW bytes); the tile's scales. Outputs: down[pair] as
+// k_down, the quantised act as k_quant_act; with gu_d / dn_d (checks on) also the int32 sums and fp32 act.
+#define E16_QW 528   // LDS bytes per quantised act row (512 + 16: rows 16 apart fall in different banks)
+template <int WAVES, int RING>
+__global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
+                                                         const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
+                                                         const int8_t *__restrict__ qx, const float *__restrict__ qsx,
+                                                         const int *__restrict__ qsumx, float *__restrict__ down,
+                                                         float *__restrict__ act_d, int8_t *__restrict__ qa_d,
+                                                         float *__restrict__ qsa_d, int *__restrict__ qsuma_d,
+                                                         int *__restrict__ gu_d, int *__restrict__ dn_d) {
+    constexpr int NT = WAVES * 64;
+    constexpr int GF = MFF / 16 / WAVES;       // gate (and up) fragments of 16 rows per wave
+    constexpr int DF = MH / 16 / WAVES;        // down fragments per wave, in passes of 8
+    constexpr int NGU = 2 * GF, NG = NGU + DF / 4, NFR = 8;
+    __shared__ __attribute__((aligned(16))) int8_t xs[16 * MH];     // input rows; later fp32 act [16][512]
+    __shared__ __attribute__((aligned(16))) int8_t qs8[16 * E16_QW];
+    __shared__ __attribute__((aligned(16))) float sg[MFF], su[MFF], sd[MH];
+    __shared__ float tqs[16], aqs[16];
+    __shared__ int tqsum[16], aqsum[16], toks[16];
+    int item = xcd_item(blockIdx.x, plan->ntile_gu);
+    if (item < 0) return;
+    Tile tl = tiles[item];
+    int p0 = tl.p0, ntok = tl.n;
+    ExpPtr ex = eptr[tl.u];
+    int tid = threadIdx.x, l = tid & 63, G = l >> 4, r16 = l & 15;
+    int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // lane offset of its 16 code bytes: row r16 of a fragment, 16-byte part of a 64-byte chunk (as k_gateup)
+    int aoff = (G >> 1) * 32 + (G & 1) * 16;
+    uint32_t gl = (uint32_t)r16 * (MH / 4) + aoff, dl = (uint32_t)r16 * (MFF / 4) + aoff;
+    const uint8_t *gb = ex.gc + (size_t)wv * GF * 16 * (MH / 4), *ub = ex.uc + (size_t)wv * GF * 16 * (MH / 4);
+    const uint8_t *db = ex.dc + (size_t)wv * DF * 16 * (MFF / 4);
+    v4i cw[RING][NFR];
+    // Each group reads whole rows (8 KB contiguous per wave): gate/up group g = gate and up fragment g / 2, the
+    // 4 chunks (g & 1) * 4 .. +3 (load k: up if k >= 4, chunk k & 3); down group NGU + 2 ps + q = fragments
+    // 4q .. 4q+3 of pass ps (8 fragments), both chunks (load k: fragment 4q + k / 2, chunk k & 1)
+    auto load_group = [&](int g, v4i (&dst)[NFR]) {
+        if (g < NGU) {
+            int fp = g >> 1, hh = g & 1;
+#pragma unroll
+            for (int k = 0; k < NFR; k++)
+                dst[k] = *(const gptr_u4 *)((k < 4 ? gb : ub) + fp * 16 * (MH / 4) + gl + (hh * 4 + (k & 3)) * 64);
+        } else {
+            int ps = (g - NGU) >> 1, q = (g - NGU) & 1;
+#pragma unroll
+            for (int k = 0; k < NFR; k++)
+                dst[k] = *(const gptr_u4 *)(db + (ps * 128 + (4 * q + (k >> 1)) * 16) * (MFF / 4) + dl + (k & 1) * 64);
+        }
+    };
+#pragma unroll
+    for (int g = 0; g < RING - 1; g++) load_group(g, cw[g]);
+    // stage the tile: input rows (zeros for padding tokens), its quantisation scales, the expert's row scales
+    if (tid < 16) {
+        int tk = tid < ntok ? utok[p0 + tid] : -1;
+        toks[tid] = tk;
+        tqs[tid] = tk >= 0 ? qsx[tk] : 0.0f;
+        tqsum[tid] = tk >= 0 ? qsumx[tk] : 0;
+    }
+    for (int i = tid; i < MFF; i += NT) { sg[i] = ex.gs[i]; su[i] = ex.us[i]; }
+    for (int i = tid; i < MH / 4; i += NT) *(float4 *)(sd + i * 4) = *(const float4 *)(ex.ds + i * 4);
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16 * 128 / NT; k++) {
+        int i = tid + NT * k, tk = i >> 7, part = i & 127;      // 128 parts of 16 bytes per row
+        int src = toks[tk];
+        v4i v = src >= 0 ? *(const gptr_u4 *)(qx + (size_t)src * MH + part * 16) : v4i{0, 0, 0, 0};
+        *(v4i *)(xs + tk * MH + (part >> 4) * 256 + (((part & 15) ^ tk) * 16)) = v;
+    }
+    __syncthreads();
+
+    v4i acc[NFR];
+#pragma unroll
+    for (int f = 0; f < NFR; f++) acc[f] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        if (g + RING - 1 < NG) load_group(g + RING - 1, cw[(g + RING - 1) % RING]);
+        const v4i(&c)[NFR] = cw[g % RING];
+        if (g < NGU) {
+            int fp = g >> 1, hh = g & 1;
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    int part = (G >> 1) * 8 + (G & 1) * 4 + t;
+                    v4i bv = *(const v4i *)(xs + r16 * MH + (hh * 4 + cc) * 256 + ((part ^ r16) * 16));
+                    uint32_t wg = (uint32_t)(t == 0 ? c[cc].x : t == 1 ? c[cc].y : t == 2 ? c[cc].z : c[cc].w);
+                    uint32_t wu = (uint32_t)(t == 0 ? c[4 + cc].x : t == 1 ? c[4 + cc].y : t == 2 ? c[4 + cc].z : c[4 + cc].w);
+                    acc[fp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(decode_word(wg), bv, acc[fp], 0, 0, 0);
+                    acc[GF + fp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(decode_word(wu), bv, acc[GF + fp], 0, 0, 0);
+                }
+        } else {
+            int q = (g - NGU) & 1;
+#pragma unroll
+            for (int h = 0; h < 2; h++)
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    v4i bv = *(const v4i *)(qs8 + r16 * E16_QW + h * 256 + (G >> 1) * 128 + (G & 1) * 64 + t * 16);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) {
+                        const v4i cj = c[2 * j + h];
+                        uint32_t w = (uint32_t)(t == 0 ? cj.x : t == 1 ? cj.y : t == 2 ? cj.z : cj.w);
+                        acc[4 * q + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(decode_word(w), bv, acc[4 * q + j], 0, 0, 0);
+                    }
+                }
+        }
+        if (g == NGU - 1) {
+            // gate/up epilogue: lane (G, n) holds rows wv*GF*16 + 16f + 4G + i of token n; act into LDS (fp32 over xs)
+            __syncthreads();   // every wave is done reading xs
+            float *act = (float *)xs;
+            float qs = tqs[r16]; int qsum = tqsum[r16];
+#pragma unroll
+            for (int f = 0; f < GF; f++) {
+                int row0 = wv * GF * 16 + f * 16 + 4 * G;
+                float o[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    float gv = (float)(acc[f][i] - qsum) * qs * sg[row0 + i];
+                    float uv = (float)(acc[GF + f][i] - qsum) * qs * su[row0 + i];
+                    float gg = gv < 7.0f ? gv : 7.0f;
+                    o[i] = silu_le7(gg) * __builtin_amdgcn_fmed3f(uv, -7.0f, 7.0f);
+                }
+                *(float4 *)(act + r16 * MFF + row0) = make_float4(o[0], o[1], o[2], o[3]);
+                if (gu_d && r16 < ntok) {
+                    int *gp = gu_d + (size_t)(p0 + r16) * 2 * MFF;
+                    *(int4 *)(gp + row0) = make_int4(acc[f][0], acc[f][1], acc[f][2], acc[f][3]);
+                    *(int4 *)(gp + MFF + row0) = make_int4(acc[GF + f][0], acc[GF + f][1], acc[GF + f][2], acc[GF + f][3]);
+                    *(float4 *)(act_d + (size_t)(p0 + r16) * MFF + row0) = make_float4(o[0], o[1], o[2], o[3]);
+                }
+            }
+            __syncthreads();
+            // quantisation of act (maple.c prep on the 512-vector): half hh of wave w -> token 2w + hh
+            if (wv < 8) {
+                int tk = 2 * wv + (l >> 5), o = l & 31, gq = o >> 3, hq = (o >> 2) & 1, tq = o & 3;
+                const float *ar = act + tk * MFF;
+                float v[16];
+#pragma unroll
+                for (int s = 0; s < 4; s++) {
+                    float4 fv = *(const float4 *)(ar + gq * 128 + s * 32 + hq * 16 + tq * 4);
+                    v[s * 4] = fv.x; v[s * 4 + 1] = fv.y; v[s * 4 + 2] = fv.z; v[s * 4 + 3] = fv.w;
+                }
+                quant_half<128>(v, l, qs8 + tk * E16_QW, aqs + tk, aqsum + tk);
+            }
+            __syncthreads();
+            if (tid < 512) {   // the quantised act as k_quant_act writes it (read by callers that check it)
+                int tk = tid >> 5, part = tid & 31;
+                if (tk < ntok) {
+                    *(v4i *)(qa_d + (size_t)(p0 + tk) * MFF + part * 16) = *(const v4i *)(qs8 + tk * E16_QW + part * 16);
+                    if (part == 0) { qsa_d[p0 + tk] = aqs[tk]; qsuma_d[p0 + tk] = aqsum[tk]; }
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < NFR; f++) acc[f] = v4i{0, 0, 0, 0};
+        }
+        if (g >= NGU && ((g - NGU) & 1)) {
+            // down epilogue of pass ps: rows wv*DF*16 + 128ps + 16f + 4G + i of pair p0 + n
+            int ps = (g - NGU) >> 1;
+            if (r16 < ntok) {
+                float qs = aqs[r16]; int qsum = aqsum[r16];
+                float *dp = down + (size_t)(p0 + r16) * MH;
+#pragma unroll
+                for (int f = 0; f < NFR; f++) {
+                    int row0 = wv * DF * 16 + ps * 128 + f * 16 + 4 * G;
+                    float o[4];
+#pragma unroll
+                    for (int i = 0; i < 4; i++) o[i] = (float)(acc[f][i] - qsum) * qs * sd[row0 + i];
+                    *(float4 *)(dp + row0) = make_float4(o[0], o[1], o[2], o[3]);
+                    if (dn_d) *(int4 *)(dn_d + (size_t)(p0 + r16) * MH + row0) = make_int4(acc[f][0], acc[f][1], acc[f][2], acc[f][3]);
+                }
+            }
+#pragma unroll
+            for (int f = 0; f < NFR; f++) acc[f] = v4i{0, 0, 0, 0};
+        }
+    }
+}
+
 // Down per tile (operand mapping as k_gateup_pk, K = 512): one workgroup takes a tile of up to 64 pairs of one expert
 // and RPB row blocks of 256 down rows. The tile's activations (64 x 512 int8) are staged in LDS once (rows
 // padded to DN_LROW bytes); the row blocks then run back to back, the codes of the next row block loaded

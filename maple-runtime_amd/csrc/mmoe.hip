@@ -30,6 +30,8 @@
 #define DN16_RF 2
 #endif
 #ifndef DN_RPB
+#define E16_W 16   // fused small-tile expert kernel: waves per workgroup, code groups in the register ring
+#define E16_RING 3
 #define DN_RPB 2   // down row blocks of 256 per workgroup
 #endif
 
@@ -218,6 +220,7 @@ static int launch(int kid, F &&f) {
 // Pipeline stages
 // ------------------------------------------------------------------------------------------------------
 static int tile_tn(int np) { return np >= 2048 ? 64 : 16; }
+static bool S_expert16 = true;   // tiles of 16: the fused whole-expert kernel (else three kernels)
 
 // Router logits of nb tokens (d_hn) with layer L's router; order 0 = batch (maple.c:853-889), 1 = step (bf_row)
 static bool S_router_exact = false;   // batches of 512+: MFMA logits + exact refinement (else the exact chain GEMM)
@@ -284,6 +287,11 @@ static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
     return launch(MMOE_K_DOWN, [&] { kl(k_down<16, DN16_W, DN16_RF>, grid8(maxtiles * (MH / (16 * DN16_W * DN16_RF))), 64 * DN16_W, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
 }
 
+// tiles of 16 with the fused path: one workgroup per tile does gate/up, the act quantisation and down
+static int launch_expert16(Work &w, int maxtiles, int *dg, int *dd) {
+    return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx,
+                                          w.down, dg ? w.act : nullptr, w.qa, w.qsa, w.qsuma, dg, dd); });
+}
 static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
     if (tn == 64) {
         // checks on: activation from the int32 sums in the debug buffer; else gate/up wrote it already
@@ -300,6 +308,7 @@ static int stage_experts(Work &w, int np, int nu_max, int tn, bool device_groupi
     int *dg = S.debug ? w.dbg_gu : nullptr, *dd = S.debug ? w.dbg_dn : nullptr;
     w.compact = device_grouping && tn == 64 && !S.debug;
     LAST.compact = w.compact;
+    if (tn == 16 && S_expert16) return launch_expert16(w, maxtiles, dg, dd);
     if (launch_gateup(w, maxtiles, tn, dg)) return -1;
     if (launch_quant_act(w, maxtiles, tn, np, dg)) return -1;
     if (launch_down(w, maxtiles, tn, dd, w.compact)) return -1;
@@ -816,6 +825,7 @@ int mmoe_init(int maxtok) {
 // before the change, so the next mmoe_stack_graph captures again and no replay touches freed memory.
 int mmoe_set_router_mode(int exact) { if (mmoe_graph_reset()) return -1; S_router_exact = exact != 0; return 0; }
 int mmoe_set_decode_path(int on) { if (mmoe_graph_reset()) return -1; S_dec_enabled = on != 0; return 0; }
+int mmoe_set_expert_path(int fused) { if (mmoe_graph_reset()) return -1; S_expert16 = fused != 0; return 0; }
 
 int mmoe_set_debug(int on) {
     if (mmoe_graph_reset()) return -1;
@@ -1044,6 +1054,11 @@ double mmoe_bench_stage(int kid, int reps) {
             else if (kid == MMOE_K_DOWN) rc = launch_dec_down(w, LAST.nb, LAST.x, LAST.order);
             else { seterr("mmoe_bench_stage: kernel %d not repeatable on the decode path", kid); return -1.0; }
             if (rc) return -1.0;
+            continue;
+        }
+        if (LAST.tn == 16 && S_expert16 && kid != MMOE_K_ROUTER) {
+            if (kid != MMOE_K_GATEUP) { seterr("mmoe_bench_stage: the fused expert path has one kernel (MMOE_K_GATEUP)"); return -1.0; }
+            if (launch_expert16(w, maxtiles, nullptr, nullptr)) return -1.0;
             continue;
         }
         switch (kid) {

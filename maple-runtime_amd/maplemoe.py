@@ -59,7 +59,7 @@ def _declare(L):
         "mmoe_rmsnorm_dev": (i, [vp, vp, i, vp]), "mmoe_stack_dev": (i, [i, i, vp, i, i]),
         "mmoe_stack_graph": (i, [i, i, vp, i, i, i]), "mmoe_graph_reset": (i, []), "mmoe_graph_held": (i, []),
         "mmoe_gfull_setup": (i, [i]), "mmoe_gfull_post_norm": (i, [i, vp]), "mmoe_gfull_stack": (i, [i, i]),
-        "mmoe_read": (i, [i, vp, sz]), "mmoe_set_debug": (i, [i]), "mmoe_set_decode_path": (i, [i]), "mmoe_set_router_mode": (i, [i]), "mmoe_last_error": (C.c_char_p, []),
+        "mmoe_read": (i, [i, vp, sz]), "mmoe_set_debug": (i, [i]), "mmoe_set_decode_path": (i, [i]), "mmoe_set_expert_path": (i, [i]), "mmoe_set_router_mode": (i, [i]), "mmoe_last_error": (C.c_char_p, []),
         "mmoe_dev_alloc": (vp, [sz]), "mmoe_dev_free": (i, [vp]), "mmoe_h2d": (i, [vp, vp, sz]),
         "mmoe_d2h": (i, [vp, vp, sz]), "mmoe_d2d": (i, [vp, vp, sz]), "mmoe_sync": (i, []), "mmoe_stream": (vp, []),
         "mmoe_event_record": (i, [i]), "mmoe_bench_stage": (d, [i, i]), "mmoe_event_elapsed_ms": (d, []), "mmoe_prof": (i, [i]),

@@ -456,3 +456,32 @@ def test_zipf_mfma_router_matches_exact(zipf_layer):
     finally:
         M.check(lib.mmoe_set_router_mode(0), "router mode")
         M.check(lib.mmoe_set_debug(1), "debug on")
+
+
+@pytest.mark.parametrize("nb", [9, 100, 255])
+def test_expert16_fused_matches_three_kernels(zipf_layer, nb):
+    """Tiles of 16 pairs: the fused whole-expert kernel (gate/up, act quantisation and down in one launch) against
+    the three separate kernels, bit for bit in every intermediate (int32 sums, act, its int8 quantisation, down)
+    and in x. The Zipf bias gives experts of many tiles (the hot expert gets most tokens) next to single-pair
+    tiles, so ragged tiles, padding rows and several workgroups per expert all occur."""
+    lib = M.lib()
+    L = zipf_layer.L
+    x, hn = normed_hidden(SEED, 4200 + nb, nb)
+    P = nb * 8
+    out = {}
+    M.check(lib.mmoe_set_debug(1), "debug on")
+    try:
+        for fused in (0, 1):
+            M.check(lib.mmoe_set_expert_path(fused), "expert path")
+            xg = run_gpu(L, hn, x, M.ORDER_BATCH)
+            out[fused] = [xg] + [M.read(n, (P, k), t) for n, k, t in (("GU_I32", 1024, np.int32), ("ACT", 512, np.float32),
+                                                                     ("QA", 512, np.int8), ("QSA", 1, np.float32),
+                                                                     ("QSUMA", 1, np.int32), ("DN_I32", 2048, np.int32),
+                                                                     ("DOWN", 2048, np.float32))]
+        cnt = np.diff(M.read_plan()["ustart"])
+        print(f"\n  nb={nb}: {len(cnt)} experts, largest {cnt.max()} pairs ({int(((cnt + 15) // 16).sum())} tiles)")
+        assert nb <= 16 or cnt.max() > 16
+        for name, a, b in zip(("x", "GU_I32", "ACT", "QA", "QSA", "QSUMA", "DN_I32", "DOWN"), out[0], out[1]):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name} differs"
+    finally:
+        M.check(lib.mmoe_set_expert_path(1), "expert path")
