@@ -1677,12 +1677,18 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
 // Output: D16 = false, D = (float)(sum - qsum) * qs * s_down[row] (fp32); D16 = true, d = sum - qsum as int16
 // (-32768 with d in dov, int32, same index), turned into D by k_combine16 with the same operations; the int16
 // results pass through a per-wave LDS tile so that each store writes 128 contiguous bytes of 8 pairs.
+// QIN: the tile's act arrives in fp32 (act) and is quantised here (maple.c:832 prep, quant_half) into the LDS
+// stage; the first workgroup of each tile also writes the int8 act, qs and qsum out (qa_w, qsa_w, qsuma_w) as
+// k_quant_act would. This saves the separate quantisation launch at the cost of quantising each tile once per
+// workgroup of the tile (MH / 256 / RPB of them).
 #define DN_LROW (MFF + 16)
-template <int RPB, bool D16>
+template <int RPB, bool D16, bool QIN = false>
 __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                       const ExpPtr *__restrict__ eptr, const int8_t *__restrict__ qa,
                                                       const float *__restrict__ qsa, const int *__restrict__ qsuma,
-                                                      float *__restrict__ down, int *__restrict__ dov, int *__restrict__ dbg) {
+                                                      float *__restrict__ down, int *__restrict__ dov, int *__restrict__ dbg,
+                                                      const float *__restrict__ act = nullptr, int8_t *__restrict__ qa_w = nullptr,
+                                                      float *__restrict__ qsa_w = nullptr, int *__restrict__ qsuma_w = nullptr) {
     constexpr int TN = 64, NT = 256, NF = 2, NA = 2, NSPLIT = MH / 256 / RPB;
     constexpr int NPC = TN * (MFF / 16) / NT;   // 8 pieces of 16 bytes per thread
     __shared__ __attribute__((aligned(16))) int8_t bs[TN * DN_LROW];
@@ -1710,16 +1716,55 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
     }
     DN_LOADC(0, rb0);
     float qs[NF]; int qsm[NF];
+    __shared__ float sqs[QIN ? TN : 1];
+    __shared__ int sqsum[QIN ? TN : 1];
+    if (!QIN) {
 #pragma unroll
-    for (int j = 0; j < NF; j++) { int pr = p0 + min(j * 32 + r32, ntok - 1); qs[j] = qsa[pr]; qsm[j] = qsuma[pr]; }
+        for (int j = 0; j < NF; j++) { int pr = p0 + min(j * 32 + r32, ntok - 1); qs[j] = qsa[pr]; qsm[j] = qsuma[pr]; }
 #pragma unroll
-    for (int k = 0; k < NPC; k++) {
-        int i = tid + k * NT, tk = i >> 5, part = i & 31;
-        if (tk < ntok)   // rows of absent pairs only feed outputs that are never stored
-            *(v4i *)(&bs[tk * DN_LROW + part * 16]) = *(const gptr_u4 *)(qa + (size_t)(p0 + tk) * MFF + part * 16);
+        for (int k = 0; k < NPC; k++) {
+            int i = tid + k * NT, tk = i >> 5, part = i & 31;
+            if (tk < ntok)   // rows of absent pairs only feed outputs that are never stored
+                *(v4i *)(&bs[tk * DN_LROW + part * 16]) = *(const gptr_u4 *)(qa + (size_t)(p0 + tk) * MFF + part * 16);
+        }
+    } else {
+        // half-wave h of wave w takes pair 8k + 2w + h; lane o = l % 32 quantises the 16 values of mfma-order
+        // part o (columns g*128 + s*32 + hh*16 + tq*4 + b, g = o/8, hh = o/4 % 2, tq = o % 4), as k_quant_act
+        int o = l & 31, g = o >> 3, hh = (o >> 2) & 1, tq = o & 3;
+#pragma unroll 2
+        for (int k = 0; k < NPC; k++) {
+            int tk = (tid >> 5) + 8 * k;
+            float v[16];
+            if (tk < ntok) {
+                const float *ar = act + (size_t)(p0 + tk) * MFF + g * 128 + hh * 16 + tq * 4;
+#pragma unroll
+                for (int q4 = 0; q4 < 4; q4++) {
+                    float4 f = *(const float4 *)(ar + q4 * 32);
+                    v[q4 * 4] = f.x; v[q4 * 4 + 1] = f.y; v[q4 * 4 + 2] = f.z; v[q4 * 4 + 3] = f.w;
+                }
+            } else {
+#pragma unroll
+                for (int q4 = 0; q4 < 16; q4++) v[q4] = 0.0f;
+            }
+            quant_half<128>(v, l, bs + tk * DN_LROW, &sqs[tk], &sqsum[tk]);
+        }
     }
     if (!D16 && tid < RPB * 64) *(float4 *)(&sds[rb0 * 256 + tid * 4]) = *(const float4 *)(dsb + rb0 * 256 + tid * 4);
     __syncthreads();
+    if (QIN) {
+#pragma unroll
+        for (int j = 0; j < NF; j++) { int tk = min(j * 32 + r32, ntok - 1); qs[j] = sqs[tk]; qsm[j] = sqsum[tk]; }
+        if (rb0 == 0) {   // the tile's int8 act as k_quant_act writes it
+#pragma unroll
+            for (int k = 0; k < NPC; k++) {
+                int i = tid + k * NT, tk = i >> 5, part = i & 31;
+                if (tk < ntok) {
+                    *(v4i *)(qa_w + (size_t)(p0 + tk) * MFF + part * 16) = *(const v4i *)(&bs[tk * DN_LROW + part * 16]);
+                    if (part == 0) { qsa_w[p0 + tk] = sqs[tk]; qsuma_w[p0 + tk] = sqsum[tk]; }
+                }
+            }
+        }
+    }
 #pragma unroll
     for (int rr = 0; rr < RPB; rr++) {
         int rb = rb0 + rr;

@@ -280,10 +280,14 @@ static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
 }
 static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
     // large batches: 4 row blocks per workgroup (half the activation staging per row); else 2 (more workgroups)
+    // compact: act arrives in fp32 and each tile is quantised inside the down kernel (no k_quant_act launch)
     if (tn == 64 && compact && maxtiles >= S.ncu)
-        return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<4, true>, grid8(maxtiles * (MH / 256 / 4)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
-    if (tn == 64 && compact) return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<DN_RPB, true>, grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd); });
-    if (tn == 64) return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<DN_RPB, false>, grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, nullptr, dd); });
+        return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<4, true, true>, grid8(maxtiles * (MH / 256 / 4)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd,
+                                            (const float *)w.act, w.qa, w.qsa, w.qsuma); });
+    if (tn == 64 && compact) return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<DN_RPB, true, true>, grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, w.dov, dd,
+                                                                 (const float *)w.act, w.qa, w.qsa, w.qsuma); });
+    if (tn == 64) return launch(MMOE_K_DOWN, [&] { kl(k_down_tile<DN_RPB, false>, grid8(maxtiles * (MH / 256 / DN_RPB)), 256, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, nullptr, dd,
+                                                       nullptr, nullptr, nullptr, nullptr); });
     return launch(MMOE_K_DOWN, [&] { kl(k_down<16, DN16_W, DN16_RF>, grid8(maxtiles * (MH / (16 * DN16_W * DN16_RF))), 64 * DN16_W, 0, w.plan, w.tiles, w.eptr, w.qa, w.qsa, w.qsuma, w.down, dd); });
 }
 
@@ -310,7 +314,7 @@ static int stage_experts(Work &w, int np, int nu_max, int tn, bool device_groupi
     LAST.compact = w.compact;
     if (tn == 16 && S_expert16) return launch_expert16(w, maxtiles, dg, dd);
     if (launch_gateup(w, maxtiles, tn, dg)) return -1;
-    if (launch_quant_act(w, maxtiles, tn, np, dg)) return -1;
+    if (!w.compact && launch_quant_act(w, maxtiles, tn, np, dg)) return -1;
     if (launch_down(w, maxtiles, tn, dd, w.compact)) return -1;
     return 0;
 }
@@ -1064,7 +1068,9 @@ double mmoe_bench_stage(int kid, int reps) {
         switch (kid) {
             case MMOE_K_GATEUP: rc = launch_gateup(w, maxtiles, LAST.tn, nullptr); break;
             case MMOE_K_DOWN: rc = launch_down(w, maxtiles, LAST.tn, nullptr, LAST.compact); break;
-            case MMOE_K_QUANT_ACT: rc = launch_quant_act(w, maxtiles, LAST.tn, LAST.np, nullptr); break;
+            case MMOE_K_QUANT_ACT:
+                if (LAST.compact) { seterr("mmoe_bench_stage: the act quantisation runs inside the down kernel here"); return -1.0; }
+                rc = launch_quant_act(w, maxtiles, LAST.tn, LAST.np, nullptr); break;
             case MMOE_K_ROUTER: rc = LAST.hn ? stage_router(w, LAST.L, LAST.hn, LAST.nb, LAST.order) : -1; break;
             default: seterr("mmoe_bench_stage: kernel %d not repeatable", kid); return -1.0;
         }
