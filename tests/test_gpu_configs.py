@@ -98,6 +98,29 @@ def test_config3_batched_decode_24_layers(stack24):
     assert e <= 1e-5
 
 
+@pytest.mark.parametrize("nb,order,nl", [(64, M.ORDER_BATCH, 4), (64, M.ORDER_BATCH, 5), (40, M.ORDER_STEP, 4),
+                                         (100, M.ORDER_BATCH, 3), (300, M.ORDER_BATCH, 3)])
+def test_stack_matches_layer_by_layer(stack24, nb, order, nl):
+    """Stacked layers (one mmoe_stack_dev call over nl layers) against the same layers run one call at a time, bit
+    for bit: both orders, several sizes on the chain-router path, and 300 tokens, whose down results travel as
+    int16."""
+    lib = stack24[0]
+    x0 = M.synth_hidden(SEED, 720 + nb + nl, nb)
+    d_x = lib.mmoe_dev_alloc(x0.nbytes)
+    try:
+        M.check(lib.mmoe_h2d(d_x, M.ptr(x0), x0.nbytes), "h2d")
+        M.check(lib.mmoe_stack_dev(2, nl, d_x, nb, order), "stack")
+        xs = np.empty_like(x0); M.check(lib.mmoe_d2h(M.ptr(xs), d_x, x0.nbytes), "d2h")
+        M.check(lib.mmoe_h2d(d_x, M.ptr(x0), x0.nbytes), "h2d")
+        for L in range(2, 2 + nl):
+            M.check(lib.mmoe_stack_dev(L, 1, d_x, nb, order), "one layer")
+        x1 = np.empty_like(x0); M.check(lib.mmoe_d2h(M.ptr(x1), d_x, x0.nbytes), "d2h")
+    finally:
+        lib.mmoe_dev_free(d_x)
+    assert np.array_equal(xs.view(np.int32), x1.view(np.int32))
+    assert not np.array_equal(xs, x0)
+
+
 # ---------------------------------------------------------------- config 4
 CTX, T = 4096, 2048
 C4_LAYERS = [(0, 0), (3, 1)]          # (layer, glob): layer 3 attends to every earlier position
