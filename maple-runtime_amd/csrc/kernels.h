@@ -1497,14 +1497,24 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
 // k_gateup), reused for fp32 act; act in int8 (rows of DN_QW bytes); the tile's scales. Outputs: down[pair] as
 // k_down, the quantised act as k_quant_act; with gu_d / dn_d (checks on) also the int32 sums and fp32 act.
 #define E16_QW 528   // LDS bytes per quantised act row (512 + 16: rows 16 apart fall in different banks)
-template <int WAVES, int RING>
+// Grouping inside the kernel (GRP, device routing of up to 1024 tokens): instead of reading a plan that k_group
+// wrote, every workgroup forms the grouping of maple.c:924-938 itself from the top-8 (G): per-expert counts in
+// LDS, their inclusive scans (pairs, used experts, tiles of 16), its tile's expert and pair range, and the
+// tile's tokens (those that picked the expert, ascending: a prefix count over tokens). It writes its pairs'
+// utok, uw, sp, pu and tp (a pair's rank among its token's 8 pairs is the number of the token's experts with a
+// smaller id, since pairs are ordered by expert); workgroup 0 writes the plan, tile table, expert pointers and
+// eu as k_group does. The outputs equal k_group's.
+#define E16_GRP_MAXTOK 256
+struct GroupIn { const int *top; const float *tw; int nb; const ExpPtr *layer_tab; Plan *plan; Tile *tiles; ExpPtr *eptr_u;
+                 int *eu; int *utok; float *uw; int *tp; int *sp; int *pu; };
+template <int WAVES, int RING, bool GRP = false>
 __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                          const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
                                                          const int8_t *__restrict__ qx, const float *__restrict__ qsx,
                                                          const int *__restrict__ qsumx, float *__restrict__ down,
                                                          float *__restrict__ act_d, int8_t *__restrict__ qa_d,
                                                          float *__restrict__ qsa_d, int *__restrict__ qsuma_d,
-                                                         int *__restrict__ gu_d, int *__restrict__ dn_d) {
+                                                         int *__restrict__ gu_d, int *__restrict__ dn_d, GroupIn gi) {
     constexpr int NT = WAVES * 64;
     constexpr int GF = MFF / 16 / WAVES;       // gate (and up) fragments of 16 rows per wave
     constexpr int DF = MH / 16 / WAVES;        // down fragments per wave, in passes of 8
@@ -1514,13 +1524,80 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     __shared__ __attribute__((aligned(16))) float sg[MFF], su[MFF], sd[MH];
     __shared__ float tqs[16], aqs[16];
     __shared__ int tqsum[16], aqsum[16], toks[16];
-    int item = xcd_item(blockIdx.x, plan->ntile_gu);
-    if (item < 0) return;
-    Tile tl = tiles[item];
-    int p0 = tl.p0, ntok = tl.n;
-    ExpPtr ex = eptr[tl.u];
     int tid = threadIdx.x, l = tid & 63, G = l >> 4, r16 = l & 15;
     int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int p0, ntok, ge = 0, gti = 0;
+    ExpPtr ex;
+    __shared__ int gc[GRP ? MNE : 1], gsc[GRP ? MNE : 1], gsu[GRP ? MNE : 1], gst[GRP ? MNE : 1], gwc[WAVES], gex;
+    __shared__ int gslot[16];
+    __shared__ __attribute__((aligned(16))) int gtl[GRP ? E16_GRP_MAXTOK * MTOPK : 4];
+    __shared__ __attribute__((aligned(16))) float gtw[GRP ? E16_GRP_MAXTOK * MTOPK : 4], gqs[GRP ? E16_GRP_MAXTOK : 1];
+    __shared__ int gqsum[GRP ? E16_GRP_MAXTOK : 1];
+    if (!GRP) {
+        int item = xcd_item(blockIdx.x, plan->ntile_gu);
+        if (item < 0) return;
+        Tile tl = tiles[item];
+        p0 = tl.p0; ntok = tl.n;
+        ex = eptr[tl.u];
+    } else {
+        int nb = gi.nb, item = blockIdx.x;
+        if (tid < MNE) gc[tid] = 0;
+        if (tid < nb) {   // token b's top-8, weights and quantisation scales into LDS (nb <= E16_GRP_MAXTOK), so no
+                          // global load waits behind the code loads later
+            const v4i *tr = (const v4i *)(gi.top + tid * MTOPK), *wr = (const v4i *)(gi.tw + tid * MTOPK);
+            *(v4i *)(gtl + tid * MTOPK) = tr[0]; *(v4i *)(gtl + tid * MTOPK + 4) = tr[1];
+            *(v4i *)(gtw + tid * MTOPK) = wr[0]; *(v4i *)(gtw + tid * MTOPK + 4) = wr[1];
+            gqs[tid] = qsx[tid]; gqsum[tid] = qsumx[tid];
+        }
+        __syncthreads();
+        for (int i = tid; i < nb * MTOPK; i += NT) atomicAdd(&gc[gtl[i]], 1);
+        __syncthreads();
+        // inclusive scans over experts (waves 0-3, expert = tid): within each wave by shuffles, then the
+        // totals of the waves before
+        __shared__ int gwt[4][3];
+        int run = 0, used = 0, nt = 0, isc = 0, isu = 0, ist = 0;
+        if (tid < MNE) {
+            run = gc[tid]; used = run > 0; nt = (run + 15) >> 4;
+            isc = run; isu = used; ist = nt;
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                int a = __shfl_up(isc, o, 64), bq = __shfl_up(isu, o, 64), cq = __shfl_up(ist, o, 64);
+                if (l >= o) { isc += a; isu += bq; ist += cq; }
+            }
+            if (l == 63) { gwt[wv][0] = isc; gwt[wv][1] = isu; gwt[wv][2] = ist; }
+        }
+        __syncthreads();
+        if (tid < MNE) {
+            for (int w2 = 0; w2 < wv; w2++) { isc += gwt[w2][0]; isu += gwt[w2][1]; ist += gwt[w2][2]; }
+            gsc[tid] = isc; gsu[tid] = isu; gst[tid] = ist;
+        }
+        __syncthreads();
+        if (tid < MNE) {
+            int e = tid, pstart = gsc[e] - run, uidx = gsu[e] - used, tstart = gst[e] - nt;
+            if (item >= tstart && item < tstart + nt) gex = e;
+            if (blockIdx.x == 0) {   // the plan as k_group publishes it
+                gi.eu[e] = used ? uidx : -1;
+                if (used) {
+                    gi.plan->ue[uidx] = e; gi.plan->ustart[uidx] = pstart; gi.plan->tstart[uidx] = tstart;
+                    gi.eptr_u[uidx] = gi.layer_tab[e];
+                    for (int i = 0; i < nt; i++) gi.tiles[tstart + i] = Tile{uidx, pstart + i * 16, min(16, run - i * 16), 0};
+                }
+                if (e == MNE - 1) {
+                    int nu = gsu[e];
+                    gi.plan->nu = nu; gi.plan->np = gsc[e]; gi.plan->ntile_gu = gst[e]; gi.plan->tn = 16;
+                    gi.plan->ustart[nu] = gsc[e]; gi.plan->tstart[nu] = gst[e];
+                }
+            }
+        }
+        __syncthreads();
+        if (item >= gst[MNE - 1]) return;   // whole workgroup
+        int e = __builtin_amdgcn_readfirstlane(gex);   // uniform: the expert table entry loads as scalars
+        int cnt = gc[e], ti = item - (gst[e] - ((cnt + 15) >> 4));
+        p0 = gsc[e] - cnt + 16 * ti;
+        ntok = min(16, cnt - 16 * ti);
+        ex = gi.layer_tab[e];
+        ge = e; gti = ti;
+    }
     // lane offset of its 16 code bytes: row r16 of a fragment, 16-byte part of a 64-byte chunk (as k_gateup)
     int aoff = (G >> 1) * 32 + (G & 1) * 16;
     uint32_t gl = (uint32_t)r16 * (MH / 4) + aoff, dl = (uint32_t)r16 * (MFF / 4) + aoff;
@@ -1545,12 +1622,36 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     };
 #pragma unroll
     for (int g = 0; g < RING - 1; g++) load_group(g, cw[g]);
+    if (GRP) {   // the tile's tokens (after the first code loads are in flight)
+        // the tokens that picked the expert, in ascending order: entries 16 ti .. of that list
+        bool has = false; int slot = 0;
+        if (tid < gi.nb) {
+#pragma unroll
+            for (int k = 0; k < MTOPK; k++) if (gtl[tid * MTOPK + k] == ge) { has = true; slot = k; }
+        }
+        unsigned long long m = __ballot(has);
+        if (l == 0) gwc[wv] = __popcll(m);
+        __syncthreads();
+        int before = __popcll(m & ((1ull << l) - 1ull));
+        for (int w2 = 0; w2 < wv; w2++) before += gwc[w2];
+        int r = before - 16 * gti;
+        if (has && r >= 0 && r < 16) { toks[r] = tid; gslot[r] = slot; }
+        __syncthreads();
+        if (tid < ntok) {   // this tile's pairs in the grouping outputs
+            int b = toks[tid], sl = gslot[tid], pr = p0 + tid, rank = 0;
+            gi.utok[pr] = b; gi.uw[pr] = gtw[b * MTOPK + sl]; gi.pu[pr] = gsu[ge] - 1;
+            if (gi.sp) gi.sp[b * MTOPK + sl] = pr;
+#pragma unroll
+            for (int k = 0; k < MTOPK; k++) rank += gtl[b * MTOPK + k] < ge;
+            gi.tp[b * MTOPK + rank] = pr;
+        }
+    }
     // stage the tile: input rows (zeros for padding tokens), its quantisation scales, the expert's row scales
     if (tid < 16) {
-        int tk = tid < ntok ? utok[p0 + tid] : -1;
+        int tk = tid < ntok ? (GRP ? toks[tid] : utok[p0 + tid]) : -1;
         toks[tid] = tk;
-        tqs[tid] = tk >= 0 ? qsx[tk] : 0.0f;
-        tqsum[tid] = tk >= 0 ? qsumx[tk] : 0;
+        tqs[tid] = tk >= 0 ? (GRP ? gqs[tk] : qsx[tk]) : 0.0f;
+        tqsum[tid] = tk >= 0 ? (GRP ? gqsum[tk] : qsumx[tk]) : 0;
     }
     for (int i = tid; i < MFF; i += NT) { sg[i] = ex.gs[i]; su[i] = ex.us[i]; }
     for (int i = tid; i < MH / 4; i += NT) *(float4 *)(sd + i * 4) = *(const float4 *)(ex.ds + i * 4);

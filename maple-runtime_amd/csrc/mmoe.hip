@@ -72,6 +72,9 @@ struct Work {
     const float *norm_x = nullptr;  // set by mmoe_stack_dev: the router normalises this x into hn (post_ln norm_w)
     const uint16_t *norm_w = nullptr;
     float *rpart = nullptr;         // partial router logits [4][T][256] (approximate router)
+    bool grp16 = false;             // the last device routing left the grouping to k_expert16 (no k_group launch)
+    int grp_nb = 0;
+    const ExpPtr *grp_tab = nullptr;
     bool refine = false;            // the last router call left approximate logits for k_refine_topk
 };
 
@@ -249,6 +252,11 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bo
 // softmax/top-8, the int8 quantisation of hn and the grouping of nb tokens; eptr filled from layer L's table
 static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) {
     int nch = (nb + 63) / 64;
+    w.grp16 = false;
+    if (!w.refine && tn == 16 && S_expert16 && nb <= E16_GRP_MAXTOK) {   // top-8 only: k_expert16 forms the grouping
+        w.grp16 = true; w.grp_nb = nb; w.grp_tab = S.layers[L].tab;
+        return launch(MMOE_K_TOPK, [&] { kl(k_topk_quant, dim3((nb + 3) / 4, 2), 256, 0, w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, (int *)nullptr); });
+    }
     if (w.refine) {   // exact logits of each token's candidates, then its softmax/top-8 (and the quantisation)
         const LayerW &lw = S.layers[L];
         if (launch(MMOE_K_TOPK, [&] { kl(k_refine_topk, (nb + 3) / 4, 256, 0, w.rpart, d_hn, nb, lw.rc8, lw.bias, lw.w1max, w.rl, w.top, w.tw, w.hist); }) ||
@@ -267,7 +275,7 @@ static int stage_quant_x(Work &w, const float *d_hn, int nb) {
 }
 
 // gate/up (+SiLU), act quantisation, down for np pairs under w.plan / w.eptr / w.utok
-static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int dec; float *x; bool compact; } LAST;
+static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int dec; float *x; bool compact, grp; } LAST;
 
 static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8); }  // xcd_item needs a multiple of 8
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
@@ -292,9 +300,15 @@ static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
 }
 
 // tiles of 16 with the fused path: one workgroup per tile does gate/up, the act quantisation and down
-static int launch_expert16(Work &w, int maxtiles, int *dg, int *dd) {
+// grp: the grouping is formed in the kernel from w.top / w.tw (device routing), else read from the plan
+static int launch_expert16(Work &w, int maxtiles, int *dg, int *dd, bool grp) {
+    if (grp) {
+        GroupIn gi{w.top, w.tw, w.grp_nb, w.grp_tab, w.plan, w.tiles, w.eptr, w.eu, w.utok, w.uw, w.tp, w.sp, w.pu};
+        return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING, true>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx,
+                                              w.qsumx, w.down, dg ? w.act : nullptr, w.qa, w.qsa, w.qsuma, dg, dd, gi); });
+    }
     return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx,
-                                          w.down, dg ? w.act : nullptr, w.qa, w.qsa, w.qsuma, dg, dd); });
+                                          w.down, dg ? w.act : nullptr, w.qa, w.qsa, w.qsuma, dg, dd, GroupIn{}); });
 }
 static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
     if (tn == 64) {
@@ -312,7 +326,8 @@ static int stage_experts(Work &w, int np, int nu_max, int tn, bool device_groupi
     int *dg = S.debug ? w.dbg_gu : nullptr, *dd = S.debug ? w.dbg_dn : nullptr;
     w.compact = device_grouping && tn == 64 && !S.debug;
     LAST.compact = w.compact;
-    if (tn == 16 && S_expert16) return launch_expert16(w, maxtiles, dg, dd);
+    LAST.grp = device_grouping && w.grp16;
+    if (tn == 16 && S_expert16) return launch_expert16(w, maxtiles, dg, dd, LAST.grp);
     if (launch_gateup(w, maxtiles, tn, dg)) return -1;
     if (!w.compact && launch_quant_act(w, maxtiles, tn, np, dg)) return -1;
     if (launch_down(w, maxtiles, tn, dd, w.compact)) return -1;
@@ -1062,7 +1077,7 @@ double mmoe_bench_stage(int kid, int reps) {
         }
         if (LAST.tn == 16 && S_expert16 && kid != MMOE_K_ROUTER) {
             if (kid != MMOE_K_GATEUP) { seterr("mmoe_bench_stage: the fused expert path has one kernel (MMOE_K_GATEUP)"); return -1.0; }
-            if (launch_expert16(w, maxtiles, nullptr, nullptr)) return -1.0;
+            if (launch_expert16(w, maxtiles, nullptr, nullptr, LAST.grp)) return -1.0;
             continue;
         }
         switch (kid) {
