@@ -594,14 +594,24 @@ __global__ void __launch_bounds__(512) k_group(const int *__restrict__ hist, int
         used = run > 0; nt = (run + tn - 1) / tn;
         sc[t] = run; su[t] = used; st[t] = nt; msk[t] = 0ull;
     }
-    __syncthreads();
-    for (int o = 1; o < MNE; o <<= 1) {
-        int a = 0, bq = 0, cq = 0;
-        if (t < MNE && t >= o) { a = sc[t - o]; bq = su[t - o]; cq = st[t - o]; }
-        __syncthreads();
-        if (t < MNE) { sc[t] += a; su[t] += bq; st[t] += cq; }
-        __syncthreads();
+    // inclusive scans over the 256 experts: within each of waves 0-3 by shuffles, then the totals of the waves
+    // before (one barrier instead of two per doubling step)
+    __shared__ int wtot[4][3];
+    int isc = run, isu = used, ist = nt, l = t & 63, w4 = t >> 6;
+    if (t < MNE) {
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            int a = __shfl_up(isc, o, 64), bq = __shfl_up(isu, o, 64), cq = __shfl_up(ist, o, 64);
+            if (l >= o) { isc += a; isu += bq; ist += cq; }
+        }
+        if (l == 63) { wtot[w4][0] = isc; wtot[w4][1] = isu; wtot[w4][2] = ist; }
     }
+    __syncthreads();
+    if (t < MNE) {
+        for (int w2 = 0; w2 < w4; w2++) { isc += wtot[w2][0]; isu += wtot[w2][1]; ist += wtot[w2][2]; }
+        sc[t] = isc; su[t] = isu; st[t] = ist;
+    }
+    __syncthreads();
     if (t < MNE) {
         int e = t, pstart = sc[e] - run, uidx = su[e] - used, tstart = st[e] - nt;
         sbase[e] = pstart + pre;
