@@ -764,8 +764,8 @@ __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl
 // p, and so tw, differ only through the softmax sum's approximate small terms.
 #define RG_ERRK (2.0f * 463.0f * 1.01f / 16777216.0f)
 #define RT_HP 260    // LDS floats per chain of the staged input (256 + 4 against bank conflicts)
-// One wave per token, 4 tokens per block (grid = ceil(nb / 4)); the tokens' int8 quantisation is k_quant, a
-// launch of its own (blocks of this kernel hold many registers). The input row sits in LDS chain-major
+// One wave per token, 4 tokens per block (grid = (ceil(nb / 4), 2)); the blocks of grid row 1 quantise the
+// tokens instead (in the same wave they would raise the register count of the refinement). The input row sits in LDS chain-major
 // (hc[j][m] = hn[j + 8m]); lane = (candidate slot l / 8, chain l % 8), so 8 candidates are resolved per pass,
 // each lane's 256-long FMA chain reading the router's chain-order copy (k_router_chainmajor, NCH = 8) with all
 // 32 of its 16-byte loads issued before the FMAs. Writes rl (exact for candidates, else approximate), top, tw
@@ -773,12 +773,17 @@ __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl
 __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P, const float *__restrict__ hn, int nb,
                                                      const uint16_t *__restrict__ wc8, const float *__restrict__ bias,
                                                      const float *__restrict__ w1max, float *__restrict__ rl,
-                                                     int *__restrict__ top, float *__restrict__ tw, int *__restrict__ hist) {
+                                                     int *__restrict__ top, float *__restrict__ tw, int *__restrict__ hist,
+                                                     int8_t *__restrict__ qx, float *__restrict__ qsx, int *__restrict__ qsumx) {
     __shared__ __attribute__((aligned(16))) float hsc[4][8 * RT_HP];
     __shared__ float row[4][MNE], E[4][MNE];
     __shared__ int cand[4][MNE];
     int wv = threadIdx.x >> 6, l = threadIdx.x & 63, b = blockIdx.x * 4 + wv;
     if (b >= nb) return;   // whole wave; no block-wide barrier below
+    if (blockIdx.y == 1) {   // grid y = 2: the tokens' int8 quantisation (maple.c prep) in blocks of their own
+        quant_wave<MH>(hn + (size_t)b * MH, l, qx + (size_t)b * MH, qsx + b, qsumx + b);
+        return;
+    }
     const float *xr = hn + (size_t)b * MH;
     float4 f[8];
 #pragma unroll

@@ -259,8 +259,8 @@ static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) 
     }
     if (w.refine) {   // exact logits of each token's candidates, then its softmax/top-8 (and the quantisation)
         const LayerW &lw = S.layers[L];
-        if (launch(MMOE_K_TOPK, [&] { kl(k_refine_topk, (nb + 3) / 4, 256, 0, w.rpart, d_hn, nb, lw.rc8, lw.bias, lw.w1max, w.rl, w.top, w.tw, w.hist); }) ||
-            launch(MMOE_K_QUANT, [&] { kl(k_quant<MH>, (nb + 3) / 4, 256, 0, d_hn, nb, w.qx, w.qsx, w.qsumx); }))
+        if (launch(MMOE_K_TOPK, [&] { kl(k_refine_topk, dim3((nb + 3) / 4, 2), 256, 0, w.rpart, d_hn, nb, lw.rc8, lw.bias, lw.w1max, w.rl, w.top, w.tw,
+                                          w.hist, w.qx, w.qsx, w.qsumx); }))
             return -1;
     } else if (launch(MMOE_K_TOPK, [&] { kl(k_topk_quant, dim3((nb + 3) / 4, 2), 256, 0, w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
     w.hist_used = nch * MNE;   // cleared by this call's combine

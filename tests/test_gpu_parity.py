@@ -485,3 +485,20 @@ def test_expert16_fused_matches_three_kernels(zipf_layer, nb):
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name} differs"
     finally:
         M.check(lib.mmoe_set_expert_path(1), "expert path")
+
+
+@pytest.mark.parametrize("nb", [12, 40])
+def test_step_order_batch_matches_oracle(layer0, nb):
+    """A batch in step order above the decode path (the chain router's step order, the grouping inside the
+    small-tile kernel, the combine over slots sp/tw): every token's x equals maple.c's step() on that token alone,
+    here the oracle's step restatement on sampled tokens, bit for bit in the top-8 and within the bar in x."""
+    x, hn = normed_hidden(SEED, 4300 + nb, nb)
+    xg = run_gpu(layer0.L, hn, x, M.ORDER_STEP)
+    top = M.read("TOP", (nb, 8), np.int32)
+    for b in (0, nb // 2, nb - 1):
+        xo = x[b].copy()
+        o = O.moe_step(hn[b], layer0.router, layer0.table, xo)
+        assert np.array_equal(top[b], o["top"].reshape(8)), f"token {b}: top-8 differs"
+        e = relmax(xg[b] - x[b], xo - x[b])
+        print(f"\n  nb={nb} token {b}: x bit-exact {np.array_equal(xg[b], xo)}, relmax {e:.1e}")
+        assert e <= TOL
