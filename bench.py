@@ -393,9 +393,21 @@ def main():
         lib.mmoe_graph_reset()
         bms, _ = timed(bstep, max(5, args.steps // 5), 2)
         lib.mmoe_graph_reset()
-        log(f"batched decode 64 x 24 layers: {bms * 1e3:.1f} us/step, {64 / bms * 1e3:.0f} tok/s")
+        # untimed: the experts each layer uses (for the step's algorithmic bytes) and per-kernel device times
+        lib.mmoe_d2d(d_xb, d_xb0, xb0.nbytes)
+        nus = []
+        for L in range(NL):
+            M.check(lib.mmoe_stack_dev(L, 1, d_xb, 64, M.ORDER_BATCH), "batched decode layer")
+            nus.append(int(M.read_plan()["nu"]))
+        bbytes = sum(nus) * CODES_SCALES_PER_EXPERT
+        bk = prof_pass(lambda i: (lib.mmoe_d2d(d_xb, d_xb0, xb0.nbytes), M.check(lib.mmoe_stack_dev(0, NL, d_xb, 64, M.ORDER_BATCH), "stack")), 2)
+        log(f"batched decode 64 x 24 layers: {bms * 1e3:.1f} us/step, {64 / bms * 1e3:.0f} tok/s, "
+            f"{bbytes / bms / 1e6:.0f} GB/s on the used experts' codes+scales ({sum(nus) / NL:.1f} experts per layer)")
         extra["batched_decode"] = dict(workload="config 3: 64 sequences x 1 token x 24 MoE layers (batch order)",
-                                       value=round(64 / bms * 1e3, 1), unit="tokens/s", ms_per_step=round(bms, 4))
+                                       value=round(64 / bms * 1e3, 1), unit="tokens/s", ms_per_step=round(bms, 4),
+                                       experts_per_layer=round(sum(nus) / NL, 1), step_gbs=round(bbytes / bms / 1e6, 1),
+                                       step_frac_hbm=round(bbytes / bms / 1e6 / HBM_PEAK_GBS, 4),
+                                       kernels_us_per_layer={k: round(v[0] / v[1] * 1e3, 2) for k, v in bk.items()})
         T0 = 128
         for LP in LPS:
             M.check(lib.mmoe_set_bias(LP, None), "bias off")
@@ -407,9 +419,11 @@ def main():
         def cstep(i):
             M.check(lib.mmoe_moe_dev(LPS[i % len(LPS)], d_h128, T0, d_x128, M.ORDER_BATCH), "moe_dev 128")
         cms, _ = timed(cstep, max(5, args.steps // 5), 2)
+        ck = prof_pass(cstep, 8)
         log(f"prefill 128 (config 0): {cms * 1e3:.1f} us/layer, {T0 / cms * 1e3:.0f} tok/s")
         extra["prefill_128"] = dict(workload="config 0: 128-token chunk, 1 MoE layer, unbiased router",
-                                    value=round(T0 / cms * 1e3, 1), unit="tokens/s", ms_per_layer=round(cms, 4))
+                                    value=round(T0 / cms * 1e3, 1), unit="tokens/s", ms_per_layer=round(cms, 4),
+                                    kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in ck.items()})
 
     # ---- config 4: a 2048-token chunk through 24 whole layers (attention + MoE) on the card, positions 0..2047
     # and 2048..4095 of a 4096-position key/value cache (mmoe_gfull_stack); the dense q/k/v/o projections of all
