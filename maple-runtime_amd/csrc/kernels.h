@@ -1503,16 +1503,17 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
 // quantisation of act and down in one launch (maple.c:471-479, 498-505, 825-832). With a few pairs per expert
 // these layers stream the expert's 798,720 bytes of codes and scales and do little arithmetic, so one
 // workgroup per tile streams the whole expert through a register ring, as fast as a plain copy of the same
-// blocks; act never leaves LDS. Block = 8 waves; wave w takes gate and up rows 64w .. +64 (8 fragments of 16 rows
-// on v_mfma_i32_16x16x64_i8, operand mapping of k_gateup), then down rows 256w .. +256 in two passes of 128.
-// The code loads form 12 groups of 8 16-byte loads per lane, each group whole rows (16 rows x 512 bytes of a
-// gate and an up fragment, or 4 down fragments x 128 bytes: 8 KB contiguous per wave; reading 64 bytes of
-// many rows per group instead streamed 20% slower). The ring holds 4 groups, so the down codes are in flight
-// while gate/up finishes. LDS: the tile's int8 input (16 rows of 2048 bytes, 16-byte parts swizzled as in
-// k_gateup), reused for fp32 act; act in int8 (rows of DN_QW bytes); the tile's scales. Outputs: down[pair] as
-// k_down, the quantised act as k_quant_act; with gu_d / dn_d (checks on) also the int32 sums and fp32 act.
+// blocks; act never leaves LDS. Block = WAVES waves (16 in use: 128 VGPRs, 4 waves per SIMD); wave w takes
+// GF = 512 / (16 WAVES) gate fragments of 16 rows and the same up rows (v_mfma_i32_16x16x64_i8, operand mapping
+// of k_gateup), then DF = 2048 / (16 WAVES) down fragments in passes of 8. The code loads come in groups of
+// 8 16-byte loads per lane, each group whole rows (16 rows x 512 bytes of a gate and an up fragment, or 4 down
+// fragments x 128 bytes: 8 KB contiguous per wave; reading 64 bytes of many rows per group instead streamed
+// 20% slower), RING groups deep in registers, so the down codes are in flight while gate/up finishes. LDS: the
+// tile's int8 input (16 rows of 2048 bytes, 16-byte parts swizzled as in k_gateup), reused for fp32 act; act
+// in int8 (rows of E16_QW bytes); the tile's scales. Outputs: down[pair] as k_down, the quantised act as
+// k_quant_act; with gu_d / dn_d (checks on) also the int32 sums and fp32 act.
 #define E16_QW 528   // LDS bytes per quantised act row (512 + 16: rows 16 apart fall in different banks)
-// Grouping inside the kernel (GRP, device routing of up to 1024 tokens): instead of reading a plan that k_group
+// Grouping inside the kernel (GRP, device routing of up to E16_GRP_MAXTOK tokens): instead of reading a plan that k_group
 // wrote, every workgroup forms the grouping of maple.c:924-938 itself from the top-8 (G): per-expert counts in
 // LDS, their inclusive scans (pairs, used experts, tiles of 16), its tile's expert and pair range, and the
 // tile's tokens (those that picked the expert, ascending: a prefix count over tokens). It writes its pairs'
