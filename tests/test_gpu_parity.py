@@ -460,9 +460,9 @@ def test_zipf_mfma_router_matches_exact(zipf_layer):
 
 @pytest.mark.parametrize("nb", [9, 100, 255])
 def test_expert16_fused_matches_three_kernels(zipf_layer, nb):
-    """Tiles of 16 pairs: the fused whole-expert kernel (gate/up, act quantisation and down in one launch) against
-    the three separate kernels, bit for bit in every intermediate (int32 sums, act, its int8 quantisation, down)
-    and in x. The Zipf bias gives experts of many tiles (the hot expert gets most tokens) next to single-pair
+    """Tiles of 16 pairs: the fused whole-expert kernel (grouping, gate/up, act quantisation and down in one launch)
+    against k_group and the three separate kernels, bit for bit in every intermediate (the grouping's utok, uw,
+    tp, sp and plan, int32 sums, act, its int8 quantisation, down) and in x. The Zipf bias gives experts of many tiles (the hot expert gets most tokens) next to single-pair
     tiles, so ragged tiles, padding rows and several workgroups per expert all occur."""
     lib = M.lib()
     L = zipf_layer.L
@@ -477,11 +477,16 @@ def test_expert16_fused_matches_three_kernels(zipf_layer, nb):
             out[fused] = [xg] + [M.read(n, (P, k), t) for n, k, t in (("GU_I32", 1024, np.int32), ("ACT", 512, np.float32),
                                                                      ("QA", 512, np.int8), ("QSA", 1, np.float32),
                                                                      ("QSUMA", 1, np.int32), ("DN_I32", 2048, np.int32),
-                                                                     ("DOWN", 2048, np.float32))]
+                                                                     ("DOWN", 2048, np.float32), ("UTOK", 1, np.int32),
+                                                                     ("UW", 1, np.float32), ("TP", 1, np.int32),
+                                                                     ("SP", 1, np.int32))]
+            plan = M.read_plan()
+            out[fused] += [np.asarray(plan["ue"]), np.asarray(plan["ustart"]), np.array([plan["nu"], plan["np"], plan["ntile"], plan["tn"]])]
         cnt = np.diff(M.read_plan()["ustart"])
         print(f"\n  nb={nb}: {len(cnt)} experts, largest {cnt.max()} pairs ({int(((cnt + 15) // 16).sum())} tiles)")
         assert nb <= 16 or cnt.max() > 16
-        for name, a, b in zip(("x", "GU_I32", "ACT", "QA", "QSA", "QSUMA", "DN_I32", "DOWN"), out[0], out[1]):
+        for name, a, b in zip(("x", "GU_I32", "ACT", "QA", "QSA", "QSUMA", "DN_I32", "DOWN", "UTOK", "UW", "TP", "SP",
+                               "plan ue", "plan ustart", "plan nu np ntile tn"), out[0], out[1]):
             assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name} differs"
     finally:
         M.check(lib.mmoe_set_expert_path(1), "expert path")
