@@ -1523,7 +1523,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
 #define E16_GRP_MAXTOK 256
 struct GroupIn { const int *top; const float *tw; int nb; const ExpPtr *layer_tab; Plan *plan; Tile *tiles; ExpPtr *eptr_u;
                  int *eu; int *utok; float *uw; int *tp; int *sp; int *pu; };
-template <int WAVES, int RING, bool GRP = false>
+template <int WAVES, int RING, bool GRP = false, int GL = 8>
 __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                          const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
                                                          const int8_t *__restrict__ qx, const float *__restrict__ qsx,
@@ -1534,7 +1534,12 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     constexpr int NT = WAVES * 64;
     constexpr int GF = MFF / 16 / WAVES;       // gate (and up) fragments of 16 rows per wave
     constexpr int DF = MH / 16 / WAVES;        // down fragments per wave, in passes of 8
-    constexpr int NGU = 2 * GF, NG = NGU + DF / 4, NFR = 8;
+    // GL loads of 16 bytes per lane per group: a gate/up group is a gate and an up fragment over CPG chunks of
+    // 256 columns, a down group FPG down fragments over both chunks of 256 columns
+    constexpr int NFR = GL, CPG = GL / 2, GPF = 8 / CPG, FPG = GL / 2, GPP = 8 / FPG;
+    constexpr int NACC = 8;                    // accumulators: 2 GF gate/up fragments, then a down pass of 8
+    static_assert(GL % 2 == 0 && 8 % CPG == 0 && 2 * GF <= NACC && FPG * GPP == NACC && DF % FPG == 0, "k_expert16 group shape");
+    constexpr int NGU = GF * GPF, NG = NGU + DF / FPG;
     __shared__ __attribute__((aligned(16))) int8_t xs[16 * MH];     // input rows; later fp32 act [16][512]
     __shared__ __attribute__((aligned(16))) int8_t qs8[16 * E16_QW];
     __shared__ __attribute__((aligned(16))) float sg[MFF], su[MFF], sd[MH];
@@ -1625,15 +1630,15 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     // 4q .. 4q+3 of pass ps (8 fragments), both chunks (load k: fragment 4q + k / 2, chunk k & 1)
     auto load_group = [&](int g, v4i (&dst)[NFR]) {
         if (g < NGU) {
-            int fp = g >> 1, hh = g & 1;
+            int fp = g / GPF, cb = (g % GPF) * CPG;
 #pragma unroll
             for (int k = 0; k < NFR; k++)
-                dst[k] = *(const gptr_u4 *)((k < 4 ? gb : ub) + fp * 16 * (MH / 4) + gl + (hh * 4 + (k & 3)) * 64);
+                dst[k] = *(const gptr_u4 *)((k < CPG ? gb : ub) + fp * 16 * (MH / 4) + gl + (cb + k % CPG) * 64);
         } else {
-            int ps = (g - NGU) >> 1, q = (g - NGU) & 1;
+            int ps = (g - NGU) / GPP, q = (g - NGU) % GPP;
 #pragma unroll
             for (int k = 0; k < NFR; k++)
-                dst[k] = *(const gptr_u4 *)(db + (ps * 128 + (4 * q + (k >> 1)) * 16) * (MFF / 4) + dl + (k & 1) * 64);
+                dst[k] = *(const gptr_u4 *)(db + (ps * 128 + (FPG * q + (k >> 1)) * 16) * (MFF / 4) + dl + (k & 1) * 64);
         }
     };
 #pragma unroll
@@ -1681,38 +1686,38 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     }
     __syncthreads();
 
-    v4i acc[NFR];
+    v4i acc[NACC];
 #pragma unroll
-    for (int f = 0; f < NFR; f++) acc[f] = v4i{0, 0, 0, 0};
+    for (int f = 0; f < NACC; f++) acc[f] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int g = 0; g < NG; g++) {
         if (g + RING - 1 < NG) load_group(g + RING - 1, cw[(g + RING - 1) % RING]);
         const v4i(&c)[NFR] = cw[g % RING];
         if (g < NGU) {
-            int fp = g >> 1, hh = g & 1;
+            int fp = g / GPF, cb = (g % GPF) * CPG;
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++)
+            for (int cc = 0; cc < CPG; cc++)
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     int part = (G >> 1) * 8 + (G & 1) * 4 + t;
-                    v4i bv = *(const v4i *)(xs + r16 * MH + (hh * 4 + cc) * 256 + ((part ^ r16) * 16));
+                    v4i bv = *(const v4i *)(xs + r16 * MH + (cb + cc) * 256 + ((part ^ r16) * 16));
                     uint32_t wg = (uint32_t)(t == 0 ? c[cc].x : t == 1 ? c[cc].y : t == 2 ? c[cc].z : c[cc].w);
-                    uint32_t wu = (uint32_t)(t == 0 ? c[4 + cc].x : t == 1 ? c[4 + cc].y : t == 2 ? c[4 + cc].z : c[4 + cc].w);
+                    uint32_t wu = (uint32_t)(t == 0 ? c[CPG + cc].x : t == 1 ? c[CPG + cc].y : t == 2 ? c[CPG + cc].z : c[CPG + cc].w);
                     acc[fp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(decode_word(wg), bv, acc[fp], 0, 0, 0);
                     acc[GF + fp] = __builtin_amdgcn_mfma_i32_16x16x64_i8(decode_word(wu), bv, acc[GF + fp], 0, 0, 0);
                 }
         } else {
-            int q = (g - NGU) & 1;
+            int q = (g - NGU) % GPP;
 #pragma unroll
             for (int h = 0; h < 2; h++)
 #pragma unroll
                 for (int t = 0; t < 4; t++) {
                     v4i bv = *(const v4i *)(qs8 + r16 * E16_QW + h * 256 + (G >> 1) * 128 + (G & 1) * 64 + t * 16);
 #pragma unroll
-                    for (int j = 0; j < 4; j++) {
+                    for (int j = 0; j < FPG; j++) {
                         const v4i cj = c[2 * j + h];
                         uint32_t w = (uint32_t)(t == 0 ? cj.x : t == 1 ? cj.y : t == 2 ? cj.z : cj.w);
-                        acc[4 * q + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(decode_word(w), bv, acc[4 * q + j], 0, 0, 0);
+                        acc[FPG * q + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(decode_word(w), bv, acc[FPG * q + j], 0, 0, 0);
                     }
                 }
         }
@@ -1762,16 +1767,16 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
                 }
             }
 #pragma unroll
-            for (int f = 0; f < NFR; f++) acc[f] = v4i{0, 0, 0, 0};
+            for (int f = 0; f < NACC; f++) acc[f] = v4i{0, 0, 0, 0};
         }
-        if (g >= NGU && ((g - NGU) & 1)) {
+        if (g >= NGU && (g - NGU) % GPP == GPP - 1) {
             // down epilogue of pass ps: rows wv*DF*16 + 128ps + 16f + 4G + i of pair p0 + n
-            int ps = (g - NGU) >> 1;
+            int ps = (g - NGU) / GPP;
             if (r16 < ntok) {
                 float qs = aqs[r16]; int qsum = aqsum[r16];
                 float *dp = down + (size_t)(p0 + r16) * MH;
 #pragma unroll
-                for (int f = 0; f < NFR; f++) {
+                for (int f = 0; f < NACC; f++) {
                     int row0 = wv * DF * 16 + ps * 128 + f * 16 + 4 * G;
                     float o[4];
 #pragma unroll
@@ -1781,7 +1786,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
                 }
             }
 #pragma unroll
-            for (int f = 0; f < NFR; f++) acc[f] = v4i{0, 0, 0, 0};
+            for (int f = 0; f < NACC; f++) acc[f] = v4i{0, 0, 0, 0};
         }
     }
 }

@@ -32,6 +32,7 @@
 #ifndef DN_RPB
 #define E16_W 16   // fused small-tile expert kernel: waves per workgroup, code groups in the register ring
 #define E16_RING 3
+#define E16_GL 4     // 16-byte code loads per lane in one ring group
 #define DN_RPB 2   // down row blocks of 256 per workgroup
 #endif
 
@@ -304,10 +305,10 @@ static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
 static int launch_expert16(Work &w, int maxtiles, int *dg, int *dd, bool grp) {
     if (grp) {
         GroupIn gi{w.top, w.tw, w.grp_nb, w.grp_tab, w.plan, w.tiles, w.eptr, w.eu, w.utok, w.uw, w.tp, w.sp, w.pu};
-        return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING, true>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx,
+        return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING, true, E16_GL>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx,
                                               w.qsumx, w.down, dg ? w.act : nullptr, w.qa, w.qsa, w.qsuma, dg, dd, gi); });
     }
-    return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx,
+    return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING, false, E16_GL>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx,
                                           w.down, dg ? w.act : nullptr, w.qa, w.qsa, w.qsuma, dg, dd, GroupIn{}); });
 }
 static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
