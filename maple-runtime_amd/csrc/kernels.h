@@ -1505,10 +1505,11 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
 // workgroup per tile streams the whole expert through a register ring, as fast as a plain copy of the same
 // blocks; act never leaves LDS. Block = WAVES waves (16 in use: 128 VGPRs, 4 waves per SIMD); wave w takes
 // GF = 512 / (16 WAVES) gate fragments of 16 rows and the same up rows (v_mfma_i32_16x16x64_i8, operand mapping
-// of k_gateup), then DF = 2048 / (16 WAVES) down fragments in passes of 8. The code loads come in groups of
-// 8 16-byte loads per lane, each group whole rows (16 rows x 512 bytes of a gate and an up fragment, or 4 down
-// fragments x 128 bytes: 8 KB contiguous per wave; reading 64 bytes of many rows per group instead streamed
-// 20% slower), RING groups deep in registers, so the down codes are in flight while gate/up finishes. LDS: the
+// of k_gateup), then DF = 2048 / (16 WAVES) down fragments in passes of 8. The code loads come in groups of GL
+// 16-byte loads per lane, each group whole cache lines of consecutive rows (a gate and an up fragment over
+// GL / 2 chunks, or GL / 2 down fragments over both chunks; reading 64 bytes of many rows per group instead
+// streamed 20% slower), RING groups deep in registers. Small groups (GL = 4, 3 deep) beat large ones (8, 3
+// deep) by 8%: every workgroup issues its first loads at once, and the first group lands sooner. LDS: the
 // tile's int8 input (16 rows of 2048 bytes, 16-byte parts swizzled as in k_gateup), reused for fp32 act; act
 // in int8 (rows of E16_QW bytes); the tile's scales. Outputs: down[pair] as k_down, the quantised act as
 // k_quant_act; with gu_d / dn_d (checks on) also the int32 sums and fp32 act.
