@@ -1524,7 +1524,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_down(const Plan *__restrict__ pl
 #define E16_GRP_MAXTOK 256
 struct GroupIn { const int *top; const float *tw; int nb; const ExpPtr *layer_tab; Plan *plan; Tile *tiles; ExpPtr *eptr_u;
                  int *eu; int *utok; float *uw; int *tp; int *sp; int *pu; };
-template <int WAVES, int RING, bool GRP = false, int GL = 8>
+template <int WAVES, int RING, int GRP = 0, int GL = 8>
 __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                          const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
                                                          const int8_t *__restrict__ qx, const float *__restrict__ qsx,
@@ -1548,21 +1548,19 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     __shared__ int tqsum[16], aqsum[16], toks[16];
     int tid = threadIdx.x, l = tid & 63, G = l >> 4, r16 = l & 15;
     int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    int p0, ntok, ge = 0, gti = 0;
+    int p0 = 0, ntok = 0, ge = 0, gti = 0;
     ExpPtr ex;
-    __shared__ int gc[GRP ? MNE : 1], gsc[GRP ? MNE : 1], gsu[GRP ? MNE : 1], gst[GRP ? MNE : 1], gwc[WAVES], gex;
+    constexpr bool GR = GRP != 0;
+    __shared__ int gc[GR ? MNE : 1], gsc[GR ? MNE : 1], gsu[GR ? MNE : 1], gst[GR ? MNE : 1], gsx[GR ? MNE : 1], gwc[WAVES], gex;
     __shared__ int gslot[16];
-    __shared__ __attribute__((aligned(16))) int gtl[GRP ? E16_GRP_MAXTOK * MTOPK : 4];
-    __shared__ __attribute__((aligned(16))) float gtw[GRP ? E16_GRP_MAXTOK * MTOPK : 4], gqs[GRP ? E16_GRP_MAXTOK : 1];
-    __shared__ int gqsum[GRP ? E16_GRP_MAXTOK : 1];
-    if (!GRP) {
-        int item = xcd_item(blockIdx.x, plan->ntile_gu);
-        if (item < 0) return;
-        Tile tl = tiles[item];
-        p0 = tl.p0; ntok = tl.n;
-        ex = eptr[tl.u];
-    } else {
-        int nb = gi.nb, item = blockIdx.x;
+    __shared__ __attribute__((aligned(16))) int gtl[GR ? E16_GRP_MAXTOK * MTOPK : 4];
+    __shared__ __attribute__((aligned(16))) float gtw[GR ? E16_GRP_MAXTOK * MTOPK : 4], gqs[GR ? E16_GRP_MAXTOK : 1];
+    __shared__ int gqsum[GR ? E16_GRP_MAXTOK : 1];
+    __shared__ int gwt[4][4];
+    // the grouping: the top-8 rows into LDS, counts per expert, inclusive scans over experts of pairs (gsc), used
+    // experts (gsu), tiles of 16 (gst) and tiles after an expert's first (gsx); workgroup 0 publishes the plan
+    auto group_scan = [&]() {
+        int nb = gi.nb;
         if (tid < MNE) gc[tid] = 0;
         if (tid < nb) {   // token b's top-8, weights and quantisation scales into LDS (nb <= E16_GRP_MAXTOK), so no
                           // global load waits behind the code loads later
@@ -1574,30 +1572,24 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
         __syncthreads();
         for (int i = tid; i < nb * MTOPK; i += NT) atomicAdd(&gc[gtl[i]], 1);
         __syncthreads();
-        // inclusive scans over experts (waves 0-3, expert = tid): within each wave by shuffles, then the
-        // totals of the waves before
-        __shared__ int gwt[4][3];
-        int run = 0, used = 0, nt = 0, isc = 0, isu = 0, ist = 0;
+        // within each of waves 0-3 (expert = tid) by shuffles, then the totals of the waves before
+        int run = 0, used = 0, nt = 0, isc = 0, isu = 0, ist = 0, isx = 0;
         if (tid < MNE) {
             run = gc[tid]; used = run > 0; nt = (run + 15) >> 4;
-            isc = run; isu = used; ist = nt;
+            isc = run; isu = used; ist = nt; isx = nt > 1 ? nt - 1 : 0;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
-                int a = __shfl_up(isc, o, 64), bq = __shfl_up(isu, o, 64), cq = __shfl_up(ist, o, 64);
-                if (l >= o) { isc += a; isu += bq; ist += cq; }
+                int a = __shfl_up(isc, o, 64), bq = __shfl_up(isu, o, 64), cq = __shfl_up(ist, o, 64), dq = __shfl_up(isx, o, 64);
+                if (l >= o) { isc += a; isu += bq; ist += cq; isx += dq; }
             }
-            if (l == 63) { gwt[wv][0] = isc; gwt[wv][1] = isu; gwt[wv][2] = ist; }
+            if (l == 63) { gwt[wv][0] = isc; gwt[wv][1] = isu; gwt[wv][2] = ist; gwt[wv][3] = isx; }
         }
         __syncthreads();
         if (tid < MNE) {
-            for (int w2 = 0; w2 < wv; w2++) { isc += gwt[w2][0]; isu += gwt[w2][1]; ist += gwt[w2][2]; }
-            gsc[tid] = isc; gsu[tid] = isu; gst[tid] = ist;
-        }
-        __syncthreads();
-        if (tid < MNE) {
-            int e = tid, pstart = gsc[e] - run, uidx = gsu[e] - used, tstart = gst[e] - nt;
-            if (item >= tstart && item < tstart + nt) gex = e;
+            for (int w2 = 0; w2 < wv; w2++) { isc += gwt[w2][0]; isu += gwt[w2][1]; ist += gwt[w2][2]; isx += gwt[w2][3]; }
+            gsc[tid] = isc; gsu[tid] = isu; gst[tid] = ist; gsx[tid] = isx;
             if (blockIdx.x == 0) {   // the plan as k_group publishes it
+                int e = tid, pstart = isc - run, uidx = isu - used, tstart = ist - nt;
                 gi.eu[e] = used ? uidx : -1;
                 if (used) {
                     gi.plan->ue[uidx] = e; gi.plan->ustart[uidx] = pstart; gi.plan->tstart[uidx] = tstart;
@@ -1605,16 +1597,40 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
                     for (int i = 0; i < nt; i++) gi.tiles[tstart + i] = Tile{uidx, pstart + i * 16, min(16, run - i * 16), 0};
                 }
                 if (e == MNE - 1) {
-                    int nu = gsu[e];
-                    gi.plan->nu = nu; gi.plan->np = gsc[e]; gi.plan->ntile_gu = gst[e]; gi.plan->tn = 16;
-                    gi.plan->ustart[nu] = gsc[e]; gi.plan->tstart[nu] = gst[e];
+                    int nu = isu;
+                    gi.plan->nu = nu; gi.plan->np = isc; gi.plan->ntile_gu = ist; gi.plan->tn = 16;
+                    gi.plan->ustart[nu] = isc; gi.plan->tstart[nu] = ist;
                 }
             }
         }
         __syncthreads();
-        if (item >= gst[MNE - 1]) return;   // whole workgroup
+    };
+    // GRP == 2: workgroup e < 256 takes the first tile of expert e, so its code loads go out before the grouping
+    // (wasted for unused experts: they leave after it); workgroups 256.. take the further tiles of experts with
+    // more than 16 pairs, in expert order. GRP == 1: workgroup b takes the b-th tile in expert order.
+    const bool first_tile = GRP == 2 && blockIdx.x < MNE;
+    if (!GR) {
+        int item = xcd_item(blockIdx.x, plan->ntile_gu);
+        if (item < 0) return;
+        Tile tl = tiles[item];
+        p0 = tl.p0; ntok = tl.n;
+        ex = eptr[tl.u];
+    } else if (first_tile) {
+        ge = blockIdx.x; gti = 0;
+        ex = gi.layer_tab[ge];
+    } else {
+        group_scan();
+        int item = GRP == 2 ? (int)blockIdx.x - MNE : (int)blockIdx.x;
+        if (tid < MNE) {
+            int e = tid, nt = (gc[e] + 15) >> 4;
+            if (GRP == 2) { int xs0 = gsx[e] - (nt > 1 ? nt - 1 : 0); if (item >= xs0 && item < gsx[e]) gex = e; }
+            else { int ts0 = gst[e] - nt; if (item >= ts0 && item < gst[e]) gex = e; }
+        }
+        __syncthreads();
+        if (item >= (GRP == 2 ? gsx[MNE - 1] : gst[MNE - 1])) return;   // whole workgroup
         int e = __builtin_amdgcn_readfirstlane(gex);   // uniform: the expert table entry loads as scalars
-        int cnt = gc[e], ti = item - (gst[e] - ((cnt + 15) >> 4));
+        int cnt = gc[e];
+        int ti = GRP == 2 ? 1 + item - (gsx[e] - (((cnt + 15) >> 4) - 1)) : item - (gst[e] - ((cnt + 15) >> 4));
         p0 = gsc[e] - cnt + 16 * ti;
         ntok = min(16, cnt - 16 * ti);
         ex = gi.layer_tab[e];
@@ -1644,7 +1660,13 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     };
 #pragma unroll
     for (int g = 0; g < RING - 1; g++) load_group(g, cw[g]);
-    if (GRP) {   // the tile's tokens (after the first code loads are in flight)
+    if (first_tile) {   // the grouping, with the expert's first code loads in flight
+        group_scan();
+        int cnt = gc[ge];
+        if (cnt == 0) return;   // unused expert: the whole workgroup leaves
+        p0 = gsc[ge] - cnt; ntok = min(16, cnt);
+    }
+    if (GR) {   // the tile's tokens (after the first code loads are in flight)
         // the tokens that picked the expert, in ascending order: entries 16 ti .. of that list
         bool has = false; int slot = 0;
         if (tid < gi.nb) {
@@ -1670,10 +1692,10 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     }
     // stage the tile: input rows (zeros for padding tokens), its quantisation scales, the expert's row scales
     if (tid < 16) {
-        int tk = tid < ntok ? (GRP ? toks[tid] : utok[p0 + tid]) : -1;
+        int tk = tid < ntok ? (GR ? toks[tid] : utok[p0 + tid]) : -1;
         toks[tid] = tk;
-        tqs[tid] = tk >= 0 ? (GRP ? gqs[tk] : qsx[tk]) : 0.0f;
-        tqsum[tid] = tk >= 0 ? (GRP ? gqsum[tk] : qsumx[tk]) : 0;
+        tqs[tid] = tk >= 0 ? (GR ? gqs[tk] : qsx[tk]) : 0.0f;
+        tqsum[tid] = tk >= 0 ? (GR ? gqsum[tk] : qsumx[tk]) : 0;
     }
     for (int i = tid; i < MFF; i += NT) { sg[i] = ex.gs[i]; su[i] = ex.us[i]; }
     for (int i = tid; i < MH / 4; i += NT) *(float4 *)(sd + i * 4) = *(const float4 *)(ex.ds + i * 4);

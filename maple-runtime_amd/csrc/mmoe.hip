@@ -303,12 +303,12 @@ static int launch_down(Work &w, int maxtiles, int tn, int *dd, bool compact) {
 // tiles of 16 with the fused path: one workgroup per tile does gate/up, the act quantisation and down
 // grp: the grouping is formed in the kernel from w.top / w.tw (device routing), else read from the plan
 static int launch_expert16(Work &w, int maxtiles, int *dg, int *dd, bool grp) {
-    if (grp) {
+    if (grp) {   // workgroup e < 256: expert e's first tile; then one per further tile (at most np / 16 of them)
         GroupIn gi{w.top, w.tw, w.grp_nb, w.grp_tab, w.plan, w.tiles, w.eptr, w.eu, w.utok, w.uw, w.tp, w.sp, w.pu};
-        return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING, true, E16_GL>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx,
+        return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING, 2, E16_GL>, MNE + w.grp_nb * MTOPK / 16, 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx,
                                               w.qsumx, w.down, dg ? w.act : nullptr, w.qa, w.qsa, w.qsuma, dg, dd, gi); });
     }
-    return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING, false, E16_GL>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx,
+    return launch(MMOE_K_GATEUP, [&] { kl(k_expert16<E16_W, E16_RING, 0, E16_GL>, grid8(maxtiles), 64 * E16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx,
                                           w.down, dg ? w.act : nullptr, w.qa, w.qsa, w.qsuma, dg, dd, GroupIn{}); });
 }
 static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
