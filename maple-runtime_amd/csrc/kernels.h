@@ -388,95 +388,104 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ h
 // makes the approximate logit A differ from maple.c's chain result L, bounded in k_refine_topk.
 //
 // Partial logits on v_mfma_f32_32x32x16_bf16: P[q][b][e] = sum over columns [512 q, 512 q + 512) and the three
-// parts of w[e][c] * h_i[b][c], accumulated per chunk of 64 columns from zero (the 192 products of a chunk) and
-// the 8 chunk sums added in order, which keeps the rounding bound of k_refine_topk small. Block: 64 experts x 64 tokens x one column quarter q (grid.z), 4 waves, wave
-// (we, wt) owns the 32 x 32 output fragment (we, wt). Columns advance in chunks of 64: the router chunk
-// (64 x 64 bf16) and the input chunk (64 x 64 fp32) are read with coalesced 16-byte loads into registers two
+// parts of w[e][c] * h_i[b][c], accumulated per chunk of 64 columns from zero (the 192 products of a chunk, in
+// 16-column steps, each step over the three parts) and the 8 chunk sums added in order, which keeps the rounding
+// bound of k_refine_topk small. A block of WAVES waves takes 32 tokens x 32 WAVES EW experts x one column
+// quarter q (grid.z); wave w owns experts w * 32 EW .. +32 EW as EW fragments of 32 against the block's 32
+// tokens, so each input chunk is split into its parts once per block. Columns advance in chunks of 64: the
+// router chunk (bf16) and the input chunk (fp32) are read with coalesced 16-byte loads into registers two
 // chunks ahead, then stored to LDS (the input as its three bf16 parts; rows padded to 72 bf16).
 #define RM_KC 64
 #define RM_LR 72
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-__device__ __forceinline__ void split3(v4i f0, v4i f1, v4i &p1, v4i &p2, v4i &p3) {
-    uint32_t v[8] = {(uint32_t)f0.x, (uint32_t)f0.y, (uint32_t)f0.z, (uint32_t)f0.w,
-                     (uint32_t)f1.x, (uint32_t)f1.y, (uint32_t)f1.z, (uint32_t)f1.w};
-    uint32_t a[8], b[8], c[8];
+__device__ __forceinline__ void split3(v4i f, uint2 &p1, uint2 &p2, uint2 &p3) {
+    uint32_t v[4] = {(uint32_t)f.x, (uint32_t)f.y, (uint32_t)f.z, (uint32_t)f.w}, a[4], b[4], c[4];
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
+    for (int u = 0; u < 4; u++) {
         uint32_t b1 = v[u] & 0xffff0000u;
         float r1 = __uint_as_float(v[u]) - __uint_as_float(b1);
         uint32_t b2 = __float_as_uint(r1) & 0xffff0000u;
         float r2 = r1 - __uint_as_float(b2);
         a[u] = b1 >> 16; b[u] = b2 >> 16; c[u] = __float_as_uint(r2) >> 16;
     }
-    p1 = v4i{(int)(a[0] | a[1] << 16), (int)(a[2] | a[3] << 16), (int)(a[4] | a[5] << 16), (int)(a[6] | a[7] << 16)};
-    p2 = v4i{(int)(b[0] | b[1] << 16), (int)(b[2] | b[3] << 16), (int)(b[4] | b[5] << 16), (int)(b[6] | b[7] << 16)};
-    p3 = v4i{(int)(c[0] | c[1] << 16), (int)(c[2] | c[3] << 16), (int)(c[4] | c[5] << 16), (int)(c[6] | c[7] << 16)};
+    p1 = make_uint2(a[0] | a[1] << 16, a[2] | a[3] << 16);
+    p2 = make_uint2(b[0] | b[1] << 16, b[2] | b[3] << 16);
+    p3 = make_uint2(c[0] | c[1] << 16, c[2] | c[3] << 16);
 }
-__global__ void __launch_bounds__(256) k_router_mfma(const uint16_t *__restrict__ w, const float *__restrict__ hn, int nb,
-                                                     float *__restrict__ P) {
-    __shared__ __attribute__((aligned(16))) uint16_t ws[64 * RM_LR];
-    __shared__ __attribute__((aligned(16))) uint16_t hsl[3][64 * RM_LR];
+template <int WAVES, int EW>
+__global__ void __launch_bounds__(WAVES * 64) k_router_mfma(const uint16_t *__restrict__ w, const float *__restrict__ hn, int nb,
+                                                              float *__restrict__ P) {
+    constexpr int NT = WAVES * 64, ER = 32 * WAVES * EW;
+    constexpr int NW = ER * 8 / NT;              // router pieces (16 bytes) staged per thread: rows wrow + (NT / 8) i
+    constexpr int NH = 32 * 16 / NT;             // input pieces (4 floats) per thread: rows hrow + (NT / 16) i
+    __shared__ __attribute__((aligned(16))) uint16_t ws[ER * RM_LR];
+    __shared__ __attribute__((aligned(16))) uint16_t hsl[3][32 * RM_LR];
     int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, r = l & 31, kg = l >> 5;
-    int we = wv >> 1, wt = wv & 1;
-    int e0 = blockIdx.y * 64, t0 = blockIdx.x * 64, kq = blockIdx.z * (MH / 4);
-    int srow = tid >> 3, spc = tid & 7;          // staging: row srow + 32 i, 8-column piece spc of the chunk
-    const uint16_t *wsrc[2]; const float *hsrc[2];
+    int e0 = blockIdx.y * ER, t0 = blockIdx.x * 32, kq = blockIdx.z * (MH / 4);
+    int wrow = tid >> 3, wpc = tid & 7, hrow = tid >> 4, hq = tid & 15;
+    const uint16_t *wsrc = w + (size_t)(e0 + wrow) * MH + kq + wpc * 8;
+    const float *hsrc[NH];
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
-        wsrc[i] = w + (size_t)(e0 + srow + 32 * i) * MH + kq + spc * 8;
-        hsrc[i] = hn + (size_t)min(t0 + srow + 32 * i, nb - 1) * MH + kq + spc * 8;
-    }
-    v4i rw[2][2], rh[2][2][2];                   // [ring][row half] / [ring][row half][16-byte half]
-#define RM_LOAD(q_, k_)                                                                              \
-    {                                                                                                \
-        _Pragma("unroll") for (int i = 0; i < 2; i++) {                                              \
-            rw[q_][i] = *(const gptr_u4 *)(wsrc[i] + (k_));                                          \
-            rh[q_][i][0] = *(const gptr_u4 *)(hsrc[i] + (k_));                                       \
-            rh[q_][i][1] = *(const gptr_u4 *)(hsrc[i] + (k_) + 4);                                   \
-        }                                                                                            \
-    }
-    RM_LOAD(0, 0);
-    RM_LOAD(1, RM_KC);
-    f32x16 acc;
+    for (int i = 0; i < NH; i++) hsrc[i] = hn + (size_t)min(t0 + hrow + (NT / 16) * i, nb - 1) * MH + kq + hq * 4;
+    v4i rw[2][NW], rh[2][NH];
+#define RMW_LOAD(q_, k_)                                                                                 {                                                                                                        _Pragma("unroll") for (int i = 0; i < NW; i++)                                                           rw[q_][i] = *(const gptr_u4 *)(wsrc + (size_t)(NT / 8) * i * MH + (k_));                         _Pragma("unroll") for (int i = 0; i < NH; i++) rh[q_][i] = *(const gptr_u4 *)(hsrc[i] + (k_));     }
+    RMW_LOAD(0, 0);
+    RMW_LOAD(1, RM_KC);
+    f32x16 acc[EW];
 #pragma unroll
-    for (int i = 0; i < 16; i++) acc[i] = 0.0f;
+    for (int f = 0; f < EW; f++)
+#pragma unroll
+        for (int i = 0; i < 16; i++) acc[f][i] = 0.0f;
 #pragma unroll 2
     for (int ck = 0; ck < MH / 4 / RM_KC; ck++) {
         const int q = ck & 1;
         __syncthreads();
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            int o = (srow + 32 * i) * RM_LR + spc * 8;
-            *(v4i *)(&ws[o]) = rw[q][i];
-            v4i p1, p2, p3;
-            split3(rh[q][i][0], rh[q][i][1], p1, p2, p3);
-            *(v4i *)(&hsl[0][o]) = p1; *(v4i *)(&hsl[1][o]) = p2; *(v4i *)(&hsl[2][o]) = p3;
+        for (int i = 0; i < NW; i++) *(v4i *)(&ws[(wrow + (NT / 8) * i) * RM_LR + wpc * 8]) = rw[q][i];
+#pragma unroll
+        for (int i = 0; i < NH; i++) {
+            int o = (hrow + (NT / 16) * i) * RM_LR + hq * 4;
+            uint2 p1, p2, p3;
+            split3(rh[q][i], p1, p2, p3);
+            *(uint2 *)(&hsl[0][o]) = p1; *(uint2 *)(&hsl[1][o]) = p2; *(uint2 *)(&hsl[2][o]) = p3;
         }
         __syncthreads();
-        if (ck + 2 < MH / 4 / RM_KC) RM_LOAD(q, (ck + 2) * RM_KC);
-        f32x16 cacc;   // the chunk's own sum from zero, added to acc after: 192 products per accumulation
+        if (ck + 2 < MH / 4 / RM_KC) RMW_LOAD(q, (ck + 2) * RM_KC);
+        f32x16 cacc[EW];
 #pragma unroll
-        for (int i = 0; i < 16; i++) cacc[i] = 0.0f;
+        for (int f = 0; f < EW; f++)
+#pragma unroll
+            for (int i = 0; i < 16; i++) cacc[f][i] = 0.0f;
 #pragma unroll
         for (int kk = 0; kk < RM_KC; kk += 16) {
-            bf16x8 av = *(const bf16x8 *)(&ws[(we * 32 + r) * RM_LR + kk + kg * 8]);
+            bf16x8 av[EW];
+#pragma unroll
+            for (int f = 0; f < EW; f++) av[f] = *(const bf16x8 *)(&ws[(wv * 32 * EW + f * 32 + r) * RM_LR + kk + kg * 8]);
 #pragma unroll
             for (int sp = 0; sp < 3; sp++) {
-                bf16x8 bv = *(const bf16x8 *)(&hsl[sp][(wt * 32 + r) * RM_LR + kk + kg * 8]);
-                cacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av, bv, cacc, 0, 0, 0);
+                bf16x8 bv = *(const bf16x8 *)(&hsl[sp][r * RM_LR + kk + kg * 8]);
+#pragma unroll
+                for (int f = 0; f < EW; f++) cacc[f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[f], bv, cacc[f], 0, 0, 0);
             }
         }
 #pragma unroll
-        for (int i = 0; i < 16; i++) acc[i] = acc[i] + cacc[i];
-    }
-#undef RM_LOAD
-    // D: register i -> expert row (i/4)*8 + kg*4 + i%4 of the fragment, token column r
-    float *Pq = P + (size_t)blockIdx.z * nb * MNE;
+        for (int f = 0; f < EW; f++)
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        int e = e0 + we * 32 + (i >> 2) * 8 + kg * 4 + (i & 3), tk = t0 + wt * 32 + r;
-        if (tk < nb) Pq[(size_t)tk * MNE + e] = acc[i];
+            for (int i = 0; i < 16; i++) acc[f][i] = acc[f][i] + cacc[f][i];
+    }
+#undef RMW_LOAD
+    // D: register i -> expert row (i/4)*8 + kg*4 + i%4 of fragment f, token column r
+    float *Pq = P + (size_t)blockIdx.z * nb * MNE;
+    int tk = t0 + r;
+    if (tk < nb) {
+#pragma unroll
+        for (int f = 0; f < EW; f++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                int e = e0 + wv * 32 * EW + f * 32 + g * 8 + kg * 4;
+                *(float4 *)(Pq + (size_t)tk * MNE + e) = make_float4(acc[f][g * 4], acc[f][g * 4 + 1], acc[f][g * 4 + 2], acc[f][g * 4 + 3]);
+            }
     }
 }
 

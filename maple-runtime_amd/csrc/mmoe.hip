@@ -247,7 +247,8 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bo
         return launch(MMOE_K_ROUTER, [&] { kl(k_router_gemm<4>, dim3((nb + 15) / 16, MNE / RG_BE), 256, 0, d_hn, nb, lw.rf8, lw.bias, w.rl); });
     // approximate logits on the bf16 MFMA; k_refine_topk makes the top-8 exact
     w.refine = true;
-    return launch(MMOE_K_ROUTER, [&] { kl(k_router_mfma, dim3((nb + 63) / 64, MNE / 64, 4), 256, 0, lw.router, d_hn, nb, w.rpart); });
+    if (nb >= 1024) return launch(MMOE_K_ROUTER, [&] { kl(k_router_mfma<8, 1>, dim3((nb + 31) / 32, MNE / 256, 4), 512, 0, lw.router, d_hn, nb, w.rpart); });
+    return launch(MMOE_K_ROUTER, [&] { kl(k_router_mfma<4, 1>, dim3((nb + 31) / 32, MNE / 128, 4), 256, 0, lw.router, d_hn, nb, w.rpart); });
 }
 
 // softmax/top-8, the int8 quantisation of hn and the grouping of nb tokens; eptr filled from layer L's table
