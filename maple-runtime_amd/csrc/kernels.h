@@ -1836,6 +1836,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
 // k_quant_act would. This saves the separate quantisation launch at the cost of quantising each tile once per
 // workgroup of the tile (MH / 256 / RPB of them).
 #define DN_LROW (MFF + 16)
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 template <int RPB, bool D16, bool QIN = false>
 __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                       const ExpPtr *__restrict__ eptr, const int8_t *__restrict__ qa,
@@ -1951,7 +1952,23 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
         if (D16) {
             // d = sum - qsum as int16 into the wave's LDS tile [32 pairs][64 rows], one pair fragment at a time,
             // then out as 8 pairs x 128 bytes per store (lane: pair l/8 + 8k, 16-byte piece l%8)
+            // range check of the live pairs' 64 values per lane at once (sum within qsum +- 32767); only a wave
+            // holding a value outside takes the per-value path (marker -32768 and the int32 side entry)
             int16_t *tw = dtw + wv * (32 * DT_LD);
+            bool bad = false;
+#pragma unroll
+            for (int j = 0; j < NF; j++) {
+                int mn = acc[0][j][0], mx = mn;
+#pragma unroll
+                for (int f = 0; f < NA; f++)
+#pragma unroll
+                    for (int i = 0; i < 16; i++) { mn = min(mn, acc[f][j][i]); mx = max(mx, acc[f][j][i]); }
+                bad |= j * 32 + r32 < ntok && (mn < qsm[j] - 32767 || mx > qsm[j] + 32767);
+            }
+            const bool wbad = __ballot(bad) != 0;
+            u16x2 qsm2[NF];
+#pragma unroll
+            for (int j = 0; j < NF; j++) qsm2[j] = u16x2{(uint16_t)qsm[j], (uint16_t)qsm[j]};
 #pragma unroll
             for (int j = 0; j < NF; j++) {
 #pragma unroll
@@ -1959,13 +1976,20 @@ __global__ void __launch_bounds__(256, 2) k_down_tile(const Plan *__restrict__ p
 #pragma unroll
                     for (int g = 0; g < 4; g++) {
                         int rl = f * 32 + g * 8 + G2 * 4, tk = j * 32 + r32;
-                        uint32_t w2[2] = {0, 0};
+                        uint32_t w2[2];
 #pragma unroll
-                        for (int i = 0; i < 4; i++) {
-                            int d = acc[f][j][g * 4 + i] - qsm[j];
-                            bool ok = d >= -32767 && d <= 32767;
-                            if (!ok && tk < ntok) dov[(size_t)(p0 + tk) * MH + rb * 256 + wv * 64 + rl + i] = d;
-                            w2[i >> 1] |= (uint32_t)(uint16_t)(ok ? d : -32768) << (16 * (i & 1));
+                        for (int h = 0; h < 2; h++) {   // low halves of two sums, minus qsum mod 2^16 in each half
+                            uint32_t pk = __builtin_amdgcn_perm((uint32_t)acc[f][j][g * 4 + 2 * h + 1], (uint32_t)acc[f][j][g * 4 + 2 * h], 0x05040100u);
+                            w2[h] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(u16x2, pk) - qsm2[j]);
+                        }
+                        if (wbad) {
+#pragma unroll
+                            for (int i = 0; i < 4; i++) {
+                                int d = acc[f][j][g * 4 + i] - qsm[j];
+                                if (d >= -32767 && d <= 32767) continue;
+                                if (tk < ntok) dov[(size_t)(p0 + tk) * MH + rb * 256 + wv * 64 + rl + i] = d;
+                                w2[i >> 1] = (w2[i >> 1] & (0xffff0000u >> (16 * (i & 1)))) | (0x8000u << (16 * (i & 1)));
+                            }
                         }
                         *(uint2 *)(tw + r32 * DT_LD + rl) = make_uint2(w2[0], w2[1]);
                     }
