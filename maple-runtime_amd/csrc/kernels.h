@@ -679,6 +679,19 @@ __global__ void k_plan_from_ustart(const int *__restrict__ ustart, int nu, Plan 
     plan->nu = nu; plan->np = ustart[nu]; plan->ntile_gu = t; plan->tn = tn;
 }
 
+// rint of four values |v| <= 2^22 as four int8 in one word (byte i = value i), and their sum added to *sum.
+// v + 1.5 * 2^23 lies in [2^23, 2^24), where the float spacing is 1, so the addition rounds v to the nearest
+// integer, ties to even (rintf's rounding), and the low byte of the sum's bit pattern is that integer mod 256.
+// The word's signed bytes are summed with one v_dot4 against 1,1,1,1.
+__device__ __forceinline__ uint32_t rint_pack4(float a, float b, float c, float d, int *sum) {
+    const float MAG = 12582912.0f;
+    uint32_t ua = __float_as_uint(a + MAG), ub = __float_as_uint(b + MAG), uc = __float_as_uint(c + MAG), ud = __float_as_uint(d + MAG);
+    uint32_t lo = __builtin_amdgcn_perm(ub, ua, 0x0c0c0400u), hi = __builtin_amdgcn_perm(ud, uc, 0x0c0c0400u);
+    uint32_t w = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    *sum = __builtin_amdgcn_sdot4((int)w, 0x01010101, *sum, false);
+    return w;
+}
+
 // =====================================================================================================
 // Per-vector int8 quantisation, maple.c:183-194 as compiled with maple.c's -ffast-math flags:
 // qs = mx * fl(1/127), inv = 127 / mx (both 1 when mx = 0), q = rint(x * inv). One wave per vector of
@@ -718,16 +731,8 @@ __device__ __forceinline__ void quant_wave(const float *__restrict__ xr, int l, 
         if (o < NCHK) {
             uint32_t wds[4];
 #pragma unroll
-            for (int d = 0; d < 4; d++) {
-                uint32_t wd = 0;
-#pragma unroll
-                for (int bb = 0; bb < 4; bb++) {
-                    int qi = (int)__builtin_rintf(v[k][d * 4 + bb] * inv);
-                    sum += qi;
-                    wd |= (uint32_t)(qi & 0xff) << (8 * bb);
-                }
-                wds[d] = wd;
-            }
+            for (int d = 0; d < 4; d++)
+                wds[d] = rint_pack4(v[k][d * 4] * inv, v[k][d * 4 + 1] * inv, v[k][d * 4 + 2] * inv, v[k][d * 4 + 3] * inv, &sum);
             *(uint4 *)(q + (o >> 3) * (128 + GPAD) + (o & 7) * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
         }
     }
@@ -901,16 +906,7 @@ __device__ __forceinline__ void quant_half(const float *v, int l, int8_t *q, flo
     if (mx > 0.0f) { qsv = mx * (1.0f / 127.0f); inv = 127.0f / mx; }
     int sum = 0; uint32_t wds[4];
 #pragma unroll
-    for (int d = 0; d < 4; d++) {
-        uint32_t wd = 0;
-#pragma unroll
-        for (int bb = 0; bb < 4; bb++) {
-            int qi = (int)__builtin_rintf(v[d * 4 + bb] * inv);
-            sum += qi;
-            wd |= (uint32_t)(qi & 0xff) << (8 * bb);
-        }
-        wds[d] = wd;
-    }
+    for (int d = 0; d < 4; d++) wds[d] = rint_pack4(v[d * 4] * inv, v[d * 4 + 1] * inv, v[d * 4 + 2] * inv, v[d * 4 + 3] * inv, &sum);
     int o = l & 31;
     if (store) *(uint4 *)(q + (o >> 3) * GS + (o & 7) * 16) = make_uint4(wds[0], wds[1], wds[2], wds[3]);
     sum += dpp<0xB1>(sum); sum += dpp<0x4E>(sum); sum += dpp<0x141>(sum); sum += dpp<0x140>(sum);
