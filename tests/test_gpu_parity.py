@@ -275,6 +275,50 @@ def test_moe_batch_mfma_router(layer0):
         M.check(lib.mmoe_set_router_mode(0), "router mode")
 
 
+@pytest.fixture(scope="module")
+def tie_layer():
+    """Layer 19: router weights all zero and a bias with large tie classes, so every logit is its expert's bias
+    exactly: 3 distinct leaders, then a class of 52 equal logits (e * 37 % 5 == 4) across the 8th place."""
+    lib = M.lib()
+    M.check(lib.mmoe_init(2048), "mmoe_init")
+    hl = HostLayer(SEED, 19)
+    hl.router = np.zeros((256, 2048), np.uint16)
+    hl.rid = M.register_layer(19, hl.blk, hl.router)
+    hl.bias = ((np.arange(256) * 37) % 5).astype(np.float32) * 0.25
+    hl.bias[[250, 3, 180]] = [3.0, 2.5, 2.25]
+    M.check(lib.mmoe_set_bias(19, M.ptr(hl.bias)), "bias")
+    yield hl
+    M.check(lib.mmoe_set_bias(19, None), "bias off")
+
+
+@pytest.mark.parametrize("nb,order", [(1, 1), (1, 0), (5, 0), (64, 0), (600, 0)])
+def test_topk_ties_pick_lowest_index(tie_layer, nb, order):
+    """Equal logits give equal softmax probabilities, and maple.c's repeated strict-> scans (maple.c:913-923)
+    then pick the lowest expert index first: expected top-8 = 250, 3, 180, then the 5 lowest experts of the tied
+    class. Checked against the oracle for the decode kernels (nb 1, both orders), small batches (nb 5), the
+    fused small-tile path (nb 64) and the MFMA router with exact refinement (nb 600, where every tied expert is
+    a candidate); top-8, weights, grouping and x."""
+    lib = M.lib()
+    M.check(lib.mmoe_set_debug(1), "debug")
+    M.check(lib.mmoe_set_router_mode(0), "router mode")
+    hl = tie_layer
+    x, hn = normed_hidden(SEED, 700 + nb, nb)
+    xg = run_gpu(hl.L, hn, x, order)
+    xo = x.copy()
+    if order == M.ORDER_STEP:
+        o = O.moe_step(hn[0], hl.router, hl.table, xo[0], bias=hl.bias)
+    else:
+        o = O.moe_batch(hn, hl.router, hl.table, xo, bias=hl.bias)
+    want = [250, 3, 180] + [e for e in range(256) if e * 37 % 5 == 4][:5]
+    otop = o["top"].reshape(nb, 8)
+    assert (otop == np.array(want)).all(), "oracle picks"
+    assert np.array_equal(M.read("TOP", (nb, 8), np.int32), otop), "top-8 indices differ"
+    assert np.array_equal(M.read("TW", (nb, 8), np.float32).view(np.int32), o["tw"].reshape(nb, 8).view(np.int32)), "weights differ"
+    assert np.array_equal(M.read("UTOK", (nb * 8,), np.int32), o["utok"]), "grouping differs"
+    assert relmax(xg - x, xo - x) <= TOL
+    print(f"\n  nb={nb} order={order}: top-8 {want}; x bit-exact {np.array_equal(xg, xo)}")
+
+
 def test_moe_batch_tn64_compact_sums(layer0):
     """With checks off the 64-token-tile path hands gate/up sums to k_act_quant and down results to k_combine as
     int16 (d = sum - qsum, int32 side buffer for the rare out-of-range entry): act int8 and x must still match."""
