@@ -1198,18 +1198,22 @@ __device__ __forceinline__ void gu_chunk(v16i (&acc)[2][2], const v4i (&cwc)[2][
 // holds row (i/4)*8 + G2*4 + i%4 of the 32-row block, token lane%32. An item is 128 gate + 128 up rows (wave w:
 // 32 of each) x a tile of 64 tokens (two fragments of 32). grid = 8 * NB workgroups; the ones on XCD x = blockIdx % 8 walk that XCD's
 // contiguous run of items (as xcd_item) with stride NB, so an XCD's L2 sees the tiles of few experts at a
-// time. The chunk pipeline runs on across items: while the last three chunks of one item are multiplied, the
-// first three of the next are loaded (codes and activations PD = 3 chunks ahead in 4-slot register rings,
-// activations then through two LDS stages), so no item starts with an empty pipeline.
-template <bool ACT>
-__global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
+// time. The chunk pipeline runs on across items: while the last chunks of one item are multiplied, the first
+// ones of the next are loaded (codes PD chunks ahead in a ring of PD + 1 register slots, activations PA chunks
+// ahead, then through two LDS stages), so no item starts with an empty pipeline. The default, PD = PA = 1 at
+// three workgroups per CU (168 VGPRs), beats PD = 3 / PA = 2 at two (214 VGPRs): the third wave per SIMD
+// fills the MFMA and VALU pipes better than the deeper prefetch hides latency.
+template <bool ACT, int PD = 1, int PA = 1, int OCC = 3>
+__global__ void __launch_bounds__(256, OCC) k_gateup_pk(const Plan *__restrict__ plan, const Tile *__restrict__ tiles,
                                                       const ExpPtr *__restrict__ eptr, const int *__restrict__ utok,
                                                       const int8_t *__restrict__ qx, const float *__restrict__ qsx,
                                                       const int *__restrict__ qsumx, void *__restrict__ out) {
     constexpr int TN = 64, NT = 256, NF = 2, NA = 2, RB = MFF / 128, NCH = MH / 256, BB = TN * GU_LROW;
     constexpr int NPC = TN * 16 / NT;          // 4 activation pieces of 16 bytes per thread per chunk
-    constexpr int PD = 3;                      // prefetch distance of the codes in chunks (ring of 4)
-    constexpr int PA = 2;                      // prefetch distance of the activations (ring of 2 + 2 LDS stages)
+    // PD: prefetch distance of the codes in chunks (ring of CR = PD + 1 slots, a divisor of NCH); PA: that of the
+    // activations (ring of PA, then 2 LDS stages); OCC: workgroups per CU the register budget is held to
+    constexpr int CR = PD + 1;
+    static_assert(NCH % CR == 0 && (PA == 1 || PA == 2), "k_gateup_pk pipeline shape");
     __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
     __shared__ int toks[2][TN];
     int nitems = plan->ntile_gu * RB;
@@ -1238,8 +1242,8 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
         for (int j = 0; j < NF; j++)
 #pragma unroll
             for (int i = 0; i < 16; i++) acc[f][j][i] = 0;
-    v4i cw[4][NA][2];   // codes of chunk c of any item in slot c % 4
-    v4i br[2][NPC];     // activations of chunk c in slot c % 2 until stored to LDS stage c % 2
+    v4i cw[CR][NA][2];  // codes of chunk c of any item in slot c % CR
+    v4i br[PA][NPC];    // activations of chunk c in slot c % PA until stored to LDS stage c % 2
 #define GU_LOADC(slot_, gb_, ub_, off_, c_)                                                                     \
     {                                                                                                           \
         cw[slot_][0][0] = *(const gptr_u4 *)((gb_) + (off_) + (c_) * 64);                                      \
@@ -1252,7 +1256,7 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
 #pragma unroll
     for (int c = 0; c < PA; c++)
 #pragma unroll
-        for (int k = 0; k < NPC; k++) br[c][k] = *(const gptr_u4 *)(qx + boff[k] + c * 256);
+        for (int k = 0; k < NPC; k++) br[c % PA][k] = *(const gptr_u4 *)(qx + boff[k] + c * 256);
 #pragma unroll
     for (int k = 0; k < NPC; k++) *(v4i *)(&bs[0][bdst + k * 16 * GU_LROW]) = br[0][k];
 
@@ -1275,20 +1279,20 @@ __global__ void __launch_bounds__(256, 2) k_gateup_pk(const Plan *__restrict__ p
                 for (int k = 0; k < NPC; k++) nboff[k] = (uint32_t)toks[slot ^ 1][(tid >> 4) + 16 * k] * MH + part * 16;
             }
             // prefetch codes of chunk ch + PD and activations of chunk ch + PA (of this item, or of the next one)
-            if (ch + PD < NCH) GU_LOADC((ch + PD) % 4, gcb, ucb, aoff, ch + PD)
-            else if (has_next) GU_LOADC((ch + PD) % 4, ngcb, nucb, naoff, (ch + PD) % NCH)
+            if (ch + PD < NCH) GU_LOADC((ch + PD) % CR, gcb, ucb, aoff, ch + PD)
+            else if (has_next) GU_LOADC((ch + PD) % CR, ngcb, nucb, naoff, (ch + PD) % NCH)
             if (ch + PA < NCH) {
 #pragma unroll
-                for (int k = 0; k < NPC; k++) br[ch % 2][k] = *(const gptr_u4 *)(qx + boff[k] + (ch + PA) * 256);
+                for (int k = 0; k < NPC; k++) br[ch % PA][k] = *(const gptr_u4 *)(qx + boff[k] + (ch + PA) * 256);
             } else if (has_next) {
 #pragma unroll
-                for (int k = 0; k < NPC; k++) br[ch % 2][k] = *(const gptr_u4 *)(qx + nboff[k] + ((ch + PA) % NCH) * 256);
+                for (int k = 0; k < NPC; k++) br[ch % PA][k] = *(const gptr_u4 *)(qx + nboff[k] + ((ch + PA) % NCH) * 256);
             }
-            gu_chunk<2>(acc, cw[ch % 4], &bs[ch % 2][0], G2, r32, ntok > 32);
+            gu_chunk<2>(acc, cw[ch % CR], &bs[ch % 2][0], G2, r32, ntok > 32);
             __builtin_amdgcn_sched_barrier(0);
             if (ch + 1 < NCH || has_next) {
 #pragma unroll
-                for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst + k * 16 * GU_LROW]) = br[(ch + 1) % 2][k];
+                for (int k = 0; k < NPC; k++) *(v4i *)(&bs[(ch + 1) % 2][bdst + k * 16 * GU_LROW]) = br[(ch + 1) % PA][k];
             }
         }
         // epilogue, token r32 of each fragment, rows (i/4)*8 + G2*4 + i%4 of the wave's 32. ACT: the activation

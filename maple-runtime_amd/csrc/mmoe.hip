@@ -280,11 +280,16 @@ static int stage_quant_x(Work &w, const float *d_hn, int nb) {
 static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int dec; float *x; bool compact, grp; } LAST;
 
 static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8); }  // xcd_item needs a multiple of 8
+#ifndef GU_OCC
+#define GU_OCC 3   // k_gateup_pk: persistent workgroups per CU, code / activation prefetch distances in chunks
+#define GU_PD 1     // (3 / 2 / 2, the deeper prefetch at two workgroups per CU, measured 64.5 against 60 us at config 2)
+#define GU_PA 1
+#endif
 static int launch_gateup(Work &w, int maxtiles, int tn, int *dg) {
     if (tn == 64) {   // checks on: int32 sums into the debug buffer; else the fp32 activation into w.act
-        int nblk = (int)grid8(S.ncu * 2 < maxtiles * (MFF / 128) ? S.ncu * 2 : maxtiles * (MFF / 128));   // two persistent blocks per CU
-        if (dg) return launch(MMOE_K_GATEUP, [&] { kl(k_gateup_pk<false>, nblk, 256, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, dg); });
-        return launch(MMOE_K_GATEUP, [&] { kl(k_gateup_pk<true>, nblk, 256, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act); });
+        int nblk = (int)grid8(S.ncu * GU_OCC < maxtiles * (MFF / 128) ? S.ncu * GU_OCC : maxtiles * (MFF / 128));   // persistent blocks, GU_OCC per CU
+        if (dg) return launch(MMOE_K_GATEUP, [&] { kl(k_gateup_pk<false, GU_PD, GU_PA, GU_OCC>, nblk, 256, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, dg); });
+        return launch(MMOE_K_GATEUP, [&] { kl(k_gateup_pk<true, GU_PD, GU_PA, GU_OCC>, nblk, 256, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act); });
     }
     return launch(MMOE_K_GATEUP, [&] { kl(k_gateup<16, GU16_W, GU16_RF>, grid8(maxtiles * (MFF / (16 * GU16_W * GU16_RF))), 64 * GU16_W, 0, w.plan, w.tiles, w.eptr, w.utok, w.qx, w.qsx, w.qsumx, w.act, dg); });
 }
