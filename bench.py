@@ -42,7 +42,8 @@ def pmc_traffic(kernel):
         return None
     for line in open(path):
         cols = [c.strip() for c in line.split("|")]
-        if len(cols) > 6 and cols[1] == kernel:
+        # "k<a>" also names an instantiation with further template arguments, "k<a, ...>"
+        if len(cols) > 6 and (cols[1] == kernel or (kernel.endswith(">") and cols[1].startswith(kernel[:-1] + ","))):
             return int(cols[6])
     return None
 
