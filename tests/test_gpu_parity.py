@@ -126,10 +126,11 @@ def test_moe_step(layer0):
     compare_layer(layer0, 1, M.ORDER_STEP)
 
 
-def test_gpre_moe(layer0):
-    """gpre_moe with a host grouping (maple.c:757-763 call) vs the oracle's grouped experts"""
+@pytest.mark.parametrize("nb", [48, 300])
+def test_gpre_moe(layer0, nb):
+    """gpre_moe with a host grouping (maple.c:757-763 call) vs the oracle's grouped experts; 300 tokens (2400
+    pairs) take the 64-pair tile kernels with a plan built from the host grouping"""
     lib = M.lib()
-    nb = 48
     x, hn = normed_hidden(SEED, 900, nb)
     rl = O.router_batch(hn, layer0.router)
     top, tw = O.topk(rl)
