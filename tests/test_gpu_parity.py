@@ -117,6 +117,15 @@ def test_moe_batch_gemm_router(layer0):
         M.check(M.lib().mmoe_set_router_mode(0), "router mode")
 
 
+@pytest.mark.parametrize("nb,refined", [(255, False), (511, False), (512, True), (1023, True), (1024, True)])
+def test_moe_batch_size_boundaries(layer0, nb, refined):
+    """Sizes at the path switches: 255 tokens is the largest batch whose grouping forms inside the fused
+    small-tile kernel; 511 the last one on the chain router and 512 the first on the MFMA router with exact
+    refinement; 1023 runs the router in blocks of 128 experts (ragged last 32-token block), 1024 in blocks of
+    all 256 experts."""
+    compare_layer(layer0, nb, M.ORDER_BATCH, f" boundary {nb}", refined=refined)
+
+
 def test_moe_batch_tn64(layer0):
     # 256 tokens -> 2048 pairs: the 64-token tile kernels
     compare_layer(layer0, 256, M.ORDER_BATCH)
