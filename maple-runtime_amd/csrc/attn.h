@@ -162,33 +162,61 @@ __global__ void __launch_bounds__(64) k_att_scores(const float *__restrict__ qkv
 }
 
 // Softmax sums of the 16 rows (heads) of token b, one workgroup per token: p = exp(s - max) (max from
-// k_att_scores) over 256-position chunks staged in LDS, summed in position order by 16 lanes (one row each);
-// inv[b * 16 + h] = 1 / sum. k_att_pv recomputes the same p.
-#define AT_SMCH 256
+// k_att_scores), summed in position order by 16 lanes of wave 0 (one row each); inv[b * 16 + h] = 1 / sum.
+// k_att_pv recomputes the same p. Waves 1-3 produce the p of 64-position chunks into two LDS buffers while
+// wave 0 sums the previous chunk, and load the raw scores one chunk further ahead into registers, so the
+// serial sums (the critical path) never wait for a load or an exp.
+#define AT_SMCH 64
+#define AT_SMPT ((16 * AT_SMCH + 191) / 192)   // p values per producer thread and chunk
 __global__ void __launch_bounds__(256) k_att_softmax(int pos0, int glob, int win, const float *__restrict__ sc,
                                                      const float *__restrict__ mx, float *__restrict__ inv, int ctx) {
     constexpr int LD = AT_SMCH + 4;   // 16-byte aligned rows; the 16 summing lanes hit distinct bank groups
-    __shared__ __attribute__((aligned(16))) float pl[16 * LD];
+    __shared__ __attribute__((aligned(16))) float pl[2][16 * LD];
+    __shared__ float smx[16];
     int b = blockIdx.x, tid = threadIdx.x, pos = pos0 + b;
-    int T = pos - att_lo(pos, glob, win) + 1;
+    int T = pos - att_lo(pos, glob, win) + 1, nch = (T + AT_SMCH - 1) / AT_SMCH;
     const float *rows = sc + (size_t)b * 16 * ctx;
     const float *mr = mx + b * 16;
+    int pt = tid - 64;                 // producer index (waves 1-3)
+    float sv[AT_SMPT];                 // raw scores of the next chunk to produce
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int k = 0; k < AT_SMPT; k++) {
+            int i = pt + 192 * k, r = i / AT_SMCH, p = i % AT_SMCH;
+            sv[k] = (i < 16 * AT_SMCH && c0 + p < T) ? rows[(size_t)r * ctx + c0 + p] : 0.0f;
+        }
+    };
+    auto produce = [&](float *buf) {
+#pragma unroll
+        for (int k = 0; k < AT_SMPT; k++) {
+            int i = pt + 192 * k;
+            if (i < 16 * AT_SMCH) buf[(i / AT_SMCH) * LD + i % AT_SMCH] = dexp(sv[k] - smx[i / AT_SMCH]);
+        }
+    };
+    if (tid < 16) smx[tid] = mr[tid];
+    if (pt >= 0) load(0);
+    __syncthreads();
+    if (pt >= 0) {
+        produce(pl[0]);
+        if (nch > 1) load(AT_SMCH);
+    }
+    __syncthreads();
     float sum = 0.0f;
-    for (int c0 = 0; c0 < T; c0 += AT_SMCH) {
-        int n = min(AT_SMCH, T - c0);
-        if (tid < n)
-#pragma unroll 4
-            for (int r = 0; r < 16; r++) pl[r * LD + tid] = dexp(rows[(size_t)r * ctx + c0 + tid] - mr[r]);
-        __syncthreads();
-        if (tid < 16) {   // in position order; 16 values are read ahead of their additions
-            const float4 *q4 = (const float4 *)(pl + tid * LD);
+    for (int c = 0; c < nch; c++) {
+        if (pt >= 0) {
+            if (c + 1 < nch) produce(pl[(c + 1) & 1]);
+            if (c + 2 < nch) load((c + 2) * AT_SMCH);
+        } else if (tid < 16) {   // in position order; 16 values are read ahead of their additions
+            int n = min(AT_SMCH, T - c * AT_SMCH);
+            const float *q = pl[c & 1] + tid * LD;
+            const float4 *q4 = (const float4 *)q;
             int t = 0;
             for (; t + 16 <= n; t += 16) {
-                float4 a = q4[t / 4], b = q4[t / 4 + 1], c = q4[t / 4 + 2], d = q4[t / 4 + 3];
-                sum += a.x; sum += a.y; sum += a.z; sum += a.w; sum += b.x; sum += b.y; sum += b.z; sum += b.w;
-                sum += c.x; sum += c.y; sum += c.z; sum += c.w; sum += d.x; sum += d.y; sum += d.z; sum += d.w;
+                float4 a = q4[t / 4], bq = q4[t / 4 + 1], cq = q4[t / 4 + 2], d = q4[t / 4 + 3];
+                sum += a.x; sum += a.y; sum += a.z; sum += a.w; sum += bq.x; sum += bq.y; sum += bq.z; sum += bq.w;
+                sum += cq.x; sum += cq.y; sum += cq.z; sum += cq.w; sum += d.x; sum += d.y; sum += d.z; sum += d.w;
             }
-            for (const float *q = pl + tid * LD; t < n; t++) sum += q[t];
+            for (; t < n; t++) sum += q[t];
         }
         __syncthreads();
     }
