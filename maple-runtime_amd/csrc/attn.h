@@ -254,18 +254,29 @@ __global__ void __launch_bounds__(256) k_att_pv(int nb, int pos0, int glob, int 
         src[k] = sc + (size_t)(ok ? r : 0) * ctx - lb + tt;   // + p0 gives the entry of position p0 + tt
         ivk[k] = ok ? inv[r] : 0.0f; mxk[k] = ok ? mx[r] : 0.0f;
     }
-    auto fetch = [&](int p0, float *w) {
+    // the raw scores of a run are loaded together (out-of-window slots read a valid address and are zeroed
+    // later) and turned into weights only after the current run's FMAs, so their latency hides behind them
+    float raw[PER];
+    auto load = [&](int p0) {
 #pragma unroll
         for (int k = 0; k < PER; k++) {
             int p = p0 + (tid + 256 * k) % AT_PVCH;
-            w[k] = (p >= lbk[k] && p <= pbk[k]) ? dexp(src[k][p0] - mxk[k]) * ivk[k] : 0.0f;
+            raw[k] = *((p >= lbk[k] && p <= pbk[k]) ? src[k] + p0 : sc);
+        }
+    };
+    auto weights = [&](int p0, float *w) {
+#pragma unroll
+        for (int k = 0; k < PER; k++) {
+            int p = p0 + (tid + 256 * k) % AT_PVCH;
+            w[k] = (p >= lbk[k] && p <= pbk[k]) ? dexp(raw[k] - mxk[k]) * ivk[k] : 0.0f;
         }
     };
     float acc[NB][2];
 #pragma unroll
     for (int bi = 0; bi < NB; bi++) acc[bi][0] = acc[bi][1] = 0.0f;
     float wn[PER];
-    fetch(lo0, wn);
+    load(lo0);
+    weights(lo0, wn);
     for (int p0 = lo0; p0 <= phi; p0 += AT_PVCH) {
         __syncthreads();
 #pragma unroll
@@ -274,7 +285,8 @@ __global__ void __launch_bounds__(256) k_att_pv(int nb, int pos0, int glob, int 
             wl[jj][tt][bi] = wn[k];
         }
         __syncthreads();
-        if (p0 + AT_PVCH <= phi) fetch(p0 + AT_PVCH, wn);
+        const bool more = p0 + AT_PVCH <= phi;
+        if (more) load(p0 + AT_PVCH);
         int n = min(AT_PVCH, phi + 1 - p0);
         const uint32_t *vr = vp + (size_t)p0 * 256;
 #pragma unroll 8
@@ -289,6 +301,7 @@ __global__ void __launch_bounds__(256) k_att_pv(int nb, int pos0, int glob, int 
                 acc[bi][1] = __builtin_fmaf(w, v1, acc[bi][1]);
             }
         }
+        if (more) weights(p0 + AT_PVCH, wn);
     }
 #pragma unroll
     for (int bi = 0; bi < NB; bi++)
