@@ -222,6 +222,8 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
     v4i wv[16];
 #pragma unroll
     for (int q = 0; q < 16; q++) wv[q] = wp[q * NCH];
+    float be = 0.0f;
+    if (bias && j == 0) be = bias[e];   // with the weights' loads, added at the end
     if (NORM) {
         double sq = 0.0;
 #pragma unroll
@@ -277,7 +279,7 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
         if (NCH == 16) { for (int i = 0; i < 8; i++) s8[i] = v[i] + v[i + 8]; }
         else { for (int i = 0; i < 8; i++) s8[i] = v[i]; }
         float r = hsum8(s8);
-        if (bias) r = r + bias[e];
+        if (bias) r = r + be;
         rl[(size_t)b * MNE + e] = r;
     }
 }
@@ -308,6 +310,9 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ h
     float *hs = smem, *ws = smem + 8 * RG_MC * HP;
     int t = threadIdx.x, j = t >> 5, tg = (t >> 3) & 3, eg = t & 7;
     int b0 = blockIdx.x * BT, e0 = blockIdx.y * RG_BE;
+    static_assert(RG_BE == 64, "the output loop gives thread t expert e0 + t % 64 in every round");
+    float be = 0.0f;
+    if (bias) be = bias[e0 + (t & 63)];   // loaded at entry, added to the thread's logits at the end
     typedef float f4v __attribute__((ext_vector_type(4)));
     f4v hr[NH], wr[8];
     float acc[TPT][8];
@@ -375,7 +380,7 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ h
 #pragma unroll
         for (int jj = 0; jj < 8; jj++) v[jj] = red[(jj * BT + tok) * RG_BE + e];
         float r = hsum8(v);
-        if (bias) r = r + bias[e0 + e];
+        if (bias) r = r + be;
         if (b0 + tok < nb) rl[(size_t)(b0 + tok) * MNE + e0 + e] = r;
     }
 }
@@ -802,12 +807,16 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
     float4 f[8];
 #pragma unroll
     for (int i = 0; i < 8; i++) f[i] = *(const float4 *)(xr + (l + 64 * i) * 4);
-    float a[4];
+    float a[4], bb[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (bias) {   // issued with the partials' loads (one wait for all)
+#pragma unroll
+        for (int i = 0; i < 4; i++) bb[i] = bias[l + 64 * i];
+    }
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         size_t o = (size_t)b * MNE + l + 64 * i, qs = (size_t)nb * MNE;
         float v = (P[o] + P[o + qs]) + (P[o + 2 * qs] + P[o + 3 * qs]);
-        if (bias) v = v + bias[l + 64 * i];
+        if (bias) v = v + bb[i];
         a[i] = v;
     }
     float *hc = &hsc[wv][0];
@@ -849,6 +858,8 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
         bool on = c0 + slot < nc;
         int e = cand[wv][on ? c0 + slot : 0];
         const gptr_u4 *wp = (const gptr_u4 *)(wc8 + (size_t)e * MH + j * 8);   // 16 bytes q of the chain at wp[q * 8]
+        float be = 0.0f;
+        if (bias && j == 0) be = bias[e];   // loaded before the chain, added after it
         float acc = 0.0f;
 #pragma unroll
         for (int hb = 0; hb < 2; hb++) {   // the chain's weights in two halves of 16 x 16 bytes (registers)
@@ -872,7 +883,7 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
         for (int i = 0; i < 8; i++) s8[i] = __shfl(acc, (l & ~7) + i, 64);
         if (j == 0 && on) {
             float rv = hsum8(s8);
-            if (bias) rv = rv + bias[e];
+            if (bias) rv = rv + be;
             row[wv][e] = rv;
         }
     }
