@@ -2149,12 +2149,19 @@ __global__ void __launch_bounds__(256) k_combine(const float *__restrict__ down,
     if (b >= nb) return;
     float4 *xp = (float4 *)(x + (size_t)b * MH + c);
     float4 acc = (mode & 1) ? *xp : make_float4(0.f, 0.f, 0.f, 0.f);
+    // the token's 8 pair ids, then their weights and down rows, each level's loads issued together
+    int a[MTOPK]; float w[MTOPK]; float4 d[MTOPK];
+#pragma unroll
+    for (int j = 0; j < MTOPK; j++) a[j] = (mode & 2) ? sp[b * MTOPK + j] : tp[b * MTOPK + j];
+#pragma unroll
     for (int j = 0; j < MTOPK; j++) {
-        int a = (mode & 2) ? sp[b * MTOPK + j] : tp[b * MTOPK + j];
-        float w = (mode & 2) ? tw[b * MTOPK + j] : uw[a];
-        float4 d = *(const float4 *)(down + (size_t)a * MH + c);
-        acc.x = __builtin_fmaf(w, d.x, acc.x); acc.y = __builtin_fmaf(w, d.y, acc.y);
-        acc.z = __builtin_fmaf(w, d.z, acc.z); acc.w = __builtin_fmaf(w, d.w, acc.w);
+        w[j] = (mode & 2) ? tw[b * MTOPK + j] : uw[a[j]];
+        d[j] = *(const float4 *)(down + (size_t)a[j] * MH + c);
+    }
+#pragma unroll
+    for (int j = 0; j < MTOPK; j++) {
+        acc.x = __builtin_fmaf(w[j], d[j].x, acc.x); acc.y = __builtin_fmaf(w[j], d[j].y, acc.y);
+        acc.z = __builtin_fmaf(w[j], d[j].z, acc.z); acc.w = __builtin_fmaf(w[j], d[j].w, acc.w);
     }
     if (mode & 4) { float4 xv = *xp; acc.x = xv.x + acc.x; acc.y = xv.y + acc.y; acc.z = xv.z + acc.z; acc.w = xv.w + acc.w; }
     *xp = acc;
