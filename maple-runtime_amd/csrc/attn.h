@@ -41,10 +41,26 @@ __global__ void __launch_bounds__(256) k_qkn(float *__restrict__ qkv, int pos0, 
     int b = blockIdx.x, t = threadIdx.x, pos = pos0 + b;
     float *row = qkv + (size_t)b * AT_QKV;
     if (t < 16) mx[b * 16 + t] = -1e30f;   // the score maxima k_att_scores raises
-    for (int i = t; i < 20 * AT_HD; i += 256) xs[(i >> 7) * AT_XS + (i & 127)] = row[i];
-    for (int i = t; i < 512; i += 256) {
-        __half h = __float2half_rn(row[2560 + i]);
-        vc[(size_t)pos * 512 + i] = h; ko[(size_t)b * 1024 + 512 + i] = h;
+    // every element a thread ropes has dim t % 128 (elements t + 256 m): its cos / sin pair, loaded up front
+    float rc = 0.0f, rsn = 0.0f;
+    if (!glob && (t & 127) < 64) {
+        float2 cv = *(const float2 *)(cs + ((size_t)pos * 32 + (t & 31)) * 2);
+        rc = cv.x; rsn = cv.y;
+    }
+    {   // all of the thread's loads first (10 q/k values, 2 v values), then the LDS and cache stores
+        float qk[10], vv[2];
+#pragma unroll
+        for (int m = 0; m < 10; m++) qk[m] = row[t + 256 * m];
+#pragma unroll
+        for (int m = 0; m < 2; m++) vv[m] = row[2560 + t + 256 * m];
+#pragma unroll
+        for (int m = 0; m < 10; m++) { int i = t + 256 * m; xs[(i >> 7) * AT_XS + (i & 127)] = qk[m]; }
+#pragma unroll
+        for (int m = 0; m < 2; m++) {
+            int i = t + 256 * m;
+            __half h = __float2half_rn(vv[m]);
+            vc[(size_t)pos * 512 + i] = h; ko[(size_t)b * 1024 + 512 + i] = h;
+        }
     }
     __syncthreads();
     if (t < 20) {
@@ -69,9 +85,8 @@ __global__ void __launch_bounds__(256) k_qkn(float *__restrict__ qkv, int pos0, 
         for (int m = 0; m < 10; m++) {
             int i = t + m * 256, h = i >> 7, d = i & 127;
             if (d >= 64) continue;
-            float c = cs[((size_t)pos * 32 + (d & 31)) * 2], sn = cs[((size_t)pos * 32 + (d & 31)) * 2 + 1];
-            if (d < 32) y[m] = __builtin_fmaf(y[m], c, -(xs[h * AT_XS + d + 32] * sn));
-            else y[m] = __builtin_fmaf(y[m], c, xs[h * AT_XS + d - 32] * sn);
+            if (d < 32) y[m] = __builtin_fmaf(y[m], rc, -(xs[h * AT_XS + d + 32] * rsn));
+            else y[m] = __builtin_fmaf(y[m], rc, xs[h * AT_XS + d - 32] * rsn);
         }
     }
 #pragma unroll
