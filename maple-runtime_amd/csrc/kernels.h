@@ -1227,6 +1227,7 @@ __global__ void __launch_bounds__(256, OCC) k_gateup_pk(const Plan *__restrict__
     static_assert(NCH % CR == 0 && (PA == 1 || PA == 2), "k_gateup_pk pipeline shape");
     __shared__ __attribute__((aligned(16))) int8_t bs[2][BB];
     __shared__ int toks[2][TN];
+    __shared__ __attribute__((aligned(16))) float ssc[2][128];   // ACT: the item's gate and up row scales (epilogue)
     int nitems = plan->ntile_gu * RB;
     int per = (nitems + 7) >> 3, xcd = blockIdx.x & 7, nbx = gridDim.x >> 3;
     int last = min(nitems, (xcd + 1) * per);
@@ -1281,10 +1282,13 @@ __global__ void __launch_bounds__(256, OCC) k_gateup_pk(const Plan *__restrict__
         uint32_t naoff = (uint32_t)(nrowblk + r32) * (MH / 4) + G2 * 32, nboff[NPC];
         int ntk = 0;
         if (has_next && tid < TN) ntk = utok[ntl.p0 + (tid < ntl.n ? tid : 0)];
+        float scv = 0.0f;   // ACT: this thread's row scale, loaded at chunk 0 and stored at chunk 4 (no wait on it)
 #pragma unroll
         for (int ch = 0; ch < NCH; ch++) {
             __syncthreads();
             if (ch == 2 && tid < TN) toks[slot ^ 1][tid] = ntk;     // read after the barrier of chunk 3
+            if (ACT && ch == 0) scv = (tid < 128 ? eptr[cu].gs : eptr[cu].us)[(cur % RB) * 128 + (tid & 127)];
+            if (ACT && ch == 4) ssc[tid >> 7][tid & 127] = scv;   // read by the epilogue after the last barrier
             if (ch == NCH - PA && has_next) {
 #pragma unroll
                 for (int k = 0; k < NPC; k++) nboff[k] = (uint32_t)toks[slot ^ 1][(tid >> 4) + 16 * k] * MH + part * 16;
@@ -1309,7 +1313,6 @@ __global__ void __launch_bounds__(256, OCC) k_gateup_pk(const Plan *__restrict__
         // epilogue, token r32 of each fragment, rows (i/4)*8 + G2*4 + i%4 of the wave's 32. ACT: the activation
         // SiLU(min(G,7)) * clamp(U,-7,7) with G = (float)(sum - qsum) * qs * s_gate[row] (maple.c:471-479,
         // 825-829), fp32 into out[pair][512]; else the raw int32 sums into out[pair][1024] (gate, then up).
-        const float *gsb = ACT ? eptr[cu].gs : nullptr, *usb = ACT ? eptr[cu].us : nullptr;
 #pragma unroll
         for (int j = 0; j < NF; j++) {
             int tk = j * 32 + r32;
@@ -1322,7 +1325,7 @@ __global__ void __launch_bounds__(256, OCC) k_gateup_pk(const Plan *__restrict__
                 for (int g = 0; g < 4; g++) {
                     int row0 = rowblk + g * 8 + G2 * 4;
                     if (ACT) {
-                        float4 sg = *(const float4 *)(gsb + row0), su = *(const float4 *)(usb + row0);
+                        float4 sg = *(const float4 *)(&ssc[0][row0 - (cur % RB) * 128]), su = *(const float4 *)(&ssc[1][row0 - (cur % RB) * 128]);
                         float sgv[4] = {sg.x, sg.y, sg.z, sg.w}, suv[4] = {su.x, su.y, su.z, su.w}, o[4];
 #pragma unroll
                         for (int i = 0; i < 4; i++) {
