@@ -221,7 +221,8 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     ExpPtr ex = tab[R.ue[u]];
     const gptr_u4 *cp = (const gptr_u4 *)((kind ? ex.uc : ex.gc) + (size_t)row * (MH / 4) + grp * 32);
     v4i c0 = cp[0], c1 = cp[1];
-    float srow = t < 16 ? (t < 8 ? ex.gs[r0 + t] : ex.us[r0 + t - 8]) : 0.0f;   // row scales, loaded with the codes
+    float srow = 0.0f;   // row scales, loaded with the codes (one load per thread: no wait between two)
+    if (t < 16) srow = *(const __attribute__((address_space(1))) float *)(t < 8 ? ex.gs + r0 + t : ex.us + r0 + t - 8);
     uint32_t cd[32];
     uint32_t cwd[8] = {(uint32_t)c0.x, (uint32_t)c0.y, (uint32_t)c0.z, (uint32_t)c0.w, (uint32_t)c1.x, (uint32_t)c1.y, (uint32_t)c1.z, (uint32_t)c1.w};
 #pragma unroll
