@@ -1683,6 +1683,10 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
     };
 #pragma unroll
     for (int g = 0; g < RING - 1; g++) load_group(g, cw[g]);
+    // the expert's row scales into registers now, behind the first code loads (stored to LDS with the tile)
+    static_assert(NT == 2 * MFF && NT >= MH / 4, "k_expert16 scale staging: one gate or up scale and one down float4 per thread");
+    const float scg = tid < MFF ? ex.gs[tid] : ex.us[tid - MFF];
+    const float4 scd = tid < MH / 4 ? *(const float4 *)(ex.ds + tid * 4) : make_float4(0.f, 0.f, 0.f, 0.f);
     if (first_tile) {   // the grouping, with the expert's first code loads in flight
         group_scan();
         int cnt = gc[ge];
@@ -1720,15 +1724,22 @@ __global__ void __launch_bounds__(WAVES * 64) k_expert16(const Plan *__restrict_
         tqs[tid] = tk >= 0 ? (GR ? gqs[tk] : qsx[tk]) : 0.0f;
         tqsum[tid] = tk >= 0 ? (GR ? gqsum[tk] : qsumx[tk]) : 0;
     }
-    for (int i = tid; i < MFF; i += NT) { sg[i] = ex.gs[i]; su[i] = ex.us[i]; }
-    for (int i = tid; i < MH / 4; i += NT) *(float4 *)(sd + i * 4) = *(const float4 *)(ex.ds + i * 4);
+    if (tid < MFF) sg[tid] = scg; else su[tid - MFF] = scg;
+    if (tid < MH / 4) *(float4 *)(sd + tid * 4) = scd;
     __syncthreads();
+    {   // 128 parts of 16 bytes per row; every load issued before the first store (padding rows read row 0)
+        constexpr int NK = 16 * 128 / NT;
+        v4i v[NK];
 #pragma unroll
-    for (int k = 0; k < 16 * 128 / NT; k++) {
-        int i = tid + NT * k, tk = i >> 7, part = i & 127;      // 128 parts of 16 bytes per row
-        int src = toks[tk];
-        v4i v = src >= 0 ? *(const gptr_u4 *)(qx + (size_t)src * MH + part * 16) : v4i{0, 0, 0, 0};
-        *(v4i *)(xs + tk * MH + (part >> 4) * 256 + (((part & 15) ^ tk) * 16)) = v;
+        for (int k = 0; k < NK; k++) {
+            int i = tid + NT * k, tk = i >> 7, part = i & 127, src = toks[tk];
+            v[k] = *(const gptr_u4 *)(qx + (size_t)(src >= 0 ? src : 0) * MH + part * 16);
+        }
+#pragma unroll
+        for (int k = 0; k < NK; k++) {
+            int i = tid + NT * k, tk = i >> 7, part = i & 127;
+            *(v4i *)(xs + tk * MH + (part >> 4) * 256 + (((part & 15) ^ tk) * 16)) = toks[tk] >= 0 ? v[k] : v4i{0, 0, 0, 0};
+        }
     }
     __syncthreads();
 
