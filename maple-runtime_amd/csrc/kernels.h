@@ -26,6 +26,8 @@
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(1))) v4i gptr_u4;   // global-memory 16 bytes (global_load, not flat_load)
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) v4f gptr_f4;      // global-memory 4 floats
 
 struct ExpPtr {  // one expert's six tensors (maple.c:276-277 GLOC order: gate codes/scales, up, down)
     const uint8_t *gc; const float *gs;
@@ -2099,13 +2101,16 @@ __global__ void __launch_bounds__(256) k_combine16(const int16_t *__restrict__ d
 #pragma unroll
     for (int jg = 0; jg < MTOPK; jg += 4) {
         uint4 dv[4];
-        float4 s0[4], s1[4];
+        v4f s0[4], s1[4];
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) {
-            dv[jj] = *(const uint4 *)(down + (size_t)sa[jg + jj] * MH + c);
-            const float *ds = sds[jg + jj] + c;
-            s0[jj] = *(const float4 *)ds; s1[jj] = *(const float4 *)(ds + 4);
+            // global (not generic) loads: a generic load also counts in the LDS counter, so the wait for the next
+            // pointer read from LDS would wait for it too and serialise the four rows
+            const gptr_f4 *ds = (const gptr_f4 *)(sds[jg + jj] + c);
+            s0[jj] = ds[0]; s1[jj] = ds[1];
         }
+#pragma unroll
+        for (int jj = 0; jj < 4; jj++) dv[jj] = *(const uint4 *)(down + (size_t)sa[jg + jj] * MH + c);
         bool ovf = false;   // any -32768 marker (its d is in dov): rare, handled by a compact loop
 #pragma unroll
         for (int jj = 0; jj < 4; jj++) {
@@ -2113,33 +2118,24 @@ __global__ void __launch_bounds__(256) k_combine16(const int16_t *__restrict__ d
 #pragma unroll
             for (int k = 0; k < 4; k++) ovf |= ((w4[k] & 0xffffu) == 0x8000u) | ((w4[k] >> 16) == 0x8000u);
         }
-        if (!ovf) {
+        // one path for both cases (the scale rows are used unconditionally, so their loads stay with the int16
+        // loads); an entry marked -32768 takes its int32 value from dov (rare)
 #pragma unroll
-            for (int jj = 0; jj < 4; jj++) {
-                int j = jg + jj;
-                float sdv[8] = {s0[jj].x, s0[jj].y, s0[jj].z, s0[jj].w, s1[jj].x, s1[jj].y, s1[jj].z, s1[jj].w};
-                uint32_t wd[4] = {dv[jj].x, dv[jj].y, dv[jj].z, dv[jj].w};
-                float qs = sq[j], wgt = sw[j];
+        for (int jj = 0; jj < 4; jj++) {
+            int j = jg + jj;
+            float sdv[8] = {s0[jj].x, s0[jj].y, s0[jj].z, s0[jj].w, s1[jj].x, s1[jj].y, s1[jj].z, s1[jj].w};
+            uint32_t wd[4] = {dv[jj].x, dv[jj].y, dv[jj].z, dv[jj].w};
+            int d[8];
 #pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    int d = (int16_t)(wd[i >> 1] >> (16 * (i & 1)));
-                    acc[i] = __builtin_fmaf(wgt, (float)d * qs * sdv[i], acc[i]);
-                }
-            }
-        } else {   // the same operations in the same order, reading the int16 and scale values again
+            for (int i = 0; i < 8; i++) d[i] = (int16_t)(wd[i >> 1] >> (16 * (i & 1)));
+            if (ovf) {
 #pragma unroll 1
-            for (int jj = 0; jj < 4; jj++) {
-                int j = jg + jj;
-                const int16_t *dr = down + (size_t)sa[j] * MH + c;
-                const float *ds = sds[j] + c;
-                float qs = sq[j], wgt = sw[j];
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    int d = dr[i];
-                    if (d == -32768) d = dov[(size_t)sa[j] * MH + c + i];
-                    acc[i] = __builtin_fmaf(wgt, (float)d * qs * ds[i], acc[i]);
-                }
+                for (int i = 0; i < 8; i++)
+                    if (d[i] == -32768) d[i] = dov[(size_t)sa[j] * MH + c + i];
             }
+            float qs = sq[j], wgt = sw[j];
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[i] = __builtin_fmaf(wgt, (float)d[i] * qs * sdv[i], acc[i]);
         }
         __builtin_amdgcn_sched_barrier(0);
     }
