@@ -222,7 +222,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     const gptr_u4 *cp = (const gptr_u4 *)((kind ? ex.uc : ex.gc) + (size_t)row * (MH / 4) + grp * 32);
     v4i c0 = cp[0], c1 = cp[1];
     float srow = 0.0f;   // row scales, loaded with the codes (one load per thread: no wait between two)
-    if (t < 16) srow = *(const __attribute__((address_space(1))) float *)(t < 8 ? ex.gs + r0 + t : ex.us + r0 + t - 8);
+    if (t < 16) srow = *(const gptr_f *)(t < 8 ? ex.gs + r0 + t : ex.us + r0 + t - 8);
     uint32_t cd[32];
     uint32_t cwd[8] = {(uint32_t)c0.x, (uint32_t)c0.y, (uint32_t)c0.z, (uint32_t)c0.w, (uint32_t)c1.x, (uint32_t)c1.y, (uint32_t)c1.z, (uint32_t)c1.w};
 #pragma unroll
@@ -312,13 +312,13 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
         const uint8_t *dc = eptr[wvu + 4 * k].dc; const float *ds = eptr[wvu + 4 * k].ds;
         bool live = wvu + 4 * k < nu;
         dc = live ? dc : dc0; ds = live ? ds : ds0;
-        cv[k] = *(const gptr_u4 *)(dc + (size_t)row * (MFF / 4) + sl * 16); sd[k] = ds[row];
+        cv[k] = *(const gptr_u4 *)(dc + (size_t)row * (MFF / 4) + sl * 16); sd[k] = *(const gptr_f *)(ds + row);
     }
 #pragma unroll
     for (int k = 2; k < DEC_DU; k++)
         if (wvu + 4 * k < nu) {
             const ExpPtr &ep = eptr[wvu + 4 * k];
-            cv[k] = *(const gptr_u4 *)(ep.dc + (size_t)row * (MFF / 4) + sl * 16); sd[k] = ep.ds[row];
+            cv[k] = *(const gptr_u4 *)(ep.dc + (size_t)row * (MFF / 4) + sl * 16); sd[k] = *(const gptr_f *)(ep.ds + row);
         }
     for (int k = 0; k < nb; k++) {
         int a = 8 * k + 2 * wv + (l >> 5);

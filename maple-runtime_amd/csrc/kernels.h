@@ -27,7 +27,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(1))) v4i gptr_u4;   // global-memory 16 bytes (global_load, not flat_load)
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(1))) v4f gptr_f4;      // global-memory 4 floats
+typedef __attribute__((address_space(1))) v4f gptr_f4;
+typedef __attribute__((address_space(1))) float gptr_f;      // global-memory float
 
 struct ExpPtr {  // one expert's six tensors (maple.c:276-277 GLOC order: gate codes/scales, up, down)
     const uint8_t *gc; const float *gs;
@@ -1422,24 +1423,34 @@ __global__ void __launch_bounds__(WAVES * 64) k_dense(const DenseMat *__restrict
         }
     }
 #undef DN2_LOADC
-    // token t0 + j*32 + r32; rows row0 + f*32 + (i/4)*8 + G2*4 + i%4
+    // token t0 + j*32 + r32; rows row0 + f*32 + (i/4)*8 + G2*4 + i%4. The row scales and both tokens' factors
+    // are loaded together, through global-memory pointers, before the first use
+    v4f sc8[2][4]; float qs2[2]; int qsum2[2];
+#pragma unroll
+    for (int f = 0; f < 2; f++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) sc8[f][g] = *(const gptr_f4 *)(M.scales + row0 + f * 32 + g * 8 + G2 * 4);
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        int b = t0 + min(j * 32 + r32, ntok - 1);
+        qs2[j] = *(const gptr_f *)(qsx + b); qsum2[j] = *(const __attribute__((address_space(1))) int *)(qsumx + b);
+    }
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         int tk = j * 32 + r32;
         if (tk >= ntok) continue;
         int b = t0 + tk;
-        float qs = qsx[b]; int qsum = qsumx[b];
+        float qs = qs2[j]; int qsum = qsum2[j];
 #pragma unroll
         for (int f = 0; f < 2; f++)
 #pragma unroll
             for (int g = 0; g < 4; g++) {
                 int r = row0 + f * 32 + g * 8 + G2 * 4;
-                float4 sc = *(const float4 *)(M.scales + r);
-                float sv[4] = {sc.x, sc.y, sc.z, sc.w}, o[4];
+                float sv[4] = {sc8[f][g].x, sc8[f][g].y, sc8[f][g].z, sc8[f][g].w}, o[4];
 #pragma unroll
                 for (int i = 0; i < 4; i++) o[i] = (float)(acc[f][j][g * 4 + i] - qsum) * qs * sv[i];
                 float4 *yp = (float4 *)(y + (size_t)b * ys + M.yoff + r);
-                if (ACC) { float4 yv = *yp; o[0] = yv.x + o[0]; o[1] = yv.y + o[1]; o[2] = yv.z + o[2]; o[3] = yv.w + o[3]; }
+                if (ACC) { v4f yv = *(const gptr_f4 *)yp; o[0] = yv.x + o[0]; o[1] = yv.y + o[1]; o[2] = yv.z + o[2]; o[3] = yv.w + o[3]; }
                 *yp = make_float4(o[0], o[1], o[2], o[3]);
             }
     }
