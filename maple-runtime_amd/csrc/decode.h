@@ -182,7 +182,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
                                                     ExpPtr *__restrict__ eptr, int8_t *__restrict__ qx, float *__restrict__ qsx,
                                                     int *__restrict__ qsumx, float *__restrict__ act, int *__restrict__ dbg) {
     __shared__ DecRoute R;
-    __shared__ float E[4][MNE];
+    __shared__ __attribute__((aligned(16))) float E[4][MNE];
     __shared__ __attribute__((aligned(16))) int8_t qs_l[DEC_MAXTOK][MH / 128 * DEC_GS];
     __shared__ float qsv_l[DEC_MAXTOK];
     __shared__ int qsum_l[DEC_MAXTOK];

@@ -510,27 +510,28 @@ __global__ void __launch_bounds__(256) k_router_l1max(const uint16_t *__restrict
 }
 
 // =====================================================================================================
-// Softmax + top-8 + renormalisation, maple.c:910-923. One wave per token; lane l holds experts l, l+64,
-// l+128, l+192. Probabilities: p_e = exp(l_e - max) / sum, the sum taken as 8 interleaved partial sums
+// Softmax + top-8 + renormalisation, maple.c:910-923. One wave per token; lane l holds experts 4l .. 4l+3.
+// Probabilities: p_e = exp(l_e - max) / sum, the sum taken as 8 interleaved partial sums
 // (lane j: experts j, j+8, ... in order) folded by hsum8 -- the same order the oracle uses. Top-8: 8 rounds
 // of argmax on p with the lowest index winning ties (maple.c's strict >), picked entries set to -1; weights
 // p / (sum of picked, in pick order, + 1e-20). Also writes slot -> expert (top) and weight (tw).
 // =====================================================================================================
-// One wave, one token: rl_row[256] -> top[8], tw[8] (written by lane 0). E = 256 floats of LDS scratch.
-// One wave, one token: rl_row[256] -> top[8], tw[8] (and lane l returns the expert of slot l % 8).
-// E = 256 floats of LDS scratch. Selection: p >= 0, so key = p_bits + 1 orders like p, and 0 marks a picked expert. Each of the 8 rounds
-// takes the largest key (lane-local over 4, DPP within 16-lane rows, the 4 row results as scalars), then the
-// lowest expert index holding it (ballots in index order: e = l + 64 i), which is the pick order of maple.c's
+// One wave, one token: rl_row[256] -> top[8], tw[8] (written by lane 0); lane l returns the expert of slot
+// l % 8. E = 256 floats of LDS scratch. Lane l holds experts 4l .. 4l+3. Selection: p >= 0 and p <= 1, so
+// key = (p_bits + 1) << 2 | (3 - slot) fits 32 bits, orders like p and, within a lane, puts the lower expert
+// first among equal p; a picked expert gets key 0. Each of the 8 rounds takes the largest key (lane-local
+// over 4, DPP within 16-lane rows, the 4 row results as scalars); the lowest lane whose best key has that p
+// holds the lowest expert index with it, and that lane's best key names it: the pick order of maple.c's
 // repeated strict-> scans, ties included.
-__device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
-    float lg[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) lg[i] = r[l + 64 * i];
+// topk_wave_v takes the lane's 4 logits; topk_wave loads them from a row in global memory.
+__device__ __forceinline__ int topk_wave_v(float4 lv, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
+    float lg[4] = {lv.x, lv.y, lv.z, lv.w};
     float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
     mx = wave_max(mx);
     mx = fmaxf(mx, -1e30f);  // maple.c starts its max at -1e30
 #pragma unroll
-    for (int i = 0; i < 4; i++) { lg[i] = dexp(lg[i] - mx); E[l + 64 * i] = lg[i]; }
+    for (int i = 0; i < 4; i++) lg[i] = dexp(lg[i] - mx);
+    *(float4 *)(E + 4 * l) = make_float4(lg[0], lg[1], lg[2], lg[3]);
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     float part = 0.0f;
@@ -547,25 +548,29 @@ __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, 
     float sum = hsum8(pv);
     uint32_t key[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) key[i] = __float_as_uint(lg[i] / sum) + 1u;
+    for (int i = 0; i < 4; i++) key[i] = ((__float_as_uint(lg[i] / sum) + 1u) << 2) | (uint32_t)(3 - i);
     float pk[MTOPK]; int ek[MTOPK];
     float tsum = 0.0f;
 #pragma unroll
     for (int k = 0; k < MTOPK; k++) {
         uint32_t b = max(max(key[0], key[1]), max(key[2], key[3]));
+        uint32_t lb = b;
         b = max(b, (uint32_t)dpp<0xB1>((int)b));
         b = max(b, (uint32_t)dpp<0x4E>((int)b));
         b = max(b, (uint32_t)dpp<0x141>((int)b));
         b = max(b, (uint32_t)dpp<0x140>((int)b));
         uint32_t m = max(max((uint32_t)__builtin_amdgcn_readlane((int)b, 0), (uint32_t)__builtin_amdgcn_readlane((int)b, 16)),
                          max((uint32_t)__builtin_amdgcn_readlane((int)b, 32), (uint32_t)__builtin_amdgcn_readlane((int)b, 48)));
-        unsigned long long m0 = __ballot(key[0] == m), m1 = __ballot(key[1] == m), m2 = __ballot(key[2] == m), m3 = __ballot(key[3] == m);
-        int e = m0 ? __ffsll((long long)m0) - 1 : m1 ? 64 + __ffsll((long long)m1) - 1 : m2 ? 128 + __ffsll((long long)m2) - 1 : 192 + __ffsll((long long)m3) - 1;
-        pk[k] = __uint_as_float(m - 1u); ek[k] = e;
+        // the lowest lane whose best p equals the largest p holds the lowest expert with it; its own best key
+        // (the lowest of its slots with that p) names the expert
+        int L = __ffsll((long long)__ballot((lb >> 2) == (m >> 2))) - 1;
+        uint32_t mL = (uint32_t)__builtin_amdgcn_readlane((int)lb, L);
+        int e = 4 * L + 3 - (int)(mL & 3u);
+        pk[k] = __uint_as_float((m >> 2) - 1u); ek[k] = e;
         tsum = tsum + pk[k];
-        if (l == (e & 63)) {
-            int i = e >> 6;
-            key[0] = i == 0 ? 0u : key[0]; key[1] = i == 1 ? 0u : key[1]; key[2] = i == 2 ? 0u : key[2]; key[3] = i == 3 ? 0u : key[3];
+        if (l == L) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) key[i] = key[i] == mL ? 0u : key[i];
         }
     }
     if (l == 0) {
@@ -576,6 +581,10 @@ __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, 
 #pragma unroll
     for (int k = 0; k < MTOPK; k++) mine = (l & (MTOPK - 1)) == k ? ek[k] : mine;
     return mine;
+}
+__device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
+    v4f lv = *(const gptr_f4 *)(r + 4 * l);
+    return topk_wave_v(make_float4(lv.x, lv.y, lv.z, lv.w), E, l, top, tw);
 }
 
 // Top-8 and the int8 quantisation of the MoE input (maple.c:909-923 and 908 prep) of 4 tokens per block,
@@ -760,7 +769,7 @@ __global__ void __launch_bounds__(256) k_quant(const float *__restrict__ x, int 
 __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl, const float *__restrict__ hn, int nb,
                                                     int *__restrict__ top, float *__restrict__ tw, int8_t *__restrict__ qx,
                                                     float *__restrict__ qsx, int *__restrict__ qsumx, int *__restrict__ hist) {
-    __shared__ float E[4][MNE];
+    __shared__ __attribute__((aligned(16))) float E[4][MNE];
     int wv = threadIdx.x >> 6, l = threadIdx.x & 63;
     int b = blockIdx.x * 4 + wv;
     if (b >= nb) return;  // whole wave exits together
@@ -798,7 +807,8 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
                                                      int *__restrict__ top, float *__restrict__ tw, int *__restrict__ hist,
                                                      int8_t *__restrict__ qx, float *__restrict__ qsx, int *__restrict__ qsumx) {
     __shared__ __attribute__((aligned(16))) float hsc[4][8 * RT_HP];
-    __shared__ float row[4][MNE], E[4][MNE];
+    __shared__ __attribute__((aligned(16))) float row[4][MNE];
+    __shared__ __attribute__((aligned(16))) float E[4][MNE];
     __shared__ int cand[4][MNE];
     int wv = threadIdx.x >> 6, l = threadIdx.x & 63, b = blockIdx.x * 4 + wv;
     if (b >= nb) return;   // whole wave; no block-wide barrier below
@@ -894,7 +904,7 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
     __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
 #pragma unroll
     for (int i = 0; i < 4; i++) rl[(size_t)b * MNE + l + 64 * i] = row[wv][l + 64 * i];
-    int ek = topk_wave(&row[wv][0], E[wv], l, top + b * MTOPK, tw + b * MTOPK);
+    int ek = topk_wave_v(*(const float4 *)(&row[wv][4 * l]), E[wv], l, top + b * MTOPK, tw + b * MTOPK);
     if (hist && l < MTOPK) atomicAdd(&hist[(b >> 6) * MNE + ek], 1);   // per-chunk expert counts for k_group
 }
 
