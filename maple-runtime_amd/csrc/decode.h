@@ -201,8 +201,27 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     }
     { v4i *tp4 = (v4i *)(tab + t); tp4[0] = my0; tp4[1] = my1; tp4[2] = my2; }
     __syncthreads();
-    dec_group_block(nb, R);
     int u = blockIdx.y;
+    int kind = wv >> 1, rr = (wv & 1) * 4 + (l >> 4), grp = l & 15;
+    int r0 = blockIdx.x * 8, row = r0 + rr;
+    v4i c0, c1;
+    float srow = 0.0f;   // row scales, loaded with the codes (one load per thread: no wait between two)
+    // the block's gate/up codes: for one token the used experts are its 8 picks ascending, so slot u's expert
+    // is known before the grouping and its loads are in flight meanwhile; for more tokens after it
+    auto load_codes = [&](int e) {
+        const ExpPtr &ex = tab[e];
+        const gptr_u4 *cp = (const gptr_u4 *)((kind ? ex.uc : ex.gc) + (size_t)row * (MH / 4) + grp * 32);
+        c0 = cp[0]; c1 = cp[1];
+        if (t < 16) srow = *(const gptr_f *)(t < 8 ? ex.gs + r0 + t : ex.us + r0 + t - 8);
+    };
+    if (nb == 1) {
+        int tv = l < MTOPK ? R.top[l] : 0x7fffffff, rank = 0;
+#pragma unroll
+        for (int j = 0; j < MTOPK; j++) rank += R.top[j] < tv;
+        int src = max(__ffsll((long long)__ballot(l < MTOPK && rank == u)) - 1, 0);   // ranks 0..7 are distinct
+        load_codes(__builtin_amdgcn_readlane(tv, src));
+    }
+    dec_group_block(nb, R);
     bool pub = blockIdx.x == 0 && blockIdx.y == 0;
     if (u >= R.nu && !pub) return;                    // whole block
     if (pub) {
@@ -216,13 +235,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
         }
         if (u >= R.nu) return;
     }
-    int kind = wv >> 1, rr = (wv & 1) * 4 + (l >> 4), grp = l & 15;
-    int r0 = blockIdx.x * 8, row = r0 + rr;
-    ExpPtr ex = tab[R.ue[u]];
-    const gptr_u4 *cp = (const gptr_u4 *)((kind ? ex.uc : ex.gc) + (size_t)row * (MH / 4) + grp * 32);
-    v4i c0 = cp[0], c1 = cp[1];
-    float srow = 0.0f;   // row scales, loaded with the codes (one load per thread: no wait between two)
-    if (t < 16) srow = *(const gptr_f *)(t < 8 ? ex.gs + r0 + t : ex.us + r0 + t - 8);
+    if (nb != 1) load_codes(R.ue[u]);
     uint32_t cd[32];
     uint32_t cwd[8] = {(uint32_t)c0.x, (uint32_t)c0.y, (uint32_t)c0.z, (uint32_t)c0.w, (uint32_t)c1.x, (uint32_t)c1.y, (uint32_t)c1.z, (uint32_t)c1.w};
 #pragma unroll
