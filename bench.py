@@ -13,6 +13,7 @@ cpu_baseline: maple.c's own int8 AVX2 path (oracle/_ref, built from the referenc
 import argparse
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -88,14 +89,33 @@ def timed(fn, steps, warmup):
     return ev_ms / steps, (t1 - t0) * 1e3 / steps
 
 
-def cpu_model():
+def cpu_topology():
+    """lscpu's model name and physical core count of the host, and the cores this process may run on (its
+    affinity mask: the box's CPU share). Falls back to /proc/cpuinfo when lscpu is absent."""
+    info = {}
     try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
-    except OSError:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            k, _, v = line.partition(":")
+            info[k.strip()] = v.strip()
+    except (OSError, subprocess.SubprocessError):
         pass
-    return "unknown"
+    model = info.get("Model name")
+    if not model:
+        model = "unknown"
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    try:
+        phys = int(info["Socket(s)"]) * int(info["Core(s) per socket"])
+    except (KeyError, ValueError):
+        phys = None
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return model, phys, usable
 
 
 def cpu_baselines(blocks, routers, seconds):
@@ -147,7 +167,11 @@ def cpu_baselines(blocks, routers, seconds):
         return n, units * n / (time.perf_counter() - t0)
 
     res = {}
-    nt_all = min(os.cpu_count() or 1, 16)
+    model, phys, usable = cpu_topology()
+    # every core this process may use (the affinity mask), at most the host's physical cores (maple.c runs one
+    # thread per core) and at most the thread budget the environment sets (OMP_NUM_THREADS on the GPU boxes)
+    budget = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    nt_all = min(x for x in (usable, phys, budget or None) if x)
     for nt in (1, nt_all):
         if nt > 1:
             nt = R.ref_set_threads(nt)
@@ -156,11 +180,11 @@ def cpu_baselines(blocks, routers, seconds):
         p2_n, p2_v = rate(lambda: prefill(2048), 2048, 0.0)
         res[nt] = dict(decode=(d_n, d_v), p128=(p1_n, p1_v), p2048=(p2_n, p2_v))
         log(f"cpu baseline, {nt} thread(s): decode {d_v:.1f} tok/s, prefill-128 {p1_v:.0f} tok/s, prefill-2048 {p2_v:.0f} tok/s")
-    model = cpu_model()
     flags = "-O3 -ffast-math -mavx2 -mfma -mf16c"
     r1, ra = res[1], res[max(res)]
     return dict(value=round(ra["decode"][1], 2), unit="tokens/s", cores=max(res), kind="reference",
-                cpu=model, value_1_thread=round(r1["decode"][1], 2),
+                cpu=model, host_physical_cores=phys, cores_usable=usable, thread_budget=budget or None,
+                value_1_thread=round(r1["decode"][1], 2),
                 sample=f"{ra['decode'][0]} decode tokens x 24 layers through maple.c's step() MoE block (int8, {flags}, "
                        f"{max(res)} threads of run()), same synthetic weights; {r1['decode'][0]} tokens on 1 thread",
                 prefill=dict(workload="maple.c step_batch MoE block (maple.c:733-834), one layer, layer-0 experts",
@@ -317,25 +341,27 @@ def main():
         lib.mmoe_d2d(d_x, tok(i), M.H * 4)
         M.check(lib.mmoe_stack_graph(0, NL, d_x, 1, M.ORDER_STEP, 1), "graph")
     step = step_graph if args.graph else step_plain
-    if args.no_decode:
-        step = lambda i: None
-    warm_ms, _ = timed(lambda i: step(0), max(5, args.steps // 2), args.warmup)
-    ms, wall_ms = timed(step, args.steps, args.warmup)
-    tok_s = 1e3 / ms
     bytes_tok = NL * 8 * CODES_SCALES_PER_EXPERT
-    log(f"decode: {ms * 1e3:.1f} us/token (wall {wall_ms * 1e3:.1f} us), {tok_s:.0f} tok/s, "
-        f"{bytes_tok / ms / 1e6:.0f} GB/s on codes+scales over the whole step; one token repeated: {warm_ms * 1e3:.1f} us")
-    kt = prof_pass(step_plain, 2 * NX) if not args.no_decode else {"gateup": (1.0, 1)}
-    for k, (tot, n) in sorted(kt.items(), key=lambda kv: -kv[1][0]):
-        log(f"  {k:10s} {tot / n * 1e3:8.2f} us avg x {n}")
-    gu_us = kt["gateup"][0] / kt["gateup"][1] * 1e3
     gu_bytes = 8 * GU_BYTES_PER_EXPERT
-    roof = dict(bound="hbm", kernel="k_dec_gateup (decode, 8 experts x 1024 rows)", achieved=round(gu_bytes / gu_us / 1e3, 1),
-                peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS, 4),
-                traffic=pmc_traffic("k_dec_gateup"), algorithmic_bytes_per_launch=gu_bytes, avg_launch_us=round(gu_us, 2),
-                timing=f"device execution of each of its {kt['gateup'][1]} launches in 24-layer steps over {NX} distinct "
-                       "tokens (events on the dispatch, as rocprofv3)",
-                step_gbs=round(bytes_tok / ms / 1e6, 1), step_frac=round(bytes_tok / ms / 1e6 / HBM_PEAK_GBS, 4))
+    if args.no_decode:   # development runs: no decode timing, no headline figures
+        ms = wall_ms = tok_s = None
+        kt, roof = {}, None
+    else:
+        warm_ms, _ = timed(lambda i: step(0), max(5, args.steps // 2), args.warmup)
+        ms, wall_ms = timed(step, args.steps, args.warmup)
+        tok_s = 1e3 / ms
+        log(f"decode: {ms * 1e3:.1f} us/token (wall {wall_ms * 1e3:.1f} us), {tok_s:.0f} tok/s, "
+            f"{bytes_tok / ms / 1e6:.0f} GB/s on codes+scales over the whole step; one token repeated: {warm_ms * 1e3:.1f} us")
+        kt = prof_pass(step_plain, 2 * NX)
+        for k, (tot, n) in sorted(kt.items(), key=lambda kv: -kv[1][0]):
+            log(f"  {k:10s} {tot / n * 1e3:8.2f} us avg x {n}")
+        gu_us = kt["gateup"][0] / kt["gateup"][1] * 1e3
+        roof = dict(bound="hbm", kernel="k_dec_gateup (decode, 8 experts x 1024 rows)", achieved=round(gu_bytes / gu_us / 1e3, 1),
+                    peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gu_bytes / gu_us / 1e3 / HBM_PEAK_GBS, 4),
+                    traffic=pmc_traffic("k_dec_gateup"), algorithmic_bytes_per_launch=gu_bytes, avg_launch_us=round(gu_us, 2),
+                    timing=f"device execution of each of its {kt['gateup'][1]} launches in 24-layer steps over {NX} distinct "
+                           "tokens (events on the dispatch, as rocprofv3)",
+                    step_gbs=round(bytes_tok / ms / 1e6, 1), step_frac=round(bytes_tok / ms / 1e6 / HBM_PEAK_GBS, 4))
 
     # ---- config 2: 2048-token prefill, one layer, Zipf(1.1)-skewed routing. Steps rotate over 4 layers with
     # different experts (4 x 204 MB, more than the 256 MB last-level cache holds)
@@ -440,8 +466,9 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baselines(blocks, routers, args.cpu_seconds)
 
-    out = {"metric": METRIC, "value": round(tok_s, 1),
-           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+    rnd = lambda v, k: None if v is None else round(v, k)
+    out = {"metric": METRIC, "value": rnd(tok_s, 1),
+           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": rnd(ms, 5),
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8xternary->int32, fp32",
            "data": "synthetic (seeded Maple-shaped ternary experts, uniform router, N(0,1) hidden)",
            "config": {"workload": "config 1: decode 1 token x 24 stacked MoE layers (d=2048, 256 experts, top-8, FF=512)",

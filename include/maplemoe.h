@@ -217,9 +217,6 @@ void *mmoe_stream(void);
 #define MMOE_K_ATT_PV 13
 #define MMOE_PROF_NKERNELS 14
 int mmoe_event_record(int slot);
-/* Re-launch one stage (MMOE_K_GATEUP, _DOWN, _QUANT_ACT, _ROUTER) of the last main-context call reps times
- * back to back between two events; returns average ms per launch, or -1.0. */
-double mmoe_bench_stage(int kid, int reps);
 double mmoe_event_elapsed_ms(void);
 int mmoe_prof(int on);
 int mmoe_prof_reset(void);
@@ -250,13 +247,5 @@ int mmoe_ckpt_load(int L0, int nl);
  * against g / (1 + exp(-g)) with IEEE division, bit for bit, over the fp32 bit patterns [lo, lo + n).
  * *nbad = number of mismatches, *first = smallest mismatching pattern (0xffffffff if none). */
 int mmoe_selftest_silu(uint32_t lo, uint32_t n, unsigned long long *nbad, uint32_t *first);
-
-/* Synthetic Maple-shaped data in the reference layout (see csrc/synth.c) */
-void mmoe_synth_expert(uint64_t seed, int L, int e, uint8_t *gc, float *gs, uint8_t *uc, float *us, uint8_t *dc, float *ds);
-size_t mmoe_synth_expert_bytes(void);
-void mmoe_synth_layer(uint64_t seed, int L, uint8_t *base, int nthreads);
-void mmoe_synth_router(uint64_t seed, int L, int dist, uint16_t *w);
-void mmoe_synth_hidden(uint64_t seed, int sid, int nb, float *x);
-void mmoe_synth_zipf_bias(uint64_t seed, double s, float *bias);
 
 #endif

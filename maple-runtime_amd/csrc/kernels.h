@@ -851,7 +851,11 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
         int e = m0 ? __ffsll((long long)m0) - 1 : m1 ? 64 + __ffsll((long long)m1) - 1 : m2 ? 128 + __ffsll((long long)m2) - 1 : 192 + __ffsll((long long)m3) - 1;
         if (l == (e & 63)) { int i = e >> 6; rem[0] = i == 0 ? -INFINITY : rem[0]; rem[1] = i == 1 ? -INFINITY : rem[1]; rem[2] = i == 2 ? -INFINITY : rem[2]; rem[3] = i == 3 ? -INFINITY : rem[3]; }
     }
-    float thr = a8 - 2.0f * (RG_ERRK * hm * w1max[0]);
+    // the bias add rounds relative to |logit + bias| on both sides (MFMA sum and exact chain): with a bias much
+    // larger than sum|w h| that error is not covered by RG_ERRK's term, so add 2^-24 (|bias| + sum|w h|) per side
+    float bm = wave_max(fmaxf(fmaxf(fabsf(bb[0]), fabsf(bb[1])), fmaxf(fabsf(bb[2]), fabsf(bb[3]))));
+    float sw = hm * w1max[0];
+    float thr = a8 - 2.0f * (RG_ERRK * sw + (2.0f / 16777216.0f) * (bm + 1.01f * sw));
     int nc = 0;
     unsigned long long lanemask = (1ull << l) - 1ull;
 #pragma unroll

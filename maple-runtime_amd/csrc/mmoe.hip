@@ -29,10 +29,12 @@
 #define DN16_W 4    // small-tile down: waves per workgroup, 16-row fragments per wave
 #define DN16_RF 2
 #endif
-#ifndef DN_RPB
+#ifndef E16_W
 #define E16_W 16   // fused small-tile expert kernel: waves per workgroup, code groups in the register ring
 #define E16_RING 3
 #define E16_GL 4     // 16-byte code loads per lane in one ring group
+#endif
+#ifndef DN_RPB
 #define DN_RPB 2   // down row blocks of 256 per workgroup
 #endif
 
@@ -277,7 +279,6 @@ static int stage_quant_x(Work &w, const float *d_hn, int nb) {
 }
 
 // gate/up (+SiLU), act quantisation, down for np pairs under w.plan / w.eptr / w.utok
-static struct { Work *w; int np, nu_max, tn, nb, L, order; const float *hn; int dec; float *x; bool compact, grp; } LAST;
 
 static inline unsigned grid8(int items) { return (unsigned)((items + 7) / 8 * 8); }  // xcd_item needs a multiple of 8
 #ifndef GU_OCC
@@ -328,13 +329,10 @@ static int launch_quant_act(Work &w, int maxtiles, int tn, int np, int *dg) {
 // device_grouping: the grouping came from k_group (pu is valid), so the 64-token-tile path may
 // hand the down results to k_combine as int16 (not with checks on: the tests read them as fp32)
 static int stage_experts(Work &w, int np, int nu_max, int tn, bool device_grouping) {
-    LAST.w = &w; LAST.np = np; LAST.nu_max = nu_max; LAST.tn = tn; LAST.dec = 0;
     int maxtiles = np / tn + (nu_max < np ? nu_max : np);
     int *dg = S.debug ? w.dbg_gu : nullptr, *dd = S.debug ? w.dbg_dn : nullptr;
     w.compact = device_grouping && tn == 64 && !S.debug;
-    LAST.compact = w.compact;
-    LAST.grp = device_grouping && w.grp16;
-    if (tn == 16 && S_expert16) return launch_expert16(w, maxtiles, dg, dd, LAST.grp);
+    if (tn == 16 && S_expert16) return launch_expert16(w, maxtiles, dg, dd, device_grouping && w.grp16);
     if (launch_gateup(w, maxtiles, tn, dg)) return -1;
     if (!w.compact && launch_quant_act(w, maxtiles, tn, np, dg)) return -1;
     if (launch_down(w, maxtiles, tn, dd, w.compact)) return -1;
@@ -367,7 +365,6 @@ static int launch_dec_down(Work &w, int nb, float *d_x, int order) {
 }
 static int moe_dec(Work &w, int L, const float *in, int do_norm, int nb, float *d_x, int order) {
     LayerW &lw = S.layers[L];
-    LAST.w = &w; LAST.np = nb * MTOPK; LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = nullptr; LAST.dec = 1; LAST.x = d_x;
     const uint16_t *pln = do_norm ? lw.post_ln : nullptr;
     if (order == MMOE_ORDER_STEP) {
         if (launch(MMOE_K_ROUTER, [&] { kl(k_dec_route<16>, MNE * 16 / 64, 64, 0, in, nb, pln, do_norm, lw.rc16, lw.bias, w.hn, w.rl); })) return -1;
@@ -384,13 +381,14 @@ static int moe_dev(Work &w, int L, const float *d_hn, int nb, float *d_x, int or
     if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("layer %d not set (mmoe_set_layer)", L); return -1; }
     if (nb <= DEC_MAXTOK && S_dec_enabled) return moe_dec(w, L, d_hn, 0, nb, d_x, order);
     int np = nb * MTOPK, tn = tile_tn(np);
-    LAST.nb = nb; LAST.L = L; LAST.order = order; LAST.hn = d_hn; LAST.dec = 0;
     if (stage_router(w, L, d_hn, nb, order)) return -1;
     int rc = stage_route_group(w, L, nb, tn, d_hn);
     if (!rc) rc = stage_experts(w, np, MNE, tn, true);
     if (!rc) rc = stage_combine(w, nb, d_x, order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH);
     if (rc && w.hist_used) {   // a stage failed before the combine cleared the expert counts: clear them here
-        (void)hipMemsetAsync(w.hist, 0, (size_t)w.hist_used * sizeof(int), S.st);
+        // a fill kernel, not hipMemsetAsync: this may run under a caller's (or mmoe_stack_graph's) capture
+        kl(k_fill_zero, (w.hist_used + 255) / 256, 256, 0, w.hist, w.hist_used);
+        (void)hipGetLastError();
         w.hist_used = 0;
     }
     return rc;
@@ -1066,43 +1064,6 @@ double mmoe_event_elapsed_ms(void) {
     float ms = 0; if (hipEventElapsedTime(&ms, S.pe[0], S.pe[1]) != hipSuccess) return -1.0;
     return ms;
 }
-// Re-launch one stage of the last mmoe_moe / mmoe_moe_dev / gpre_moe call `reps` times back to back between
-// two events; returns the average milliseconds per launch (the stages are idempotent on their inputs).
-double mmoe_bench_stage(int kid, int reps) {
-    if (!LAST.w || reps < 1 || S.prof) { seterr("mmoe_bench_stage: nothing to repeat"); return -1.0; }
-    Work &w = *LAST.w;
-    int maxtiles = LAST.dec || LAST.tn < 1 ? 0 : LAST.np / LAST.tn + (LAST.nu_max < LAST.np ? LAST.nu_max : LAST.np);
-    if (hipEventRecord(S.pe[0], S.st) != hipSuccess) return -1.0;
-    for (int i = 0; i < reps; i++) {
-        int rc = 0;
-        if (LAST.dec) {   // decode kernels (k_dec_down adds into x again: timing only)
-            if (kid == MMOE_K_GATEUP) rc = launch_dec_gateup(w, LAST.nb, LAST.L);
-            else if (kid == MMOE_K_DOWN) rc = launch_dec_down(w, LAST.nb, LAST.x, LAST.order);
-            else { seterr("mmoe_bench_stage: kernel %d not repeatable on the decode path", kid); return -1.0; }
-            if (rc) return -1.0;
-            continue;
-        }
-        if (LAST.tn == 16 && S_expert16 && kid != MMOE_K_ROUTER) {
-            if (kid != MMOE_K_GATEUP) { seterr("mmoe_bench_stage: the fused expert path has one kernel (MMOE_K_GATEUP)"); return -1.0; }
-            if (launch_expert16(w, maxtiles, nullptr, nullptr, LAST.grp)) return -1.0;
-            continue;
-        }
-        switch (kid) {
-            case MMOE_K_GATEUP: rc = launch_gateup(w, maxtiles, LAST.tn, nullptr); break;
-            case MMOE_K_DOWN: rc = launch_down(w, maxtiles, LAST.tn, nullptr, LAST.compact); break;
-            case MMOE_K_QUANT_ACT:
-                if (LAST.compact) { seterr("mmoe_bench_stage: the act quantisation runs inside the down kernel here"); return -1.0; }
-                rc = launch_quant_act(w, maxtiles, LAST.tn, LAST.np, nullptr); break;
-            case MMOE_K_ROUTER: rc = LAST.hn ? stage_router(w, LAST.L, LAST.hn, LAST.nb, LAST.order) : -1; break;
-            default: seterr("mmoe_bench_stage: kernel %d not repeatable", kid); return -1.0;
-        }
-        if (rc) return -1.0;
-    }
-    if (hipEventRecord(S.pe[1], S.st) != hipSuccess || hipEventSynchronize(S.pe[1]) != hipSuccess) return -1.0;
-    float ms = 0; (void)hipEventElapsedTime(&ms, S.pe[0], S.pe[1]);
-    return ms / reps;
-}
-
 // Exhaustive check of the SiLU used by k_act_quant against its IEEE-division form over the bit patterns
 // [lo, lo + n). Blocks until done; *nbad = mismatches, *first = smallest mismatching pattern (0xffffffff
 // if none).

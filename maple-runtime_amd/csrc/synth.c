@@ -15,6 +15,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "maplesynth.h"
+
 #define SY_H 2048
 #define SY_NE 256
 #define SY_FF 512

@@ -15,6 +15,7 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmaplemoe.so")
+SYNTH_PATH = os.path.join(HERE, "libmaplesynth.so")   # synthetic data (bench and test tooling, not the path)
 
 H, NE, TOPK, FF = 2048, 256, 8, 512
 EXPERT_BYTES = 798720
@@ -28,6 +29,7 @@ KERNELS = ["rmsnorm", "router", "topk", "group", "quant", "gateup", "quant_act",
            "att_scores", "att_softmax", "att_pv"]
 
 _lib = None
+_slib = None
 
 
 def lib():
@@ -38,6 +40,24 @@ def lib():
         _lib = C.CDLL(LIB_PATH)
         _declare(_lib)
     return _lib
+
+
+def slib():
+    """libmaplesynth.so: seeded synthetic Maple-shaped data (include/maplesynth.h)"""
+    global _slib
+    if _slib is None:
+        if not os.path.exists(SYNTH_PATH):
+            raise RuntimeError(f"{SYNTH_PATH} is not built (make -C maple-runtime_amd)")
+        _slib = C.CDLL(SYNTH_PATH)
+        u64, i, d, vp, sz = C.c_uint64, C.c_int, C.c_double, C.c_void_p, C.c_size_t
+        for name, (res, args) in {
+            "mmoe_synth_expert": (None, [u64, i, i, vp, vp, vp, vp, vp, vp]), "mmoe_synth_expert_bytes": (sz, []),
+            "mmoe_synth_layer": (None, [u64, i, vp, i]), "mmoe_synth_router": (None, [u64, i, i, vp]),
+            "mmoe_synth_hidden": (None, [u64, i, i, vp]), "mmoe_synth_zipf_bias": (None, [u64, d, vp]),
+        }.items():
+            f = getattr(_slib, name)
+            f.restype, f.argtypes = res, args
+    return _slib
 
 
 def _declare(L):
@@ -62,16 +82,13 @@ def _declare(L):
         "mmoe_read": (i, [i, vp, sz]), "mmoe_set_debug": (i, [i]), "mmoe_set_decode_path": (i, [i]), "mmoe_set_expert_path": (i, [i]), "mmoe_set_router_mode": (i, [i]), "mmoe_last_error": (C.c_char_p, []),
         "mmoe_dev_alloc": (vp, [sz]), "mmoe_dev_free": (i, [vp]), "mmoe_h2d": (i, [vp, vp, sz]),
         "mmoe_d2h": (i, [vp, vp, sz]), "mmoe_d2d": (i, [vp, vp, sz]), "mmoe_sync": (i, []), "mmoe_stream": (vp, []),
-        "mmoe_event_record": (i, [i]), "mmoe_bench_stage": (d, [i, i]), "mmoe_event_elapsed_ms": (d, []), "mmoe_prof": (i, [i]),
+        "mmoe_event_record": (i, [i]), "mmoe_event_elapsed_ms": (d, []), "mmoe_prof": (i, [i]),
         "mmoe_prof_reset": (i, []), "mmoe_prof_get": (i, [i, C.POINTER(C.c_double), C.POINTER(C.c_long)]),
         "mmoe_device_info": (i, [C.c_char_p, i, ip, ip]),
         "mmoe_selftest_silu": (i, [C.c_uint32, C.c_uint32, C.POINTER(C.c_ulonglong), u32p]),
         "mmoe_ckpt_open": (i, [C.c_char_p]), "mmoe_ckpt_close": (None, []), "mmoe_ckpt_error": (C.c_char_p, []),
         "mmoe_ckpt_layer_plan": (i, [i, ip, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), vp]),
         "mmoe_ckpt_bf16": (vp, [i, i]), "mmoe_ckpt_load": (i, [i, i]),
-        "mmoe_synth_expert": (None, [u64, i, i, vp, vp, vp, vp, vp, vp]), "mmoe_synth_expert_bytes": (sz, []),
-        "mmoe_synth_layer": (None, [u64, i, vp, i]), "mmoe_synth_router": (None, [u64, i, i, vp]),
-        "mmoe_synth_hidden": (None, [u64, i, i, vp]), "mmoe_synth_zipf_bias": (None, [u64, d, vp]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -102,7 +119,7 @@ def page_aligned(nbytes):
 def synth_layer_block(seed, L, nthreads=8):
     """All 256 experts of layer L, contiguous (EXPERT_BYTES each), page aligned."""
     blk = page_aligned(NE * EXPERT_BYTES)
-    lib().mmoe_synth_layer(seed, L, ptr(blk), nthreads)
+    slib().mmoe_synth_layer(seed, L, ptr(blk), nthreads)
     return blk
 
 
@@ -117,19 +134,19 @@ def expert_views(blk, e):
 
 def synth_router(seed, L, dist=0):
     w = np.empty((NE, H), np.uint16)
-    lib().mmoe_synth_router(seed, L, dist, ptr(w))
+    slib().mmoe_synth_router(seed, L, dist, ptr(w))
     return w
 
 
 def synth_hidden(seed, sid, nb):
     x = np.empty((nb, H), np.float32)
-    lib().mmoe_synth_hidden(seed, sid, nb, ptr(x))
+    slib().mmoe_synth_hidden(seed, sid, nb, ptr(x))
     return x
 
 
 def zipf_bias(seed, s=1.1):
     b = np.empty(NE, np.float32)
-    lib().mmoe_synth_zipf_bias(seed, s, ptr(b))
+    slib().mmoe_synth_zipf_bias(seed, s, ptr(b))
     return b
 
 

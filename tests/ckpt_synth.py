@@ -43,7 +43,7 @@ def write_checkpoint(d, seed, nexp=6, gu_shards=2):
         gc = np.empty((M.FF, M.H // 4), np.uint8); gs = np.empty(M.FF, np.float32)
         uc = np.empty((M.FF, M.H // 4), np.uint8); us = np.empty(M.FF, np.float32)
         dc = np.empty((M.H, M.FF // 4), np.uint8); ds = np.empty(M.H, np.float32)
-        M.lib().mmoe_synth_expert(seed, 0, k, M.ptr(gc), M.ptr(gs), M.ptr(uc), M.ptr(us), M.ptr(dc), M.ptr(ds))
+        M.slib().mmoe_synth_expert(seed, 0, k, M.ptr(gc), M.ptr(gs), M.ptr(uc), M.ptr(us), M.ptr(dc), M.ptr(ds))
         experts.append((gc, gs, uc, us, dc, ds))
         g = sh[k % gu_shards]
         o_gc = g.put(gc); o_gs = g.put(gs); o_uc = g.put(uc); o_us = g.put(us)
@@ -104,7 +104,7 @@ def write_model_checkpoint(d, seed, nexp=16, vocab_rows=4096):
         gc = np.empty((M.FF, M.H // 4), np.uint8); gs = np.empty(M.FF, np.float32)
         uc = np.empty((M.FF, M.H // 4), np.uint8); us = np.empty(M.FF, np.float32)
         dc = np.empty((M.H, M.FF // 4), np.uint8); ds = np.empty(M.H, np.float32)
-        M.lib().mmoe_synth_expert(seed, 0, k, M.ptr(gc), M.ptr(gs), M.ptr(uc), M.ptr(us), M.ptr(dc), M.ptr(ds))
+        M.slib().mmoe_synth_expert(seed, 0, k, M.ptr(gc), M.ptr(gs), M.ptr(uc), M.ptr(us), M.ptr(dc), M.ptr(ds))
         g = sh[k % 2]
         o = (k % 2, g.put(gc), g.put(gs), g.put(uc), g.put(us), sh[2].put(dc), sh[2].put(ds))
         eoff.append(o)

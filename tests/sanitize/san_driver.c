@@ -15,6 +15,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include "maplemoe.h"
+#include "maplesynth.h"
 #include "moe_oracle.h"
 
 #define STUB_MAXREG 64   /* the stand-in's own region table (gpu_pre.m:21's size) */

@@ -23,6 +23,17 @@ def test_exports_every_declared_symbol():
     assert not missing, missing
 
 
+def test_synth_library_exports_its_header():
+    with open(os.path.join(ROOT, "include", "maplesynth.h")) as f:
+        src = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+    names = sorted(set(re.findall(r"^\s*[A-Za-z_][\w\s\*]*?\b(\w+)\s*\([^;]*\)\s*;", src, flags=re.M)))
+    assert len(names) == 6
+    slib = C.CDLL(M.SYNTH_PATH)
+    assert all(hasattr(slib, n) for n in names)
+    prod = C.CDLL(M.LIB_PATH)   # the product library carries no bench tooling
+    assert not any(hasattr(prod, n) for n in names)
+
+
 def test_reference_entry_points_present():
     # every prototype maple.c declares for its GPU path (maple.c:247-272)
     want = ["gpu_head_init", "gpu_head_init_i8", "gpu_head_run", "gpu_head_run_multi", "gpux_init", "gpux_upload",

@@ -503,6 +503,15 @@ def test_zipf_mfma_router_matches_exact(zipf_layer):
         print(f"\n  mfma vs exact router: tw relmax {relmax(w0, w1):.1e}, x relmax {relmax(x0 - x, x1 - x):.1e}, "
               f"other logits relmax {relmax(r0, r1):.1e}")
         assert relmax(w0, w1) <= TOL and relmax(x0 - x, x1 - x) <= TOL
+        # how close the MFMA logits came to the refinement's rounding bound: every approximate logit's distance
+        # from its exact chain value, as a share of the token's bound err_b (the kernel's candidate margin is
+        # twice err_b, so a share below 1 leaves every non-candidate provably outside the exact top 8)
+        wf = (zipf_layer.router.astype(np.uint32) << 16).view(np.float32)
+        w1max = float(np.abs(wf).sum(1, dtype=np.float32).max())
+        err_b = 2.0 * 463.0 * 1.01 / 2 ** 24 * np.abs(hn).max(1) * w1max
+        share = float((np.abs(r0.astype(np.float64) - r1) / err_b[:, None]).max())
+        print(f"  largest |approximate - exact| logit: {share:.3f} of the bound err_b")
+        assert share < 1.0
         h = T // 2
         for lo, hi in ((0, h), (h, T)):
             xs = run_gpu(L, np.ascontiguousarray(hn[lo:hi]), np.ascontiguousarray(x[lo:hi]), M.ORDER_BATCH)
@@ -561,3 +570,32 @@ def test_step_order_batch_matches_oracle(layer0, nb):
         e = relmax(xg[b] - x[b], xo - x[b])
         print(f"\n  nb={nb} token {b}: x bit-exact {np.array_equal(xg[b], xo)}, relmax {e:.1e}")
         assert e <= TOL
+
+
+def test_mfma_router_large_bias(zipf_layer):
+    """The MFMA router's candidate margin with a bias far larger than the logits themselves: the final bias add
+    rounds relative to |logit + bias| (ulp 2^-5 at 2^18), and the margin covers that term too. Biases of 2^18 plus
+    the Zipf values put many experts within a few ulp of the 8th place; the MFMA router with refinement must pick
+    the exact chain router's top-8 (ties to the lowest index) with the same logits for the picks, at 600 tokens."""
+    lib = M.lib()
+    L, T = zipf_layer.L, 600
+    big = (np.float32(262144.0) + zipf_layer.bias).astype(np.float32)
+    M.check(lib.mmoe_set_bias(L, M.ptr(big)), "bias")
+    x, hn = normed_hidden(SEED, 4400, T)
+    try:
+        out = {}
+        for mode in (1, 0):
+            M.check(lib.mmoe_set_router_mode(mode), "router mode")
+            xg = run_gpu(L, hn, x, M.ORDER_BATCH)
+            out[mode] = (xg, M.read("TOP", (T, 8), np.int32), M.read("LOGITS", (T, 256), np.float32))
+        (x1, t1, r1), (x0, t0, r0) = out[1], out[0]
+        assert np.array_equal(t0, t1), f"top-8 differs on {int((t0 != t1).any(1).sum())} tokens"
+        sel = np.take_along_axis(r0, t0, 1).view(np.int32), np.take_along_axis(r1, t1, 1).view(np.int32)
+        assert np.array_equal(*sel), "the picked experts' logits differ"
+        assert relmax(x0 - x, x1 - x) <= TOL
+        srt = np.sort(r1, 1)
+        near = int((srt[:, -9] >= srt[:, -8] - 2 ** -4).sum())
+        print(f"\n  bias 2^18: top-8 identical; tokens with a 9th expert within 2 ulp of the 8th: {near}")
+    finally:
+        M.check(lib.mmoe_set_router_mode(0), "router mode")
+        M.check(lib.mmoe_set_bias(L, M.ptr(zipf_layer.bias)), "bias")

@@ -48,7 +48,7 @@ def test_synth_codes_are_ternary_with_the_configured_mix():
     blk = M.page_aligned(M.EXPERT_BYTES)
     gc, gs, uc, us, dc, ds = (np.empty(s, d) for s, d in [((512, 512), np.uint8), (512, np.float32), ((512, 512), np.uint8),
                                                           (512, np.float32), ((2048, 128), np.uint8), (2048, np.float32)])
-    M.lib().mmoe_synth_expert(SEED, 0, 5, *[M.ptr(a) for a in (gc, gs, uc, us, dc, ds)])
+    M.slib().mmoe_synth_expert(SEED, 0, 5, *[M.ptr(a) for a in (gc, gs, uc, us, dc, ds)])
     codes = np.zeros((512, 2048), np.uint8)
     O.oracle().mo_unpack(O._p(gc), 512, 2048, O._p(codes))
     frac = np.bincount(codes.ravel(), minlength=4) / codes.size

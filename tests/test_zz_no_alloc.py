@@ -1,7 +1,8 @@
 """mmoe_moe_dev_noalloc (work buffers in the library's static scratch, no allocation) against mmoe_moe_dev on
 the same inputs, bit for bit: two calls in a row, the second with a smaller batch, on the decode kernels
-(<= 8 tokens) and on the grouped 16-token-tile kernels (9..64 tokens), in both summation orders; sizes past
-the scratch are refused."""
+(<= 8 tokens) and on the grouped 16-token-tile kernels (9..64 tokens), in both summation orders, and with the
+other kernel choices (the separate gate/up, quantisation and down kernels with k_group's per-chunk counts in the
+scratch; the grouped kernels for <= 8 tokens); sizes past the scratch are refused."""
 import numpy as np
 import pytest
 
@@ -45,6 +46,24 @@ def test_noalloc_matches_moe_dev(layer, sizes, order):
         got = run(lib, lib.mmoe_moe_dev_noalloc, hn, x, order)
         assert np.array_equal(got.view(np.int32), want.view(np.int32)), f"nb={nb}: differs from mmoe_moe_dev"
         assert not np.array_equal(got, x)
+
+
+@pytest.mark.parametrize("fused,dec", [(0, 1), (1, 0), (0, 0)])
+def test_noalloc_other_kernel_paths(layer, fused, dec):
+    lib = layer
+    M.check(lib.mmoe_set_expert_path(fused), "expert path")
+    M.check(lib.mmoe_set_decode_path(dec), "decode path")
+    try:
+        for k, nb in enumerate((64, 9, 8, 3)):
+            print(f"\n  fused={fused} dec={dec} call {k}: nb={nb}", flush=True)
+            x, hn = normed_hidden(SEED, 900 + 10 * nb + k, nb)
+            want = run(lib, lib.mmoe_moe_dev, hn, x, M.ORDER_BATCH)
+            got = run(lib, lib.mmoe_moe_dev_noalloc, hn, x, M.ORDER_BATCH)
+            assert np.array_equal(got.view(np.int32), want.view(np.int32)), f"nb={nb}: differs from mmoe_moe_dev"
+            assert not np.array_equal(got, x)
+    finally:
+        M.check(lib.mmoe_set_expert_path(1), "expert path")
+        M.check(lib.mmoe_set_decode_path(1), "decode path")
 
 
 def test_noalloc_refuses_past_scratch(layer):
