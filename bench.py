@@ -49,6 +49,25 @@ def pmc_traffic(kernel):
     return None
 
 
+def pmc_mfma(kernel, workload):
+    """counter-based MFMA figures of `kernel` (a prefix of its instantiation) at `workload` from the committed
+    rocprofv3 summary: busy share of the 1024 SIMDs at the published clock over the kernel's duration, and the
+    ops the MFMA pipes ran over the algorithmic ops (tile padding). None if the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "mfma_util.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        cols = [c.strip() for c in line.split("|")]
+        if len(cols) > 12 and cols[1].startswith(kernel) and cols[2] == workload:
+            try:
+                return dict(busy_frac_at_peak_clock=float(cols[9]), mfma_util_rocprof=float(cols[8]),
+                            padded_ops_ratio=round(float(cols[10]) / float(cols[11]), 3),
+                            avg_launch_us_profiled=float(cols[4]), source="profiles/mfma_util.md")
+            except ValueError:
+                return None
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -403,7 +422,8 @@ def main():
                        experts_used=plan["nu"], max_expert_load=int(cnt.max()),
                        roofline=dict(bound="mfma", kernel="k_gateup_pk<true> (grouped int8 MFMA)", achieved=round(g_ops / g_us / 1e6, 1),
                                      peak=INT8_PEAK_TOPS, unit="TOPS", frac=round(g_ops / g_us / 1e6 / INT8_PEAK_TOPS, 4),
-                                     traffic=pmc_traffic("k_gateup_pk<true>"), avg_launch_us=round(g_us, 2)),
+                                     traffic=pmc_traffic("k_gateup_pk<true>"), avg_launch_us=round(g_us, 2),
+                                     counters=pmc_mfma("k_gateup_pk<true", "config 2")),
                        kernels_us={k: round(v[0] / v[1] * 1e3, 2) for k, v in pk.items()})
 
     # ---- config 3: batched decode, 64 sequences x 24 layers (batch order), and config 0: a 128-token chunk
