@@ -382,6 +382,19 @@ def main():
                            "tokens (events on the dispatch, as rocprofv3)",
                     step_gbs=round(bytes_tok / ms / 1e6, 1), step_frac=round(bytes_tok / ms / 1e6 / HBM_PEAK_GBS, 4))
 
+    # ---- the floor under the decode layer: 3 x 24 dependent kernels at the decode grid shapes, one HIP graph
+    floor = None
+    fpath = os.path.join(ROOT, "maple-runtime_amd", "libmaplefloor.so")
+    if not args.no_decode and os.path.exists(fpath):
+        fl = C.CDLL(fpath)
+        fl.floor_layer_us.restype, fl.floor_layer_us.argtypes = C.c_double, [C.c_int, C.c_int, C.c_int]
+        fv = [fl.floor_layer_us(f, NL, 200) for f in (0, 1, 2)]
+        floor = dict(unit="us per layer (3 dependent kernels)", empty_kernels=round(fv[0], 2),
+                     one_dependent_load=round(fv[1], 2), dependent_load_then_cold_load=round(fv[2], 2),
+                     measured_layer=round(ms * 1e3 / NL, 2))
+        log(f"decode floor per layer (graph of 3 x 24 kernels at the decode grids): empty {fv[0]:.2f} us, "
+            f"one dependent load {fv[1]:.2f} us, dependent + cold load {fv[2]:.2f} us; measured layer {ms * 1e3 / NL:.2f} us")
+
     # ---- config 2: 2048-token prefill, one layer, Zipf(1.1)-skewed routing. Steps rotate over 4 layers with
     # different experts (4 x 204 MB, more than the 256 MB last-level cache holds)
     prefill = None
@@ -494,7 +507,7 @@ def main():
            "config": {"workload": "config 1: decode 1 token x 24 stacked MoE layers (d=2048, 256 experts, top-8, FF=512)",
                       "tokens_per_step": 1, "layers": NL, "hip_graph": bool(args.graph), "device": name},
            "roofline": roof, "cpu_baseline": cpu, "prefill": prefill,
-           "decode_kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in kt.items()}, **extra}
+           "decode_kernels_us": {k: round(v[0] / v[1] * 1e3, 2) for k, v in kt.items()}, "decode_floor": floor, **extra}
     print(json.dumps(out), flush=True)
 
 

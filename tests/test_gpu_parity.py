@@ -285,20 +285,28 @@ def test_moe_batch_mfma_router(layer0):
         M.check(lib.mmoe_set_router_mode(0), "router mode")
 
 
-@pytest.fixture(scope="module")
-def tie_layer():
-    """Layer 19: router weights all zero and a bias with large tie classes, so every logit is its expert's bias
-    exactly: 3 distinct leaders, then a class of 52 equal logits (e * 37 % 5 == 4) across the 8th place."""
+@pytest.fixture(scope="module", params=[52, 253])
+def tie_layer(request):
+    """Layers 19 and 20: router weights all zero and a bias with large tie classes, so every logit is its expert's
+    bias exactly: 3 distinct leaders, then a class of equal logits across the 8th place. Layer 19: 52 experts
+    (e * 37 % 5 == 4); layer 20: the 253 other experts all equal (every lane holds four tied experts, so each
+    pick after the third must find the lowest lane and, inside it, the lowest slot)."""
     lib = M.lib()
     M.check(lib.mmoe_init(2048), "mmoe_init")
-    hl = HostLayer(SEED, 19)
+    L = 19 if request.param == 52 else 20
+    hl = HostLayer(SEED, L)
     hl.router = np.zeros((256, 2048), np.uint16)
-    hl.rid = M.register_layer(19, hl.blk, hl.router)
-    hl.bias = ((np.arange(256) * 37) % 5).astype(np.float32) * 0.25
+    hl.rid = M.register_layer(L, hl.blk, hl.router)
+    if request.param == 52:
+        hl.bias = ((np.arange(256) * 37) % 5).astype(np.float32) * 0.25
+        hl.want = [250, 3, 180] + [e for e in range(256) if e * 37 % 5 == 4][:5]
+    else:
+        hl.bias = np.zeros(256, np.float32)
+        hl.want = [250, 3, 180, 0, 1, 2, 4, 5]
     hl.bias[[250, 3, 180]] = [3.0, 2.5, 2.25]
-    M.check(lib.mmoe_set_bias(19, M.ptr(hl.bias)), "bias")
+    M.check(lib.mmoe_set_bias(L, M.ptr(hl.bias)), "bias")
     yield hl
-    M.check(lib.mmoe_set_bias(19, None), "bias off")
+    M.check(lib.mmoe_set_bias(L, None), "bias off")
 
 
 @pytest.mark.parametrize("nb,order", [(1, 1), (1, 0), (5, 0), (64, 0), (600, 0)])
@@ -319,7 +327,7 @@ def test_topk_ties_pick_lowest_index(tie_layer, nb, order):
         o = O.moe_step(hn[0], hl.router, hl.table, xo[0], bias=hl.bias)
     else:
         o = O.moe_batch(hn, hl.router, hl.table, xo, bias=hl.bias)
-    want = [250, 3, 180] + [e for e in range(256) if e * 37 % 5 == 4][:5]
+    want = hl.want
     otop = o["top"].reshape(nb, 8)
     assert (otop == np.array(want)).all(), "oracle picks"
     assert np.array_equal(M.read("TOP", (nb, 8), np.int32), otop), "top-8 indices differ"
