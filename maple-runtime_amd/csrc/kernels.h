@@ -611,6 +611,14 @@ __global__ void __launch_bounds__(512) k_group(const int *__restrict__ hist, int
     __shared__ int slots[64][MTOPK];
     int c = blockIdx.x, t = threadIdx.x, nchunk = (nb + 63) / 64;
     int run = 0, pre = 0, used = 0, nt = 0;
+    // loads that do not depend on the counts go out first: block 0's copies of the used experts' table entries
+    // and every thread's pair (token, slot) for the placement
+    v4i lt0 = {0, 0, 0, 0}, lt1 = lt0, lt2 = lt0;
+    if (c == 0 && layer_tab && t < MNE) { const v4i *lp = (const v4i *)(layer_tab + t); lt0 = lp[0]; lt1 = lp[1]; lt2 = lp[2]; }
+    int tk = t >> 3, s = t & 7, b = c * 64 + tk;
+    bool live = b < nb;
+    int e = live ? top[b * MTOPK + s] : 0;
+    float wv = live ? tw[b * MTOPK + s] : 0.0f;
     if (t < MNE) {
         int cnt[MAXCH];
 #pragma unroll
@@ -648,7 +656,7 @@ __global__ void __launch_bounds__(512) k_group(const int *__restrict__ hist, int
                 plan->ue[uidx] = e;
                 plan->ustart[uidx] = pstart;
                 plan->tstart[uidx] = tstart;
-                if (layer_tab) eptr_u[uidx] = layer_tab[e];
+                if (layer_tab) { v4i *d = (v4i *)(eptr_u + uidx); d[0] = lt0; d[1] = lt1; d[2] = lt2; }
                 for (int i = 0; i < nt; i++) tiles[tstart + i] = Tile{uidx, pstart + i * tn, min(tn, run - i * tn), 0};
             }
             if (e == MNE - 1) {
@@ -660,10 +668,6 @@ __global__ void __launch_bounds__(512) k_group(const int *__restrict__ hist, int
     }
     __syncthreads();
     // placement: thread (token tk of the chunk, slot s)
-    int tk = t >> 3, s = t & 7, b = c * 64 + tk;
-    bool live = b < nb;
-    int e = live ? top[b * MTOPK + s] : 0;
-    float wv = live ? tw[b * MTOPK + s] : 0.0f;
     int bs = live ? sbase[e] : 0;
     if (live) atomicOr(&msk[e], 1ull << tk);
     __syncthreads();
