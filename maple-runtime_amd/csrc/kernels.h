@@ -197,15 +197,27 @@ __device__ __forceinline__ float hsum8(const float *v) {
 // NORM: `in` is the hidden state x and the block first forms hn = rmsnorm(x, post_ln) for its token with
 // exactly k_rmsnorm's arithmetic (thread t sums columns t, t+256, ... in fp64, then the same 256-wide tree);
 // blocks with blockIdx.x == 0 write hn to hn_out. Else `in` is hn.
-template <int NCH, bool NORM = false>
+// the top-8 / quantisation outputs of a router launch that also routes its tokens (TK); defined further down:
+struct RouteTail { int *top; float *tw; int8_t *qx; float *qsx; int *qsumx; int *hist; int *cnt; };
+__device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw);
+template <int N, int GPAD = 0>
+__device__ __forceinline__ void quant_wave(const float *__restrict__ xr, int l, int8_t *__restrict__ q, float *__restrict__ qs,
+                                           int *__restrict__ qsum);
+template <int NCH, bool NORM = false, bool TK = false>
 __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__ in, int nb, const uint16_t *__restrict__ wc,
                                                        const float *__restrict__ bias, float *__restrict__ rl,
-                                                       const uint16_t *__restrict__ post_ln = nullptr, float *__restrict__ hn_out = nullptr) {
+                                                       const uint16_t *__restrict__ post_ln = nullptr, float *__restrict__ hn_out = nullptr,
+                                                       RouteTail tail = RouteTail{}) {
     constexpr int LEN = MH / NCH, HP = LEN + 4;
     __shared__ __attribute__((aligned(16))) float hc[NCH * HP];
     __shared__ double red[NORM ? 256 : 1];
     __shared__ float kk;
-    int tid = threadIdx.x, b = blockIdx.y, j = tid % NCH, e = blockIdx.x * (256 / NCH) + tid / NCH;
+    // TK: a 1-D grid in which the NCH blocks of token b (expert groups y) all get ids = b mod 8, i.e. run on
+    // XCD b mod 8 (workgroup ids go to the 8 XCDs round robin) and share its L2; else grid (NCH, nb)
+    int b = TK ? (int)(blockIdx.x / (8 * NCH)) * 8 + (int)(blockIdx.x % 8) : (int)blockIdx.y;
+    int y = TK ? (int)(blockIdx.x / 8) % NCH : (int)blockIdx.x;
+    if (TK && b >= nb) return;   // whole block
+    int tid = threadIdx.x, j = tid % NCH, e = y * (256 / NCH) + tid / NCH;
     const float *xr = in + (size_t)b * MH;
     float xv[8];
     uint32_t pw[8];   // bf16 bits, one per register (no packing between the loads and the barrier)
@@ -243,7 +255,7 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
             float wn = __uint_as_float(pw[i] << 16);
             float h = xv[i] * k * wn;
             hc[(c % NCH) * HP + c / NCH] = h;
-            if (blockIdx.x == 0) hn_out[(size_t)b * MH + c] = h;
+            if (y == 0) hn_out[(size_t)b * MH + c] = h;
         }
     } else {
 #pragma unroll
@@ -284,6 +296,28 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
         float r = hsum8(s8);
         if (bias) r = r + be;
         rl[(size_t)b * MNE + e] = r;
+    }
+    if (TK) {
+        // the token's softmax/top-8 and int8 quantisation in the last of its NCH blocks to arrive: every block's
+        // stores (logits; hn from block 0) reach the XCD's L2 before its arrival is counted, and the last one
+        // reads them there (its L1 holds none of those lines: nothing in this kernel read them before)
+        __shared__ int last;
+        __shared__ __attribute__((aligned(16))) float E[MNE];
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (tid == 0) last = atomicAdd(&tail.cnt[b], 1) == NCH - 1;
+        __syncthreads();
+        if (!last) return;
+        int wv = tid >> 6, l = tid & 63;
+        if (wv == 0) {
+            int ek = topk_wave(rl + (size_t)b * MNE, E, l, tail.top + b * MTOPK, tail.tw + b * MTOPK);
+            if (tail.hist && l < MTOPK) atomicAdd(&tail.hist[(b >> 6) * MNE + ek], 1);   // per-chunk counts for k_group
+        } else if (wv == 1) {
+            const float *hr = (NORM ? hn_out : in) + (size_t)b * MH;
+            quant_wave<MH>(hr, l, tail.qx + (size_t)b * MH, tail.qsx + b, tail.qsumx + b);
+        } else if (tid == 128) {
+            tail.cnt[b] = 0;   // for the next launch (every block of the token has counted)
+        }
     }
 }
 
@@ -721,7 +755,7 @@ __device__ __forceinline__ uint32_t rint_pack4(float a, float b, float c, float 
 // =====================================================================================================
 // One wave quantises one vector of N (2048 or 512) floats into q (mfma order), *qs, *qsum (lane 0 writes).
 // GPAD: bytes of padding after each 128-column group of q (LDS copies read by lanes one group apart).
-template <int N, int GPAD = 0>
+template <int N, int GPAD>
 __device__ __forceinline__ void quant_wave(const float *__restrict__ xr, int l, int8_t *__restrict__ q, float *__restrict__ qs,
                                            int *__restrict__ qsum) {
     constexpr int NCHK = N / 16;                    // 16-byte output chunks per vector

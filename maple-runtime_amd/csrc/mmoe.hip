@@ -76,6 +76,8 @@ struct Work {
     const uint16_t *norm_w = nullptr;
     float *rpart = nullptr;         // partial router logits [4][T][256] (approximate router)
     bool grp16 = false;             // the last device routing left the grouping to k_expert16 (no k_group launch)
+    bool routed = false;            // the last chain-router launch also ran the top-8 and the quantisation
+    int *rcnt = nullptr;            // per token: router blocks done (that launch's arrival counts, back to 0 after)
     int grp_nb = 0;
     const ExpPtr *grp_tab = nullptr;
     bool refine = false;            // the last router call left approximate logits for k_refine_topk
@@ -156,10 +158,11 @@ static int work_alloc(Work &w, int maxtok, Carve *c = nullptr) {
         wbuf(w.utok, P * 4, c) || wbuf(w.uw, P * 4, c) || wbuf(w.tp, P * 4, c) || wbuf(w.sp, P * 4, c) ||
         wbuf(w.ustart, (MNE + 1) * 4, c) || wbuf(w.qx, T * MH, c) || wbuf(w.qsx, T * 4, c) || wbuf(w.qsumx, T * 4, c) ||
         wbuf(w.act, P * MFF * 4, c) || wbuf(w.qa, P * MFF, c) || wbuf(w.qsa, P * 4, c) || wbuf(w.qsuma, P * 4, c) ||
-        wbuf(w.down, P * MH * 4, c) || wbuf(w.eu, MNE * 4, c) || wbuf(w.pu, P * 4, c))
+        wbuf(w.down, P * MH * 4, c) || wbuf(w.eu, MNE * 4, c) || wbuf(w.pu, P * 4, c) || wbuf(w.rcnt, T * 4, c))
         return -1;
     // the per-chunk expert counts start at zero; the combine after k_group clears what it used
     kl(k_fill_zero, (nch * MNE + 255) / 256, 256, 0, w.hist, nch * MNE);
+    kl(k_fill_zero, (maxtok + 255) / 256, 256, 0, w.rcnt, maxtok);
     HC(hipGetLastError());
     if (c) return 0;
     HC(hipMalloc(&w.x, T * MH * 4));
@@ -229,21 +232,40 @@ static int tile_tn(int np) { return np >= 2048 ? 64 : 16; }
 static bool S_expert16 = true;   // tiles of 16: the fused whole-expert kernel (else three kernels)
 
 // Router logits of nb tokens (d_hn) with layer L's router; order 0 = batch (maple.c:853-889), 1 = step (bf_row)
-static bool S_router_exact = false;   // batches of 512+: MFMA logits + exact refinement (else the exact chain GEMM)
+static bool S_router_exact = false;
+#ifndef ROUTER_TK
+#define ROUTER_TK 1
+#endif
+static bool S_router_tk = ROUTER_TK;   // batches below 512: top-8 and quantisation in the router launch   // batches of 512+: MFMA logits + exact refinement (else the exact chain GEMM)
 // exact_only: never the approximate large-batch router (callers that hand the logits themselves to the host)
-static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bool exact_only = false) {
+// tk (batches below 512 tokens): the router launch also runs each token's softmax/top-8 (per-chunk counts into
+// hist unless hist is null) and its int8 quantisation, in the last of the token's router blocks
+static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bool exact_only = false, bool tk = false,
+                        int *hist = nullptr) {
     LayerW &lw = S.layers[L];
     w.refine = false;
+    w.routed = false;
     if (!lw.router) { seterr("layer %d has no router (mmoe_set_layer)", L); return -1; }
     // w.norm_x set (stacked path): the chain routers form hn = rmsnorm(x, post_ln) into d_hn themselves
     float *hn_w = const_cast<float *>(d_hn);
+    if (tk && nb < 512) {
+        RouteTail rt{w.top, w.tw, w.qx, w.qsx, w.qsumx, hist, w.rcnt};
+        w.routed = true;
+        unsigned g8 = (unsigned)((nb + 7) / 8 * 8);
+        if (order == MMOE_ORDER_STEP) {
+            if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16, true, true>, g8 * 16, 256, 0, w.norm_x, nb, lw.rc16, lw.bias, w.rl, w.norm_w, hn_w, rt); });
+            return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16, false, true>, g8 * 16, 256, 0, d_hn, nb, lw.rc16, lw.bias, w.rl, nullptr, nullptr, rt); });
+        }
+        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<8, true, true>, g8 * 8, 256, 0, w.norm_x, nb, lw.rc8, lw.bias, w.rl, w.norm_w, hn_w, rt); });
+        return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<8, false, true>, g8 * 8, 256, 0, d_hn, nb, lw.rc8, lw.bias, w.rl, nullptr, nullptr, rt); });
+    }
     if (order == MMOE_ORDER_STEP) {
-        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16, true>, dim3(MNE * 16 / 256, nb), 256, 0, w.norm_x, nb, lw.rc16, lw.bias, w.rl, w.norm_w, hn_w); });
-        return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16>, dim3(MNE * 16 / 256, nb), 256, 0, d_hn, nb, lw.rc16, lw.bias, w.rl, nullptr, nullptr); });
+        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16, true>, dim3(MNE * 16 / 256, nb), 256, 0, w.norm_x, nb, lw.rc16, lw.bias, w.rl, w.norm_w, hn_w, RouteTail{}); });
+        return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16>, dim3(MNE * 16 / 256, nb), 256, 0, d_hn, nb, lw.rc16, lw.bias, w.rl, nullptr, nullptr, RouteTail{}); });
     }
     if (nb < 512) {   // one block per (token, 32 experts): 8 nb blocks, router reread from L2 per token
-        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<8, true>, dim3(MNE * 8 / 256, nb), 256, 0, w.norm_x, nb, lw.rc8, lw.bias, w.rl, w.norm_w, hn_w); });
-        return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<8>, dim3(MNE * 8 / 256, nb), 256, 0, d_hn, nb, lw.rc8, lw.bias, w.rl, nullptr, nullptr); });
+        if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<8, true>, dim3(MNE * 8 / 256, nb), 256, 0, w.norm_x, nb, lw.rc8, lw.bias, w.rl, w.norm_w, hn_w, RouteTail{}); });
+        return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<8>, dim3(MNE * 8 / 256, nb), 256, 0, d_hn, nb, lw.rc8, lw.bias, w.rl, nullptr, nullptr, RouteTail{}); });
     }
     if (S_router_exact || exact_only)
         return launch(MMOE_K_ROUTER, [&] { kl(k_router_gemm<4>, dim3((nb + 15) / 16, MNE / RG_BE), 256, 0, d_hn, nb, lw.rf8, lw.bias, w.rl); });
@@ -259,6 +281,7 @@ static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) 
     w.grp16 = false;
     if (!w.refine && tn == 16 && S_expert16 && nb <= E16_GRP_MAXTOK) {   // top-8 only: k_expert16 forms the grouping
         w.grp16 = true; w.grp_nb = nb; w.grp_tab = S.layers[L].tab;
+        if (w.routed) return 0;   // the router launch ran the top-8 and the quantisation
         return launch(MMOE_K_TOPK, [&] { kl(k_topk_quant, dim3((nb + 3) / 4, 2), 256, 0, w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, (int *)nullptr); });
     }
     if (w.refine) {   // exact logits of each token's candidates, then its softmax/top-8 (and the quantisation)
@@ -266,7 +289,7 @@ static int stage_route_group(Work &w, int L, int nb, int tn, const float *d_hn) 
         if (launch(MMOE_K_TOPK, [&] { kl(k_refine_topk, dim3((nb + 3) / 4, 2), 256, 0, w.rpart, d_hn, nb, lw.rc8, lw.bias, lw.w1max, w.rl, w.top, w.tw,
                                           w.hist, w.qx, w.qsx, w.qsumx); }))
             return -1;
-    } else if (launch(MMOE_K_TOPK, [&] { kl(k_topk_quant, dim3((nb + 3) / 4, 2), 256, 0, w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
+    } else if (!w.routed && launch(MMOE_K_TOPK, [&] { kl(k_topk_quant, dim3((nb + 3) / 4, 2), 256, 0, w.rl, d_hn, nb, w.top, w.tw, w.qx, w.qsx, w.qsumx, w.hist); })) return -1;
     w.hist_used = nch * MNE;   // cleared by this call's combine
     return launch(MMOE_K_GROUP, [&] {
         kl(k_group, nch, 512, 0, w.hist, nb, w.plan, S.layers[L].tab, w.eptr, tn, w.tiles, w.eu, w.top, w.tw, w.utok, w.uw,
@@ -381,7 +404,10 @@ static int moe_dev(Work &w, int L, const float *d_hn, int nb, float *d_x, int or
     if (L < 0 || L >= NLMAX || !S.layers[L].tab) { seterr("layer %d not set (mmoe_set_layer)", L); return -1; }
     if (nb <= DEC_MAXTOK && S_dec_enabled) return moe_dec(w, L, d_hn, 0, nb, d_x, order);
     int np = nb * MTOPK, tn = tile_tn(np);
-    if (stage_router(w, L, d_hn, nb, order)) return -1;
+    // below 512 tokens the router launch also runs the top-8 and the quantisation; the per-chunk counts are for
+    // k_group, which the fused small-tile kernel does without (it groups itself)
+    bool grp16 = tn == 16 && S_expert16 && nb <= E16_GRP_MAXTOK;
+    if (stage_router(w, L, d_hn, nb, order, false, S_router_tk, grp16 ? nullptr : w.hist)) return -1;
     int rc = stage_route_group(w, L, nb, tn, d_hn);
     if (!rc) rc = stage_experts(w, np, MNE, tn, true);
     if (!rc) rc = stage_combine(w, nb, d_x, order == MMOE_ORDER_STEP ? MMOE_COMBINE_STEP : MMOE_COMBINE_BATCH);
