@@ -199,6 +199,20 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
         if (it < nb) topk_wave(rl + (size_t)it * MNE, E[wv], l, R.top + it * MTOPK, R.tw + it * MTOPK);
         else quant_wave<MH, DEC_GS - 128>(hn + (size_t)(it - nb) * MH, l, qs_l[it - nb], &qsv_l[it - nb], &qsum_l[it - nb]);
     }
+    if (nb == 1 && wv == 0) {
+        // one token: the grouping is its 8 picks in ascending expert order (pair = rank), written by the top-8
+        // wave itself instead of dec_group_block (maple.c:924-938 on one token: ue = sorted picks, ustart[u] = u)
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        if (l < MTOPK) {
+            int e = R.top[l], rank = 0;
+            float w = R.tw[l];
+#pragma unroll
+            for (int j = 0; j < MTOPK; j++) rank += R.top[j] < e;
+            R.ue[rank] = e; R.ustart[rank] = rank; R.utok[rank] = 0; R.uw[rank] = w; R.sp[l] = rank; R.tp[rank] = rank;
+            if (l == 0) { R.nu = MTOPK; R.ustart[MTOPK] = MTOPK; }
+        }
+    }
     { v4i *tp4 = (v4i *)(tab + t); tp4[0] = my0; tp4[1] = my1; tp4[2] = my2; }
     __syncthreads();
     int u = blockIdx.y;
@@ -206,22 +220,16 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     int r0 = blockIdx.x * 8, row = r0 + rr;
     v4i c0, c1;
     float srow = 0.0f;   // row scales, loaded with the codes (one load per thread: no wait between two)
-    // the block's gate/up codes: for one token the used experts are its 8 picks ascending, so slot u's expert
-    // is known before the grouping and its loads are in flight meanwhile; for more tokens after it
+    // the block's gate/up codes: for one token the grouping is written by the top-8 wave (its 8 picks ascending),
+    // so slot u's expert is R.ue[u] right after the barrier; for more tokens after dec_group_block
     auto load_codes = [&](int e) {
         const ExpPtr &ex = tab[e];
         const gptr_u4 *cp = (const gptr_u4 *)((kind ? ex.uc : ex.gc) + (size_t)row * (MH / 4) + grp * 32);
         c0 = cp[0]; c1 = cp[1];
         if (t < 16) srow = *(const gptr_f *)(t < 8 ? ex.gs + r0 + t : ex.us + r0 + t - 8);
     };
-    if (nb == 1) {
-        int tv = l < MTOPK ? R.top[l] : 0x7fffffff, rank = 0;
-#pragma unroll
-        for (int j = 0; j < MTOPK; j++) rank += R.top[j] < tv;
-        int src = max(__ffsll((long long)__ballot(l < MTOPK && rank == u)) - 1, 0);   // ranks 0..7 are distinct
-        load_codes(__builtin_amdgcn_readlane(tv, src));
-    }
-    dec_group_block(nb, R);
+    if (nb == 1) load_codes(R.ue[u]);   // slot u = the u-th pick in ascending expert order (above)
+    else dec_group_block(nb, R);
     bool pub = blockIdx.x == 0 && blockIdx.y == 0;
     if (u >= R.nu && !pub) return;                    // whole block
     if (pub) {
