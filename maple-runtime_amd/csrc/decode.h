@@ -103,15 +103,8 @@ __global__ void __launch_bounds__(64) k_dec_route(const float *__restrict__ x, i
             acc = __builtin_fmaf(__uint_as_float(q2 << 16), h1.x, acc); acc = __builtin_fmaf(__uint_as_float(q2 & 0xffff0000u), h1.y, acc);
             acc = __builtin_fmaf(__uint_as_float(q3 << 16), h1.z, acc); acc = __builtin_fmaf(__uint_as_float(q3 & 0xffff0000u), h1.w, acc);
         }
-        float vv[NCH];
-        int base = l & ~(NCH - 1);
-#pragma unroll
-        for (int i = 0; i < NCH; i++) vv[i] = __shfl(acc, base + i, 64);
+        float r = hsum8_lanes<NCH>(acc);
         if (j == 0) {
-            float s8[8];
-            if (NCH == 16) { for (int i = 0; i < 8; i++) s8[i] = vv[i] + vv[i + 8]; }
-            else { for (int i = 0; i < 8; i++) s8[i] = vv[i]; }
-            float r = hsum8(s8);
             if (bias) r = r + bv;
             rl[(size_t)b * MNE + e] = r;
         }
@@ -362,8 +355,7 @@ __global__ void __launch_bounds__(256) k_dec_down(const Plan *__restrict__ plan,
         for (int a = a0; a < a1; a++) {
             const uint32_t *qd = (const uint32_t *)(&qa[a][(sl >> 1) * DEC_GS + (sl & 1) * 64]);
             int acc = dot16(cd, qd, 0);
-#pragma unroll
-            for (int o = 4; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+            acc += dpp<0xB1>(acc); acc += dpp<0x4E>(acc); acc += dpp<0x141>(acc);   // the 8 lanes of the row half
             if (sl == 0) {
                 float d = (float)(acc - qsuma[a]) * qsa[a] * sd[k];
                 Dl[a][rr] = d;

@@ -187,6 +187,17 @@ __device__ __forceinline__ float hsum8(const float *v) {
     float a0 = v[0] + v[4], a1 = v[1] + v[5], a2 = v[2] + v[6], a3 = v[3] + v[7];
     return (a0 + a1) + (a2 + a3);
 }
+// The same fold over the chain values of NCH (16 or 8) consecutive lanes of one 16-lane row, one value per
+// lane (16 chains first pair chain i with chain i + 8, as the step router does): DPP row shifts pair the same
+// operands as hsum8 (row_ror:8, then row_shl:4, 1, 2: lane i adds lane i + n), so the group's first lane holds
+// hsum8's result bit for bit. Every lane of the row must be active.
+template <int NCH>
+__device__ __forceinline__ float hsum8_lanes(float v) {
+    if (NCH == 16) v = v + __int_as_float(dpp<0x128>(__float_as_int(v)));   // row_ror:8
+    v = v + __int_as_float(dpp<0x104>(__float_as_int(v)));                   // row_shl:4
+    v = v + __int_as_float(dpp<0x101>(__float_as_int(v)));                   // row_shl:1
+    return v + __int_as_float(dpp<0x102>(__float_as_int(v)));                // row_shl:2
+}
 
 // Mid-size batches: one thread per (expert, chain) of one token, block = 256/NCH experts of token
 // blockIdx.y. The token's row sits in LDS chain-major (hc[j][m] = hn[j + NCH m]) and the router comes from
@@ -285,15 +296,8 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
             acc = __builtin_fmaf(__uint_as_float(q3 << 16), h1.z, acc); acc = __builtin_fmaf(__uint_as_float(q3 & 0xffff0000u), h1.w, acc);
         }
     }
-    float v[NCH];
-    int base = (tid & 63) & ~(NCH - 1);
-#pragma unroll
-    for (int i = 0; i < NCH; i++) v[i] = __shfl(acc, base + i, 64);
+    float r = hsum8_lanes<NCH>(acc);
     if (j == 0) {
-        float s8[8];
-        if (NCH == 16) { for (int i = 0; i < 8; i++) s8[i] = v[i] + v[i + 8]; }
-        else { for (int i = 0; i < 8; i++) s8[i] = v[i]; }
-        float r = hsum8(s8);
         if (bias) r = r + be;
         rl[(size_t)b * MNE + e] = r;
     }
@@ -933,11 +937,8 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
                 acc = __builtin_fmaf(__uint_as_float(q3 << 16), h1.z, acc); acc = __builtin_fmaf(__uint_as_float(q3 & 0xffff0000u), h1.w, acc);
             }
         }
-        float s8[8];
-#pragma unroll
-        for (int i = 0; i < 8; i++) s8[i] = __shfl(acc, (l & ~7) + i, 64);
+        float rv = hsum8_lanes<8>(acc);
         if (j == 0 && on) {
-            float rv = hsum8(s8);
             if (bias) rv = rv + be;
             row[wv][e] = rv;
         }
