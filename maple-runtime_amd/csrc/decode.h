@@ -176,6 +176,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
                                                     int *__restrict__ qsumx, float *__restrict__ act, int *__restrict__ dbg) {
     __shared__ DecRoute R;
     __shared__ __attribute__((aligned(16))) float E[4][MNE];
+    __shared__ __attribute__((aligned(16))) float Pl[MNE];   // one token: p of every expert (wave 2)
     __shared__ __attribute__((aligned(16))) int8_t qs_l[DEC_MAXTOK][MH / 128 * DEC_GS];
     __shared__ float qsv_l[DEC_MAXTOK];
     __shared__ int qsum_l[DEC_MAXTOK];
@@ -187,23 +188,44 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     const v4i *ltp = (const v4i *)(layer_tab + t);   // the layer's expert table, stored to LDS after top-8 (three
     v4i my0 = ltp[0], my1 = ltp[1], my2 = ltp[2];     // vectors: held as a struct it went to scratch memory)
 
-    // top-8 of every token and the int8 quantisation (maple.c:908-909 prep) of every token, spread over waves
-    for (int it = wv; it < 2 * nb; it += 4) {
-        if (it < nb) topk_wave(rl + (size_t)it * MNE, E[wv], l, R.top + it * MTOPK, R.tw + it * MTOPK);
-        else quant_wave<MH, DEC_GS - 128>(hn + (size_t)(it - nb) * MH, l, qs_l[it - nb], &qsv_l[it - nb], &qsum_l[it - nb]);
-    }
-    if (nb == 1 && wv == 0) {
-        // one token: the grouping is its 8 picks in ascending expert order (pair = rank), written by the top-8
-        // wave itself instead of dec_group_block (maple.c:924-938 on one token: ue = sorted picks, ustart[u] = u)
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-        if (l < MTOPK) {
-            int e = R.top[l], rank = 0;
-            float w = R.tw[l];
+    // one token: the 8 picks are selected on the logits (wave 0) while wave 2 computes the softmax and wave 1
+    // quantises x; p = exp(l - max) / sum is non-decreasing in l, so after the barrier a check against p proves the
+    // selection is maple.c's (below), and only a token that fails it (ties in p) runs the selection on p again.
+    // More tokens: top-8 (topk_wave) and quantisation (maple.c:908-923) of every token, spread over waves.
+    if (nb == 1) {
+        if (wv == 0) {
+            v4f lv = *(const gptr_f4 *)(rl + 4 * l);
+            float lg[4] = {lv.x, lv.y, lv.z, lv.w};
+            uint32_t key[4];   // order-preserving logit bits, low 2 bits replaced by 3 - slot (lower expert first)
 #pragma unroll
-            for (int j = 0; j < MTOPK; j++) rank += R.top[j] < e;
-            R.ue[rank] = e; R.ustart[rank] = rank; R.utok[rank] = 0; R.uw[rank] = w; R.sp[l] = rank; R.tp[rank] = rank;
-            if (l == 0) { R.nu = MTOPK; R.ustart[MTOPK] = MTOPK; }
+            for (int i = 0; i < 4; i++) {
+                uint32_t b = __float_as_uint(lg[i]);
+                b = (b >> 31) ? ~b : (b | 0x80000000u);
+                key[i] = (b & ~3u) | (uint32_t)(3 - i);
+            }
+            float pk[MTOPK]; int ek[MTOPK]; float ts = 0.0f;
+            topk_rounds(key, l, pk, ek, ts);
+            if (l < MTOPK) {   // the one-token grouping: picks in ascending expert order (pair = rank)
+                int e = 0, rank = 0;
+#pragma unroll
+                for (int k = 0; k < MTOPK; k++) e = l == k ? ek[k] : e;
+#pragma unroll
+                for (int k = 0; k < MTOPK; k++) rank += ek[k] < e;
+                R.top[l] = e; R.ue[rank] = e; R.ustart[rank] = rank; R.utok[rank] = 0; R.sp[l] = rank; R.tp[rank] = rank;
+                if (l == 0) { R.nu = MTOPK; R.ustart[MTOPK] = MTOPK; }
+            }
+        } else if (wv == 1) {
+            quant_wave<MH, DEC_GS - 128>(hn, l, qs_l[0], &qsv_l[0], &qsum_l[0]);
+        } else if (wv == 2) {
+            v4f lv = *(const gptr_f4 *)(rl + 4 * l);
+            float pv[4];
+            softmax_wave(make_float4(lv.x, lv.y, lv.z, lv.w), E[2], l, pv);
+            *(float4 *)(&Pl[4 * l]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
+        }
+    } else {
+        for (int it = wv; it < 2 * nb; it += 4) {
+            if (it < nb) topk_wave(rl + (size_t)it * MNE, E[wv], l, R.top + it * MTOPK, R.tw + it * MTOPK);
+            else quant_wave<MH, DEC_GS - 128>(hn + (size_t)(it - nb) * MH, l, qs_l[it - nb], &qsv_l[it - nb], &qsum_l[it - nb]);
         }
     }
     { v4i *tp4 = (v4i *)(tab + t); tp4[0] = my0; tp4[1] = my1; tp4[2] = my2; }
@@ -221,8 +243,61 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
         c0 = cp[0]; c1 = cp[1];
         if (t < 16) srow = *(const gptr_f *)(t < 8 ? ex.gs + r0 + t : ex.us + r0 + t - 8);
     };
-    if (nb == 1) load_codes(R.ue[u]);   // slot u = the u-th pick in ascending expert order (above)
-    else dec_group_block(nb, R);
+    if (nb == 1) {
+        load_codes(R.ue[u]);   // slot u = the u-th pick in ascending expert order (above)
+        // the check, by every thread alike: with the picks s_0..s_7 in logit order, p(s_0) > ... > p(s_7) and every
+        // other expert's p < p(s_7) mean the 8 largest p are s_0..s_7 in that order with no ties, i.e. maple.c's
+        // picks; otherwise (a tie in p) the selection runs again on p keys (topk_wave) and the codes are reloaded
+        int sk[MTOPK]; float ps[MTOPK];
+#pragma unroll
+        for (int k = 0; k < MTOPK; k++) sk[k] = R.top[k];
+#pragma unroll
+        for (int k = 0; k < MTOPK; k++) ps[k] = Pl[sk[k]];
+        bool dec = true;
+#pragma unroll
+        for (int k = 0; k + 1 < MTOPK; k++) dec = dec && ps[k] > ps[k + 1];
+        float4 pv = *(const float4 *)(&Pl[4 * l]);
+        float pl4[4] = {pv.x, pv.y, pv.z, pv.w}, mo = -1.0f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bool picked = false;
+#pragma unroll
+            for (int k = 0; k < MTOPK; k++) picked = picked || sk[k] == 4 * l + i;
+            mo = picked ? mo : fmaxf(mo, pl4[i]);
+        }
+        mo = wave_max(mo);
+        if (!(dec && ps[MTOPK - 1] > mo)) {   // uniform: every wave computes the same values
+            __syncthreads();                  // all reads of R.top above are done
+            if (wv == 0) {
+                v4f lv = *(const gptr_f4 *)(rl + 4 * l);
+                topk_wave_v(make_float4(lv.x, lv.y, lv.z, lv.w), E[0], l, R.top, R.tw);
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+                if (l < MTOPK) {
+                    int e = R.top[l], rank = 0;
+#pragma unroll
+                    for (int j = 0; j < MTOPK; j++) rank += R.top[j] < e;
+                    R.ue[rank] = e; R.uw[rank] = R.tw[l]; R.sp[l] = rank;
+                }
+            }
+            __syncthreads();
+            load_codes(R.ue[u]);
+        } else if (blockIdx.x == 0 && blockIdx.y == 0) {   // the publishing block: weights in pick order
+            if (wv == 0 && l < MTOPK) {
+                float tsum = 0.0f;
+#pragma unroll
+                for (int k = 0; k < MTOPK; k++) tsum = tsum + ps[k];
+                float w = 0.0f;
+#pragma unroll
+                for (int k = 0; k < MTOPK; k++) w = l == k ? ps[k] : w;
+                w = w / (tsum + 1e-20f);
+                R.tw[l] = w; R.uw[R.sp[l]] = w;
+            }
+            __syncthreads();
+        }
+    } else {
+        dec_group_block(nb, R);
+    }
     bool pub = blockIdx.x == 0 && blockIdx.y == 0;
     if (u >= R.nu && !pub) return;                    // whole block
     if (pub) {

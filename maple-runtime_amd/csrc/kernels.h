@@ -562,7 +562,9 @@ __global__ void __launch_bounds__(256) k_router_l1max(const uint16_t *__restrict
 // holds the lowest expert index with it, and that lane's best key names it: the pick order of maple.c's
 // repeated strict-> scans, ties included.
 // topk_wave_v takes the lane's 4 logits; topk_wave loads them from a row in global memory.
-__device__ __forceinline__ int topk_wave_v(float4 lv, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
+// maple.c's softmax (maple.c:608-610) of the wave's token: p of the lane's 4 experts 4l .. 4l+3 (E: 256 floats of
+// LDS scratch).
+__device__ __forceinline__ void softmax_wave(float4 lv, float *E, int l, float *pv) {
     float lg[4] = {lv.x, lv.y, lv.z, lv.w};
     float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
     mx = wave_max(mx);
@@ -580,15 +582,16 @@ __device__ __forceinline__ int topk_wave_v(float4 lv, float *E, int l, int *__re
 #pragma unroll
         for (int m = 0; m < MNE / 8; m++) part = part + ev[m];
     }
-    float pv[8];
+    float p8[8];
 #pragma unroll
-    for (int i = 0; i < 8; i++) pv[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), i));
-    float sum = hsum8(pv);
-    uint32_t key[4];
+    for (int i = 0; i < 8; i++) p8[i] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), i));
+    float sum = hsum8(p8);
 #pragma unroll
-    for (int i = 0; i < 4; i++) key[i] = ((__float_as_uint(lg[i] / sum) + 1u) << 2) | (uint32_t)(3 - i);
-    float pk[MTOPK]; int ek[MTOPK];
-    float tsum = 0.0f;
+    for (int i = 0; i < 4; i++) pv[i] = lg[i] / sum;
+}
+// The 8 selection rounds on 32-bit keys whose low 2 bits are 3 - slot (key 0 = taken): picks in order (ek) and,
+// for p keys ((p_bits + 1) << 2 | (3 - slot)), their p (pk) and the sum of picked p in pick order (tsum).
+__device__ __forceinline__ void topk_rounds(uint32_t *key, int l, float *pk, int *ek, float &tsum) {
 #pragma unroll
     for (int k = 0; k < MTOPK; k++) {
         uint32_t b = max(max(key[0], key[1]), max(key[2], key[3]));
@@ -611,6 +614,16 @@ __device__ __forceinline__ int topk_wave_v(float4 lv, float *E, int l, int *__re
             for (int i = 0; i < 4; i++) key[i] = key[i] == mL ? 0u : key[i];
         }
     }
+}
+__device__ __forceinline__ int topk_wave_v(float4 lv, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
+    float pv[4];
+    softmax_wave(lv, E, l, pv);
+    uint32_t key[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) key[i] = ((__float_as_uint(pv[i]) + 1u) << 2) | (uint32_t)(3 - i);
+    float pk[MTOPK]; int ek[MTOPK];
+    float tsum = 0.0f;
+    topk_rounds(key, l, pk, ek, tsum);
     if (l == 0) {
 #pragma unroll
         for (int k = 0; k < MTOPK; k++) { top[k] = ek[k]; tw[k] = pk[k] / (tsum + 1e-20f); }
