@@ -307,6 +307,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-decode", action="store_true", help="skip the config-1 decode timing (development runs)")
     ap.add_argument("--no-full", action="store_true", help="skip config 4 (24 whole layers with attention)")
+    ap.add_argument("--no-floor", action="store_true",
+                    help="skip the decode-floor probe (libmaplefloor); profiled runs leave it out")
     ap.add_argument("--graph", type=int, default=1, help="replay the 24-layer decode as a HIP graph")
     ap.add_argument("--router", choices=["exact", "mfma"], default="mfma",
                     help="router of the 2048-token prefill: bf16 MFMA logits with each token's near-top-8 experts recomputed "
@@ -385,7 +387,7 @@ def main():
     # ---- the floor under the decode layer: 3 x 24 dependent kernels at the decode grid shapes, one HIP graph
     floor = None
     fpath = os.path.join(ROOT, "maple-runtime_amd", "libmaplefloor.so")
-    if not args.no_decode and os.path.exists(fpath):
+    if not args.no_decode and not args.no_floor and os.path.exists(fpath):
         fl = C.CDLL(fpath)
         fl.floor_layer_us.restype, fl.floor_layer_us.argtypes = C.c_double, [C.c_int, C.c_int, C.c_int]
         fv = [fl.floor_layer_us(f, NL, 200) for f in (0, 1, 2)]
