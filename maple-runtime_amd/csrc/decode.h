@@ -195,16 +195,8 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
     if (nb == 1) {
         if (wv == 0) {
             v4f lv = *(const gptr_f4 *)(rl + 4 * l);
-            float lg[4] = {lv.x, lv.y, lv.z, lv.w};
-            uint32_t key[4];   // order-preserving logit bits, low 2 bits replaced by 3 - slot (lower expert first)
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                uint32_t b = __float_as_uint(lg[i]);
-                b = (b >> 31) ? ~b : (b | 0x80000000u);
-                key[i] = (b & ~3u) | (uint32_t)(3 - i);
-            }
-            float pk[MTOPK]; int ek[MTOPK]; float ts = 0.0f;
-            topk_rounds(key, l, pk, ek, ts);
+            int ek[MTOPK];
+            topk_logit_rounds(make_float4(lv.x, lv.y, lv.z, lv.w), l, ek);
             if (l < MTOPK) {   // the one-token grouping: picks in ascending expert order (pair = rank)
                 int e = 0, rank = 0;
 #pragma unroll
@@ -251,22 +243,7 @@ __global__ void __launch_bounds__(256) k_dec_gateup(const float *__restrict__ rl
         int sk[MTOPK]; float ps[MTOPK];
 #pragma unroll
         for (int k = 0; k < MTOPK; k++) sk[k] = R.top[k];
-#pragma unroll
-        for (int k = 0; k < MTOPK; k++) ps[k] = Pl[sk[k]];
-        bool dec = true;
-#pragma unroll
-        for (int k = 0; k + 1 < MTOPK; k++) dec = dec && ps[k] > ps[k + 1];
-        float4 pv = *(const float4 *)(&Pl[4 * l]);
-        float pl4[4] = {pv.x, pv.y, pv.z, pv.w}, mo = -1.0f;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            bool picked = false;
-#pragma unroll
-            for (int k = 0; k < MTOPK; k++) picked = picked || sk[k] == 4 * l + i;
-            mo = picked ? mo : fmaxf(mo, pl4[i]);
-        }
-        mo = wave_max(mo);
-        if (!(dec && ps[MTOPK - 1] > mo)) {   // uniform: every wave computes the same values
+        if (!picks_exact(sk, Pl, l, ps)) {   // uniform: every wave computes the same values
             __syncthreads();                  // all reads of R.top above are done
             if (wv == 0) {
                 v4f lv = *(const gptr_f4 *)(rl + 4 * l);

@@ -211,6 +211,7 @@ __device__ __forceinline__ float hsum8_lanes(float v) {
 // the top-8 / quantisation outputs of a router launch that also routes its tokens (TK); defined further down:
 struct RouteTail { int *top; float *tw; int8_t *qx; float *qsx; int *qsumx; int *hist; int *cnt; };
 __device__ __forceinline__ int topk_wave(const float *__restrict__ r, float *E, int l, int *__restrict__ top, float *__restrict__ tw);
+
 template <int N, int GPAD = 0>
 __device__ __forceinline__ void quant_wave(const float *__restrict__ xr, int l, int8_t *__restrict__ q, float *__restrict__ qs,
                                            int *__restrict__ qsum);
@@ -614,6 +615,42 @@ __device__ __forceinline__ void topk_rounds(uint32_t *key, int l, float *pk, int
             for (int i = 0; i < 4; i++) key[i] = key[i] == mL ? 0u : key[i];
         }
     }
+}
+// Selection on the logits themselves (no softmax first): keys are the order-preserving bits of each logit with the
+// low 2 bits replaced by 3 - slot, so the lower expert comes first among keys that tie. ek: the 8 picks in order.
+__device__ __forceinline__ void topk_logit_rounds(float4 lv, int l, int *ek) {
+    float lg[4] = {lv.x, lv.y, lv.z, lv.w};
+    uint32_t key[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t b = __float_as_uint(lg[i]);
+        b = (b >> 31) ? ~b : (b | 0x80000000u);
+        key[i] = (b & ~3u) | (uint32_t)(3 - i);
+    }
+    float pk[MTOPK]; float ts = 0.0f;
+    topk_rounds(key, l, pk, ek, ts);
+}
+// Whether picks sk[0..7] taken on the logits are maple.c's picks on p (P: the token's 256 p in LDS). p = exp(l - max)
+// / sum does not decrease with the logit, so p(s_0) > ... > p(s_7) > every other expert's p means the 8 largest p
+// are s_0..s_7 in that order with no ties: exactly what maple.c's strict-> scans select. A tie in p (distinct
+// logits may round to one p) fails the check. ps: p of the picks. The result is uniform over the wave.
+__device__ __forceinline__ bool picks_exact(const int *sk, const float *P, int l, float *ps) {
+#pragma unroll
+    for (int k = 0; k < MTOPK; k++) ps[k] = P[sk[k]];
+    bool dec = true;
+#pragma unroll
+    for (int k = 0; k + 1 < MTOPK; k++) dec = dec && ps[k] > ps[k + 1];
+    float4 pv = *(const float4 *)(&P[4 * l]);
+    float pl4[4] = {pv.x, pv.y, pv.z, pv.w}, mo = -1.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        bool picked = false;
+#pragma unroll
+        for (int k = 0; k < MTOPK; k++) picked = picked || sk[k] == 4 * l + i;
+        mo = picked ? mo : fmaxf(mo, pl4[i]);
+    }
+    mo = wave_max(mo);
+    return dec && ps[MTOPK - 1] > mo;
 }
 __device__ __forceinline__ int topk_wave_v(float4 lv, float *E, int l, int *__restrict__ top, float *__restrict__ tw) {
     float pv[4];

@@ -285,15 +285,19 @@ def test_moe_batch_mfma_router(layer0):
         M.check(lib.mmoe_set_router_mode(0), "router mode")
 
 
-@pytest.fixture(scope="module", params=[52, 253])
+@pytest.fixture(scope="module", params=[52, 253, "round"])
 def tie_layer(request):
     """Layers 19 and 20: router weights all zero and a bias with large tie classes, so every logit is its expert's
     bias exactly: 3 distinct leaders, then a class of equal logits across the 8th place. Layer 19: 52 experts
     (e * 37 % 5 == 4); layer 20: the 253 other experts all equal (every lane holds four tied experts, so each
-    pick after the third must find the lowest lane and, inside it, the lowest slot)."""
+    pick after the third must find the lowest lane and, inside it, the lowest slot).
+    Layer 21 ("round"): leaders 0.03, 0.02, 0.015, every other logit 0 except expert 200 at 1e-30. Its logit is
+    the 4th largest, but 1e-30 - 0.03 rounds to -0.03, so its p equals the tied class's and maple.c takes the
+    lowest experts 0, 1, 2, 4, 5 first: a selection on logits alone picks 200, and only the check against p
+    (then a selection on p) gives maple.c's picks."""
     lib = M.lib()
     M.check(lib.mmoe_init(2048), "mmoe_init")
-    L = 19 if request.param == 52 else 20
+    L = {52: 19, 253: 20, "round": 21}[request.param]
     hl = HostLayer(SEED, L)
     hl.router = np.zeros((256, 2048), np.uint16)
     hl.rid = M.register_layer(L, hl.blk, hl.router)
@@ -303,7 +307,10 @@ def tie_layer(request):
     else:
         hl.bias = np.zeros(256, np.float32)
         hl.want = [250, 3, 180, 0, 1, 2, 4, 5]
-    hl.bias[[250, 3, 180]] = [3.0, 2.5, 2.25]
+    if request.param == "round":
+        hl.bias[[250, 3, 180, 200]] = [0.03, 0.02, 0.015, 1e-30]
+    else:
+        hl.bias[[250, 3, 180]] = [3.0, 2.5, 2.25]
     M.check(lib.mmoe_set_bias(L, M.ptr(hl.bias)), "bias")
     yield hl
     M.check(lib.mmoe_set_bias(L, None), "bias off")
