@@ -443,6 +443,7 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ h
 // router chunk (bf16) and the input chunk (fp32) are read with coalesced 16-byte loads into registers two
 // chunks ahead, then stored to LDS (the input as its three bf16 parts; rows padded to 72 bf16).
 #define RM_KC 64
+#define RM_PF 2   // router chunks loaded ahead (registers); 4 and 8 measured slower
 #define RM_LR 72
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -466,8 +467,12 @@ __global__ void __launch_bounds__(WAVES * 64) k_router_mfma(const uint16_t *__re
     constexpr int NT = WAVES * 64, ER = 32 * WAVES * EW;
     constexpr int NW = ER * 8 / NT;              // router pieces (16 bytes) staged per thread: rows wrow + (NT / 8) i
     constexpr int NH = 32 * 16 / NT;             // input pieces (4 floats) per thread: rows hrow + (NT / 16) i
-    __shared__ __attribute__((aligned(16))) uint16_t ws[ER * RM_LR];
-    __shared__ __attribute__((aligned(16))) uint16_t hsl[3][32 * RM_LR];
+    // LDS stages (2 for the 8-wave block, one per CU anyway; 1 for the 4-wave block, several per CU): chunk ck
+    // is stored to stage ck % NB, so with 2 stages one barrier per chunk suffices (a stage is rewritten two chunks
+    // later, after every wave has passed the barrier of the chunk in between)
+    constexpr int NB = WAVES == 8 ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) uint16_t ws_[NB][ER * RM_LR];
+    __shared__ __attribute__((aligned(16))) uint16_t hsl_[NB][3][32 * RM_LR];
     int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, r = l & 31, kg = l >> 5;
     int e0 = blockIdx.y * ER, t0 = blockIdx.x * 32, kq = blockIdx.z * (MH / 4);
     int wrow = tid >> 3, wpc = tid & 7, hrow = tid >> 4, hq = tid & 15;
@@ -475,19 +480,22 @@ __global__ void __launch_bounds__(WAVES * 64) k_router_mfma(const uint16_t *__re
     const float *hsrc[NH];
 #pragma unroll
     for (int i = 0; i < NH; i++) hsrc[i] = hn + (size_t)min(t0 + hrow + (NT / 16) * i, nb - 1) * MH + kq + hq * 4;
-    v4i rw[2][NW], rh[2][NH];
+    constexpr int NCK = MH / 4 / RM_KC;          // chunks of this column quarter
+    v4i rw[RM_PF][NW], rh[RM_PF][NH];            // chunk ck in slot ck % RM_PF, loaded RM_PF chunks ahead
 #define RMW_LOAD(q_, k_)                                                                                 {                                                                                                        _Pragma("unroll") for (int i = 0; i < NW; i++)                                                           rw[q_][i] = *(const gptr_u4 *)(wsrc + (size_t)(NT / 8) * i * MH + (k_));                         _Pragma("unroll") for (int i = 0; i < NH; i++) rh[q_][i] = *(const gptr_u4 *)(hsrc[i] + (k_));     }
-    RMW_LOAD(0, 0);
-    RMW_LOAD(1, RM_KC);
+#pragma unroll
+    for (int c = 0; c < RM_PF; c++) RMW_LOAD(c, c * RM_KC);
     f32x16 acc[EW];
 #pragma unroll
     for (int f = 0; f < EW; f++)
 #pragma unroll
         for (int i = 0; i < 16; i++) acc[f][i] = 0.0f;
-#pragma unroll 2
-    for (int ck = 0; ck < MH / 4 / RM_KC; ck++) {
-        const int q = ck & 1;
-        __syncthreads();
+#pragma unroll
+    for (int ck = 0; ck < NCK; ck++) {
+        const int q = ck % RM_PF;
+        uint16_t *ws = ws_[ck % NB];
+        uint16_t (*hsl)[32 * RM_LR] = hsl_[ck % NB];
+        if (NB == 1) __syncthreads();
 #pragma unroll
         for (int i = 0; i < NW; i++) *(v4i *)(&ws[(wrow + (NT / 8) * i) * RM_LR + wpc * 8]) = rw[q][i];
 #pragma unroll
@@ -498,7 +506,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_router_mfma(const uint16_t *__re
             *(uint2 *)(&hsl[0][o]) = p1; *(uint2 *)(&hsl[1][o]) = p2; *(uint2 *)(&hsl[2][o]) = p3;
         }
         __syncthreads();
-        if (ck + 2 < MH / 4 / RM_KC) RMW_LOAD(q, (ck + 2) * RM_KC);
+        if (ck + RM_PF < NCK) RMW_LOAD(q, (ck + RM_PF) * RM_KC);
         f32x16 cacc[EW];
 #pragma unroll
         for (int f = 0; f < EW; f++)
