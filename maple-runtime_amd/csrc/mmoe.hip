@@ -104,6 +104,7 @@ struct LayerW { ExpPtr *tab = nullptr; uint16_t *router = nullptr; uint16_t *rc1
 
 static struct {
     bool ready = false;
+    ExpPtr *zero_tab = nullptr;     // mmoe_route: the expert table k_group reads when no layer is involved
     hipStream_t st = nullptr;
     Work main;                 // gpre / gfull / mmoe
     Work dec;                  // gpux
@@ -946,6 +947,43 @@ int mmoe_moe(int L, const float *hn, int nb, float *x, int order) {
 }
 
 int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) { return moe_dev(S.main, L, d_hn, nb, d_x, order); }
+
+// maple.c's softmax/top-8 (job_topk, maple.c:910-922) and grouping (group_pairs, maple.c:924-938, plus the tp table
+// its callers build before gpre_moe / gfull_moe, maple.c:762 and 1019) of nb tokens' logits, on the device: the top-8
+// kernel (its quantisation row of blocks left out) and k_group, which also fill the plan and tiles the expert
+// kernels would use. k_group publishes the used experts' pointers from a layer table: routing alone has no layer,
+// so a zeroed table stands in.
+int mmoe_route(const float *rl, int nb, int *top, float *tw, int *ue, int *ustart, int *utok, float *uw, int *tp) {
+    Work &w = S.main;
+    if (!w.maxtok) { seterr("mmoe_route before mmoe_init"); return -1; }
+    if (!rl) { seterr("mmoe_route: no logits"); return -1; }
+    if (nb < 1 || nb > w.maxtok) { seterr("mmoe_route: nb %d outside 1..%d", nb, w.maxtok); return -1; }
+    if (!S.zero_tab) {
+        HC(hipMalloc(&S.zero_tab, sizeof(ExpPtr) * MNE));
+        HC(hipMemset(S.zero_tab, 0, sizeof(ExpPtr) * MNE));
+    }
+    const int nch = (nb + 63) / 64, P = nb * MTOPK;
+    HC(hipMemcpyAsync(w.rl, rl, (size_t)nb * MNE * 4, hipMemcpyHostToDevice, S.st));
+    if (launch(MMOE_K_TOPK, [&] { kl(k_topk_quant, dim3((nb + 3) / 4, 1), 256, 0, (const float *)w.rl, (const float *)nullptr, nb, w.top, w.tw,
+                                     (int8_t *)nullptr, (float *)nullptr, (int *)nullptr, w.hist); }))
+        return -1;
+    int rc = launch(MMOE_K_GROUP, [&] { kl(k_group, nch, 512, 0, w.hist, nb, w.plan, S.zero_tab, w.eptr, 64, w.tiles, w.eu, w.top, w.tw, w.utok,
+                                           w.uw, w.tp, w.sp, w.pu); });
+    kl(k_fill_zero, (nch * MNE + 255) / 256, 256, 0, w.hist, nch * MNE);   // the per-chunk counts, for the next call
+    if (rc) { (void)hipGetLastError(); return -1; }
+    HC(hipGetLastError());
+    static Plan pl;
+    HC(hipMemcpyAsync(&pl, w.plan, sizeof(Plan), hipMemcpyDeviceToHost, S.st));
+    if (top) HC(hipMemcpyAsync(top, w.top, (size_t)P * 4, hipMemcpyDeviceToHost, S.st));
+    if (tw) HC(hipMemcpyAsync(tw, w.tw, (size_t)P * 4, hipMemcpyDeviceToHost, S.st));
+    if (utok) HC(hipMemcpyAsync(utok, w.utok, (size_t)P * 4, hipMemcpyDeviceToHost, S.st));
+    if (uw) HC(hipMemcpyAsync(uw, w.uw, (size_t)P * 4, hipMemcpyDeviceToHost, S.st));
+    if (tp) HC(hipMemcpyAsync(tp, w.tp, (size_t)P * 4, hipMemcpyDeviceToHost, S.st));
+    HC(hipStreamSynchronize(S.st));
+    if (ue) memcpy(ue, pl.ue, sizeof(int) * pl.nu);
+    if (ustart) memcpy(ustart, pl.ustart, sizeof(int) * (pl.nu + 1));
+    return pl.nu;
+}
 
 // mmoe_moe_dev for batches of up to MMOE_NOALLOC_MAXTOK tokens with every work buffer in the library's static
 // scratch: no allocation of any kind. Calls on one device share that scratch (and queue on one stream).

@@ -76,6 +76,7 @@ def _declare(L):
         "gpu_head_init": (i, [vp, i, i]),
         "mmoe_init": (i, [i]), "mmoe_set_layer": (i, [i, vp, vp, vp, vp]), "mmoe_set_bias": (i, [i, vp]),
         "mmoe_moe": (i, [i, vp, i, vp, i]), "mmoe_moe_dev": (i, [i, vp, i, vp, i]), "mmoe_moe_dev_noalloc": (i, [i, vp, i, vp, i]),
+        "mmoe_route": (i, [vp, i, vp, vp, vp, vp, vp, vp, vp]),
         "mmoe_rmsnorm_dev": (i, [vp, vp, i, vp]), "mmoe_stack_dev": (i, [i, i, vp, i, i]),
         "mmoe_stack_graph": (i, [i, i, vp, i, i, i]), "mmoe_graph_reset": (i, []), "mmoe_graph_held": (i, []),
         "mmoe_gfull_setup": (i, [i]), "mmoe_gfull_post_norm": (i, [i, vp]), "mmoe_gfull_stack": (i, [i, i]),
