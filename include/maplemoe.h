@@ -132,8 +132,10 @@ int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order);
 int mmoe_moe_dev_noalloc(int L, const float *d_hn, int nb, float *d_x, int order);
 /* Routing only, in place of maple.c's job_topk + group_pairs (maple.c:910-938) and the tp table its callers
  * build (maple.c:762, 1019), for a caller that keeps its own gpre_moe / gfull_moe (maple.c:763, 1021): rl[nb][256]
- * router logits (host) -> maple.c's TOPB/TWB (top[nb][8], tw[nb][8]: softmax, the 8 largest p in pick order,
- * renormalised), the pairs grouped by expert (ue[nu] used experts ascending, ustart[nu+1], utok[nb*8] and
+ * router logits (host), or NULL for the logits the last router call left on the device (gfull_attn,
+ * mmoe_gfull_post_norm, and mmoe_moe* when every logit was computed exactly: below 512 tokens or with
+ * mmoe_set_router_mode(1)); NULL is refused with -1 unless that call covered exactly nb tokens.
+ * -> maple.c's TOPB/TWB (top[nb][8], tw[nb][8]: softmax, the 8 largest p in pick order, renormalised), the pairs grouped by expert (ue[nu] used experts ascending, ustart[nu+1], utok[nb*8] and
  * uw[nb*8] = UTOK/UW) and tp[nb][8] (each token's pair ids, ascending). Any output may be NULL. Synchronous;
  * returns nu, or -1 (mmoe_last_error). nb <= mmoe_init's maxtok. */
 int mmoe_route(const float *rl, int nb, int *top, float *tw, int *ue, int *ustart, int *utok, float *uw, int *tp);

@@ -81,6 +81,7 @@ struct Work {
     int grp_nb = 0;
     const ExpPtr *grp_tab = nullptr;
     bool refine = false;            // the last router call left approximate logits for k_refine_topk
+    int rl_nb = 0;                  // rl holds exact logits of this many tokens (last router call), else 0
 };
 
 // Where a Work set's buffers come from: hipMalloc (c == nullptr) or a fixed device span carved in order
@@ -241,8 +242,7 @@ static bool S_router_tk = ROUTER_TK;   // batches below 512: top-8 and quantisat
 // exact_only: never the approximate large-batch router (callers that hand the logits themselves to the host)
 // tk (batches below 512 tokens): the router launch also runs each token's softmax/top-8 (per-chunk counts into
 // hist unless hist is null) and its int8 quantisation, in the last of the token's router blocks
-static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bool exact_only = false, bool tk = false,
-                        int *hist = nullptr) {
+static int stage_router_launch(Work &w, int L, const float *d_hn, int nb, int order, bool exact_only, bool tk, int *hist) {
     LayerW &lw = S.layers[L];
     w.refine = false;
     w.routed = false;
@@ -274,6 +274,15 @@ static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bo
     w.refine = true;
     if (nb >= 1024) return launch(MMOE_K_ROUTER, [&] { kl(k_router_mfma<8, 1>, dim3((nb + 31) / 32, MNE / 256, 4), 512, 0, lw.router, d_hn, nb, w.rpart); });
     return launch(MMOE_K_ROUTER, [&] { kl(k_router_mfma<4, 1>, dim3((nb + 31) / 32, MNE / 128, 4), 256, 0, lw.router, d_hn, nb, w.rpart); });
+}
+
+// the router launch, recording whether rl now holds every logit exactly (mmoe_route may then take them as they are)
+static int stage_router(Work &w, int L, const float *d_hn, int nb, int order, bool exact_only = false, bool tk = false,
+                        int *hist = nullptr) {
+    w.rl_nb = 0;
+    int rc = stage_router_launch(w, L, d_hn, nb, order, exact_only, tk, hist);
+    if (!rc && !w.refine) w.rl_nb = nb;
+    return rc;
 }
 
 // softmax/top-8, the int8 quantisation of hn and the grouping of nb tokens; eptr filled from layer L's table
@@ -390,11 +399,13 @@ static int launch_dec_down(Work &w, int nb, float *d_x, int order) {
 static int moe_dec(Work &w, int L, const float *in, int do_norm, int nb, float *d_x, int order) {
     LayerW &lw = S.layers[L];
     const uint16_t *pln = do_norm ? lw.post_ln : nullptr;
+    w.rl_nb = 0;
     if (order == MMOE_ORDER_STEP) {
         if (launch(MMOE_K_ROUTER, [&] { kl(k_dec_route<16>, MNE * 16 / 64, 64, 0, in, nb, pln, do_norm, lw.rc16, lw.bias, w.hn, w.rl); })) return -1;
     } else {
         if (launch(MMOE_K_ROUTER, [&] { kl(k_dec_route<8>, MNE * 8 / 64, 64, 0, in, nb, pln, do_norm, lw.rc8, lw.bias, w.hn, w.rl); })) return -1;
     }
+    w.rl_nb = nb;
     if (launch_dec_gateup(w, nb, L)) return -1;
     return launch_dec_down(w, nb, d_x, order);
 }
@@ -952,18 +963,22 @@ int mmoe_moe_dev(int L, const float *d_hn, int nb, float *d_x, int order) { retu
 // its callers build before gpre_moe / gfull_moe, maple.c:762 and 1019) of nb tokens' logits, on the device: the top-8
 // kernel (its quantisation row of blocks left out) and k_group, which also fill the plan and tiles the expert
 // kernels would use. k_group publishes the used experts' pointers from a layer table: routing alone has no layer,
-// so a zeroed table stands in.
+// so a zeroed table stands in. rl = NULL takes the logits already in the work set's rl (exact ones only, of nb tokens):
+// after gfull_attn(L, glob, NULL) the chunk's routing then needs no logits on the host at all.
 int mmoe_route(const float *rl, int nb, int *top, float *tw, int *ue, int *ustart, int *utok, float *uw, int *tp) {
     Work &w = S.main;
     if (!w.maxtok) { seterr("mmoe_route before mmoe_init"); return -1; }
-    if (!rl) { seterr("mmoe_route: no logits"); return -1; }
     if (nb < 1 || nb > w.maxtok) { seterr("mmoe_route: nb %d outside 1..%d", nb, w.maxtok); return -1; }
+    if (!rl && w.rl_nb != nb) {
+        seterr("mmoe_route: no logits given and the last router call did not leave exact logits of %d tokens", nb);
+        return -1;
+    }
     if (!S.zero_tab) {
         HC(hipMalloc(&S.zero_tab, sizeof(ExpPtr) * MNE));
         HC(hipMemset(S.zero_tab, 0, sizeof(ExpPtr) * MNE));
     }
     const int nch = (nb + 63) / 64, P = nb * MTOPK;
-    HC(hipMemcpyAsync(w.rl, rl, (size_t)nb * MNE * 4, hipMemcpyHostToDevice, S.st));
+    if (rl) { HC(hipMemcpyAsync(w.rl, rl, (size_t)nb * MNE * 4, hipMemcpyHostToDevice, S.st)); w.rl_nb = nb; }
     if (launch(MMOE_K_TOPK, [&] { kl(k_topk_quant, dim3((nb + 3) / 4, 1), 256, 0, (const float *)w.rl, (const float *)nullptr, nb, w.top, w.tw,
                                      (int8_t *)nullptr, (float *)nullptr, (int *)nullptr, w.hist); }))
         return -1;

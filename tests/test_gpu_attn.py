@@ -92,7 +92,9 @@ def test_gfull_whole_layers(gfull_model):
     """maple.c's step_batch_card (maple.c:1001-1031): per layer gfull_attn, top-8 and grouping on the host from
     the card's logits, gfull_moe; two chunks through layers 0 (local) and 3 (global). As maple.c's GFULL_CHECK
     (maple.c:940-1000) each layer is checked from the card's own input: the oracle's attention half, then its
-    MoE block on rmsnorm(x, post_ln) with the same top-8."""
+    MoE block on rmsnorm(x, post_ln) with the same top-8. The second chunk routes on the card instead
+    (gfull_attn without a logits copy, then mmoe_route on the device logits, in place of maple.c's job_topk and
+    group_pairs) and hands gfull_moe the tables mmoe_route returned."""
     lib, layers, post, routers, cs = gfull_model[:5]
     blocks = [HostLayer(SEED, k) for k in range(2)]                  # experts of even / odd layers
     rids = [lib.gpre_region(M.ptr(h.blk), h.blk.nbytes) for h in blocks]
@@ -107,10 +109,20 @@ def test_gfull_whole_layers(gfull_model):
             k = L % 2
             xin = np.empty((nb, H), np.float32)
             lib.gfull_read(M.ptr(xin), None)
-            rl = np.empty((nb, 256), np.float32)
-            assert lib.gfull_attn(L, glob, M.ptr(rl)) >= 0, lib.mmoe_last_error()
-            top, tw = O.topk(rl)
-            g = O.group(top, tw)
+            if pos0 == 0:
+                rl = np.empty((nb, 256), np.float32)
+                assert lib.gfull_attn(L, glob, M.ptr(rl)) >= 0, lib.mmoe_last_error()
+                top, tw = O.topk(rl)
+                g = O.group(top, tw)
+            else:
+                assert lib.gfull_attn(L, glob, None) >= 0, lib.mmoe_last_error()
+                rl = M.read("LOGITS", (nb, 256), np.float32)
+                top = np.empty((nb, 8), np.int32); tw = np.empty((nb, 8), np.float32)
+                ue = np.empty(256, np.int32); us = np.empty(257, np.int32)
+                utok = np.empty(nb * 8, np.int32); uw = np.empty(nb * 8, np.float32); tpr = np.empty((nb, 8), np.int32)
+                nu = lib.mmoe_route(None, nb, M.ptr(top), M.ptr(tw), M.ptr(ue), M.ptr(us), M.ptr(utok), M.ptr(uw), M.ptr(tpr))
+                assert nu > 0, lib.mmoe_last_error()
+                g = dict(nu=nu, ue=ue[:nu].copy(), ustart=us[:nu + 1].copy(), utok=utok, uw=uw, tp=tpr)
             loc = M.block_loc(0, list(g["ue"]))
             regs = np.array([rids[k], -1, -1, -1], np.int32)
             tp = np.ascontiguousarray(g["tp"])
@@ -125,6 +137,9 @@ def test_gfull_whole_layers(gfull_model):
             o = O.moe_batch(hn, routers[k], blocks[k].table, xo, want=("rl", "top", "tw", "nu", "ue", "ustart", "utok", "uw", "tp"))
             assert np.array_equal(rl.view(np.uint32), o["rl"].view(np.uint32)), "router logits"
             assert np.array_equal(top, o["top"]), "top-8"
+            if pos0:   # the card's routing tables, as maple.c's group_pairs forms them
+                assert g["nu"] == o["nu"] and np.array_equal(g["ustart"], np.ravel(o["ustart"])[:g["nu"] + 1]) and np.array_equal(g["utok"], o["utok"])
+                assert np.array_equal(g["uw"].view(np.uint32), o["uw"].view(np.uint32)) and np.array_equal(g["tp"].ravel(), np.ravel(o["tp"]))
             e = relmax(xg - xin, xo - xin)
             print(f"\n  pos0={pos0} nb={nb} layer {L}: {g['nu']} experts, x bit-exact {np.array_equal(xg, xo)}, relmax {e:.1e}",
                   flush=True)

@@ -65,7 +65,9 @@ def test_route_null_outputs_and_limits(ctx):
     assert nu > 0 and np.array_equal(top, O.topk(rl)[0])
     assert lib.mmoe_route(M.ptr(rl), 0, None, None, None, None, None, None, None) == -1 and b"nb" in lib.mmoe_last_error()
     assert lib.mmoe_route(M.ptr(rl), 4096, None, None, None, None, None, None, None) == -1
-    assert lib.mmoe_route(None, 40, None, None, None, None, None, None, None) == -1
+    # no logits: the ones the call above uploaded stay on the device (40 tokens), none of 41
+    assert lib.mmoe_route(None, 40, None, None, None, None, None, None, None) == nu
+    assert lib.mmoe_route(None, 41, None, None, None, None, None, None, None) == -1
 
 
 def test_route_between_layer_calls(ctx):
@@ -79,3 +81,63 @@ def test_route_between_layer_calls(ctx):
     M.check(lib.mmoe_moe(3, M.ptr(hn), 200, M.ptr(x), M.ORDER_BATCH), "moe")
     for s in (11, 12):
         check_route(np.random.default_rng(s).standard_normal((257, 256)).astype(np.float32))
+
+
+def route_dev(nb):
+    """mmoe_route on the logits the last router call left on the device (rl = NULL)"""
+    lib = M.lib()
+    P = nb * 8
+    top = np.full((nb, 8), -1, np.int32); tw = np.zeros((nb, 8), np.float32)
+    ue = np.full(256, -1, np.int32); us = np.full(257, -1, np.int32)
+    utok = np.full(P, -1, np.int32); uw = np.zeros(P, np.float32); tp = np.full((nb, 8), -1, np.int32)
+    nu = lib.mmoe_route(None, nb, M.ptr(top), M.ptr(tw), M.ptr(ue), M.ptr(us), M.ptr(utok), M.ptr(uw), M.ptr(tp))
+    return nu, dict(top=top, tw=tw, ue=ue[:max(nu, 0)], ustart=us[:max(nu, 0) + 1], utok=utok, uw=uw, tp=tp)
+
+
+@pytest.mark.parametrize("nb", [1, 300])
+def test_route_on_device_logits(ctx, nb):
+    """rl = NULL: the routing of the logits a whole-layer call just computed on the device (the decode router at
+    one token, the chain router below 512 tokens), without a host copy; equal to the oracle's routing of those
+    logits and to the layer call's own top-8."""
+    from helpers import SEED, HostLayer, normed_hidden
+    lib = M.lib()
+    hl = HostLayer(SEED, 4)
+    M.register_layer(4, hl.blk, hl.router)
+    x, hn = normed_hidden(SEED, 60 + nb, nb)
+    M.check(lib.mmoe_moe(4, M.ptr(hn), nb, M.ptr(x), M.ORDER_BATCH), "moe")
+    rl = M.read("LOGITS", (nb, 256), np.float32)
+    top_layer = M.read("TOP", (nb, 8), np.int32)
+    nu, g = route_dev(nb)
+    assert nu > 0, lib.mmoe_last_error()
+    top, tw = O.topk(rl)
+    o = O.group(top, tw)
+    assert np.array_equal(g["top"], top) and np.array_equal(g["top"], top_layer)
+    assert np.array_equal(g["tw"].view(np.int32), tw.view(np.int32))
+    assert nu == o["nu"] and np.array_equal(g["ue"], o["ue"]) and np.array_equal(g["ustart"], o["ustart"])
+    assert np.array_equal(g["utok"], o["utok"]) and np.array_equal(g["uw"].view(np.int32), o["uw"].view(np.int32))
+    assert np.array_equal(g["tp"], o["tp"])
+    # another token count than the router call covered is refused
+    assert route_dev(nb + 1)[0] == -1 and b"last router call" in lib.mmoe_last_error()
+
+
+def test_route_device_logits_refused_after_mfma_router(ctx):
+    """The default router of a 1024-token batch leaves approximate logits for the experts that cannot reach the
+    top 8: rl = NULL is refused then, and accepted after the same call with the exact router option."""
+    from helpers import SEED, HostLayer, normed_hidden
+    lib = M.lib()
+    hl = HostLayer(SEED, 5)
+    M.register_layer(5, hl.blk, hl.router)
+    nb = 1024
+    x, hn = normed_hidden(SEED, 70, nb)
+    xa = x.copy()   # held: the library writes through the pointer
+    M.check(lib.mmoe_moe(5, M.ptr(hn), nb, M.ptr(xa), M.ORDER_BATCH), "moe")
+    assert route_dev(nb)[0] == -1
+    M.check(lib.mmoe_set_router_mode(1), "router mode")
+    try:
+        xb = x.copy()
+        M.check(lib.mmoe_moe(5, M.ptr(hn), nb, M.ptr(xb), M.ORDER_BATCH), "moe")
+        rl = M.read("LOGITS", (nb, 256), np.float32)
+        nu, g = route_dev(nb)
+        assert nu > 0 and np.array_equal(g["top"], O.topk(rl)[0])
+    finally:
+        M.check(lib.mmoe_set_router_mode(0), "router mode")
