@@ -987,7 +987,7 @@ int mmoe_route(const float *rl, int nb, int *top, float *tw, int *ue, int *ustar
     kl(k_fill_zero, (nch * MNE + 255) / 256, 256, 0, w.hist, nch * MNE);   // the per-chunk counts, for the next call
     if (rc) { (void)hipGetLastError(); return -1; }
     HC(hipGetLastError());
-    static Plan pl;
+    Plan pl;   // pageable: the copy completes before the synchronisation below returns
     HC(hipMemcpyAsync(&pl, w.plan, sizeof(Plan), hipMemcpyDeviceToHost, S.st));
     if (top) HC(hipMemcpyAsync(top, w.top, (size_t)P * 4, hipMemcpyDeviceToHost, S.st));
     if (tw) HC(hipMemcpyAsync(tw, w.tw, (size_t)P * 4, hipMemcpyDeviceToHost, S.st));
