@@ -127,6 +127,17 @@ __device__ __forceinline__ float wave_max(float v) {
     float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
     return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
+// sum over the wave in an arbitrary fixed order (used only where the order does not matter: bounds)
+__device__ __forceinline__ float wave_sumf(float v) {
+    v = v + __int_as_float(dpp<0xB1>(__float_as_int(v)));
+    v = v + __int_as_float(dpp<0x4E>(__float_as_int(v)));
+    v = v + __int_as_float(dpp<0x141>(__float_as_int(v)));
+    v = v + __int_as_float(dpp<0x140>(__float_as_int(v)));
+    int b = __float_as_int(v);
+    float r0 = __int_as_float(__builtin_amdgcn_readlane(b, 0)), r1 = __int_as_float(__builtin_amdgcn_readlane(b, 16));
+    float r2 = __int_as_float(__builtin_amdgcn_readlane(b, 32)), r3 = __int_as_float(__builtin_amdgcn_readlane(b, 48));
+    return (r0 + r1) + (r2 + r3);
+}
 __device__ __forceinline__ int wave_sum_i(int v) {
     v += dpp<0xB1>(v);
     v += dpp<0x4E>(v);
@@ -544,16 +555,20 @@ __global__ void __launch_bounds__(WAVES * 64) k_router_mfma(const uint16_t *__re
     }
 }
 
-// max over experts of sum_c |w_ec| (one block)
+// out[0] = max over experts of sum_c |w_ec|, out[1] = max over experts of sqrt(sum_c w_ec^2) (one block). Each
+// carries a 1.001 margin for its own float arithmetic (2048 rounded additions: relative error below 1.3e-4).
 __global__ void __launch_bounds__(256) k_router_l1max(const uint16_t *__restrict__ w, float *__restrict__ out) {
-    __shared__ float red[256];
+    __shared__ float red[2][256];
     int e = threadIdx.x;
-    float s = 0.0f;
-    for (int c = 0; c < MH; c++) s += fabsf(bf16f(w[(size_t)e * MH + c]));
-    red[e] = s;
+    float s = 0.0f, q = 0.0f;
+    for (int c = 0; c < MH; c++) { float v = bf16f(w[(size_t)e * MH + c]); s += fabsf(v); q += v * v; }
+    red[0][e] = s; red[1][e] = sqrtf(q);
     __syncthreads();
-    for (int o = 128; o > 0; o >>= 1) { if (e < o) red[e] = fmaxf(red[e], red[e + o]); __syncthreads(); }
-    if (e == 0) out[0] = red[0] * 1.001f;   // margin for the float sum's own rounding
+    for (int o = 128; o > 0; o >>= 1) {
+        if (e < o) { red[0][e] = fmaxf(red[0][e], red[0][e + o]); red[1][e] = fmaxf(red[1][e], red[1][e + o]); }
+        __syncthreads();
+    }
+    if (e == 0) { out[0] = red[0][0] * 1.001f; out[1] = red[1][0] * 1.001f; }
 }
 
 // =====================================================================================================
@@ -882,8 +897,10 @@ __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl
 }
 
 // Exact top-8 from the approximate logits of k_router_mfma, fused with the softmax/top-8 of the token.
-// |A - L| <= RG_ERRK * max|h_b| * max_e sum_c |w_ec| = err_b bounds the gap between the MFMA logit A and maple.c's
-// chain logit L. On the MFMA side a product of a column and an input part is exact and passes through at most
+// |A - L| <= RG_ERRK * sw = err_b bounds the gap between the MFMA logit A and maple.c's chain logit L, where sw
+// bounds sum_c |w_ec h_c| for every expert: the smaller of max|h_b| max_e sum_c |w_ec| (Hoelder) and
+// |h_b|_2 max_e |w_e|_2 (Cauchy-Schwarz, far smaller when a few coordinates of h dominate). Of the gap to
+// L: on the MFMA side a product of a column and an input part is exact and passes through at most
 // 192 roundings inside its chunk's accumulation (every one of the chunk's 3 x 64 products rounded on its own,
 // the worst case for the MFMA's internal sums), 8 for the chunk sums of its quarter, 3 for the quarter partials
 // and 1 for the bias; on the chain side through 256 FMAs and 3 hsum additions. Each rounding is at most 2^-24
@@ -942,6 +959,10 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
         for (int u = 0; u < 4; u++) { hc[((c + u) & 7) * RT_HP + ((c + u) >> 3)] = v4[u]; hm = fmaxf(hm, fabsf(v4[u])); }
     }
     hm = wave_max(hm);
+    float h2 = 0.0f;   // sum of squares of the row (fp32; below 2^-18 relative error, covered by the 1.001 below)
+#pragma unroll
+    for (int i = 0; i < 8; i++) h2 += (f[i].x * f[i].x + f[i].y * f[i].y) + (f[i].z * f[i].z + f[i].w * f[i].w);
+    h2 = wave_sumf(h2);
     // a8: the 8th largest approximate logit (8 rounds of the wave maximum, lowest index first)
     float rem[4] = {a[0], a[1], a[2], a[3]}, a8 = 0.0f;
     for (int k = 0; k < MTOPK; k++) {
@@ -954,7 +975,9 @@ __global__ void __launch_bounds__(256) k_refine_topk(const float *__restrict__ P
     // the bias add rounds relative to |logit + bias| on both sides (MFMA sum and exact chain): with a bias much
     // larger than sum|w h| that error is not covered by RG_ERRK's term, so add 2^-24 (|bias| + sum|w h|) per side
     float bm = wave_max(fmaxf(fmaxf(fabsf(bb[0]), fabsf(bb[1])), fmaxf(fabsf(bb[2]), fabsf(bb[3]))));
-    float sw = hm * w1max[0];
+    // sum_c |w_ec h_c| <= min(max|h| max_e sum_c |w_ec|, |h|_2 max_e |w_e|_2) (Hoelder, Cauchy-Schwarz): the second
+    // is far tighter when a few columns of h dominate (one outlier coordinate: max|h| ~ |h|_2 while sum |w| ~ 45 |w|_2)
+    float sw = fminf(hm * w1max[0], sqrtf(h2) * 1.001f * w1max[1]);
     float thr = a8 - 2.0f * (RG_ERRK * sw + (2.0f / 16777216.0f) * (bm + 1.01f * sw));
     int nc = 0;
     unsigned long long lanemask = (1ull << l) - 1ull;

@@ -927,7 +927,7 @@ static int set_router(int L, const uint16_t *router) {
     kl(k_router_chainmajor<8>, MNE * MH / 256, 256, 0, lw.router, lw.rc8);
     if (!lw.rf8) HC(hipMalloc(&lw.rf8, (size_t)MNE * MH * 4));
     kl(k_router_chain8_f32, MNE * MH / 256, 256, 0, lw.router, lw.rf8);
-    if (!lw.w1max) HC(hipMalloc(&lw.w1max, sizeof(float)));
+    if (!lw.w1max) HC(hipMalloc(&lw.w1max, 2 * sizeof(float)));
     kl(k_router_l1max, 1, 256, 0, lw.router, lw.w1max);
     HC(hipGetLastError());
     HC(hipStreamSynchronize(S.st));

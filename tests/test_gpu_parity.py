@@ -497,6 +497,18 @@ def test_flip_token_matches_oracle(layer0):
     M.lib().mmoe_set_decode_path(1)
 
 
+def bound_share(router, hn, ra, rx):
+    """largest |approximate - exact| logit as a share of the refinement's bound err_b = RG_ERRK x sw, sw the
+    smaller of max|h| max_e sum|w_e| and |h|_2 max_e |w_e|_2 (both bound sum_c |w_ec h_c|), as the kernel forms it"""
+    wf = (router.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    w1max = np.abs(wf).sum(1).max() * 1.001
+    w2max = np.sqrt((wf ** 2).sum(1)).max() * 1.001
+    h = hn.astype(np.float64)
+    sw = np.minimum(np.abs(h).max(1) * w1max, np.sqrt((h ** 2).sum(1)) * 1.001 * w2max)
+    err_b = 2.0 * 463.0 * 1.01 / 2 ** 24 * sw
+    return float((np.abs(ra.astype(np.float64) - rx) / err_b[:, None]).max())
+
+
 def test_zipf_mfma_router_matches_exact(zipf_layer):
     """Config 2 (2048 Zipf-routed tokens) with the MFMA router against the exact chain router: identical top-8,
     the picked experts' logits bit for bit, tw and x within the bar; and, with the MFMA router too, each token's
@@ -521,10 +533,7 @@ def test_zipf_mfma_router_matches_exact(zipf_layer):
         # how close the MFMA logits came to the refinement's rounding bound: every approximate logit's distance
         # from its exact chain value, as a share of the token's bound err_b (the kernel's candidate margin is
         # twice err_b, so a share below 1 leaves every non-candidate provably outside the exact top 8)
-        wf = (zipf_layer.router.astype(np.uint32) << 16).view(np.float32)
-        w1max = float(np.abs(wf).sum(1, dtype=np.float32).max())
-        err_b = 2.0 * 463.0 * 1.01 / 2 ** 24 * np.abs(hn).max(1) * w1max
-        share = float((np.abs(r0.astype(np.float64) - r1) / err_b[:, None]).max())
+        share = bound_share(zipf_layer.router, hn, r0, r1)
         print(f"  largest |approximate - exact| logit: {share:.3f} of the bound err_b")
         assert share < 1.0
         h = T // 2
@@ -614,3 +623,39 @@ def test_mfma_router_large_bias(zipf_layer):
     finally:
         M.check(lib.mmoe_set_router_mode(0), "router mode")
         M.check(lib.mmoe_set_bias(L, M.ptr(zipf_layer.bias)), "bias")
+
+
+def test_mfma_router_outlier_coordinate(zipf_layer):
+    """Hidden states with one dominant coordinate (x[c] 300 times the rest before the norm, as attention outputs
+    can make them): max|h| is then close to |h|_2, and the refinement's bound takes the Cauchy-Schwarz form
+    |h|_2 max_e |w_e|_2 instead of max|h| max_e sum|w_e| (about 30 times smaller here), so few experts need their
+    exact chains. The MFMA router must still give the exact router's top-8 and picked logits bit for bit, and
+    every approximate logit must lie within the bound."""
+    lib = M.lib()
+    L, T = zipf_layer.L, 1024
+    x, _ = normed_hidden(SEED, 4300, T)
+    rng = np.random.default_rng(11)
+    x[np.arange(T), rng.integers(0, M.H, T)] *= 300.0
+    hn = np.empty_like(x)
+    for b in range(T):
+        O.oracle().mo_rmsnorm(O._p(x[b]), None, M.H, O._p(hn[b]))
+    M.check(lib.mmoe_set_debug(0), "debug off")
+    try:
+        out = {}
+        for mode in (1, 0):
+            M.check(lib.mmoe_set_router_mode(mode), "router mode")
+            xg = run_gpu(L, hn, x, M.ORDER_BATCH)
+            out[mode] = (xg, M.read("TOP", (T, 8), np.int32), M.read("TW", (T, 8), np.float32), M.read("LOGITS", (T, 256), np.float32))
+        (x1, t1, w1, r1), (x0, t0, w0, r0) = out[1], out[0]
+        assert np.array_equal(t0, t1)
+        assert np.array_equal(np.take_along_axis(r0, t0, 1).view(np.int32), np.take_along_axis(r1, t1, 1).view(np.int32))
+        assert relmax(w0, w1) <= TOL and relmax(x0 - x, x1 - x) <= TOL
+        share = bound_share(zipf_layer.router, hn, r0, r1)
+        wf = (zipf_layer.router.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+        h = hn.astype(np.float64)
+        ratio = float(np.median((np.abs(h).max(1) * np.abs(wf).sum(1).max()) / (np.sqrt((h ** 2).sum(1)) * np.sqrt((wf ** 2).sum(1)).max())))
+        print(f"\n  outlier rows: largest |approximate - exact| {share:.3f} of err_b; Hoelder / Cauchy-Schwarz bound {ratio:.1f}x")
+        assert share < 1.0
+    finally:
+        M.check(lib.mmoe_set_router_mode(0), "router mode")
+        M.check(lib.mmoe_set_debug(1), "debug on")
