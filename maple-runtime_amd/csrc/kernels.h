@@ -337,6 +337,139 @@ __global__ void __launch_bounds__(256) k_router_chains(const float *__restrict__
     }
 }
 
+// k_router_chains for two tokens per block (the TK form: top-8 and quantisation in the last block): every thread
+// runs its chain for both tokens side by side from the same router words in registers, so a block reads its 32
+// experts' weights once for two tokens (half the blocks, half the L2 traffic) and the two FMA chains are
+// independent. Token pair q = (2q, 2q + 1) takes the NCH blocks with ids congruent to q mod 8 (one XCD). The
+// arithmetic per token is k_router_chains' exactly (the rmsnorm of each token as k_rmsnorm, the chains, the fold).
+template <int NCH, bool NORM>
+__global__ void __launch_bounds__(256) k_router_chains2(const float *__restrict__ in, int nb, const uint16_t *__restrict__ wc,
+                                                        const float *__restrict__ bias, float *__restrict__ rl,
+                                                        const uint16_t *__restrict__ post_ln, float *__restrict__ hn_out,
+                                                        RouteTail tail) {
+    constexpr int LEN = MH / NCH, HP = LEN + 4;
+    __shared__ __attribute__((aligned(16))) float hc[2][NCH * HP];
+    __shared__ double red[NORM ? 2 : 1][NORM ? 256 : 1];
+    __shared__ float kk[2];
+    int q = (int)(blockIdx.x / (8 * NCH)) * 8 + (int)(blockIdx.x % 8);
+    int y = (int)(blockIdx.x / 8) % NCH;
+    int b0 = 2 * q;
+    if (b0 >= nb) return;   // whole block
+    const bool two = b0 + 1 < nb;
+    int tid = threadIdx.x, j = tid % NCH, e = y * (256 / NCH) + tid / NCH;
+    float xv[2][8];
+    uint32_t pw[8];
+    if (NORM) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const float *xr = in + (size_t)(two ? b0 + t : b0) * MH;
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[t][i] = xr[tid + i * 256];
+        }
+        if (post_ln) {
+#pragma unroll
+            for (int i = 0; i < 8; i++) pw[i] = post_ln[tid + i * 256];
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) pw[i] = 0x3f80;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    const gptr_u4 *wp = (const gptr_u4 *)(wc + (size_t)e * MH + j * 8);
+    v4i wv[16];
+#pragma unroll
+    for (int qq = 0; qq < 16; qq++) wv[qq] = wp[qq * NCH];
+    float be = 0.0f;
+    if (bias && j == 0) be = bias[e];
+    if (NORM) {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            double sq = 0.0;
+#pragma unroll
+            for (int i = 0; i < 8; i++) sq += (double)xv[t][i] * (double)xv[t][i];
+            red[t][tid] = sq;
+        }
+        __syncthreads();
+        for (int o = 128; o > 0; o >>= 1) {
+            if (tid < o) { red[0][tid] += red[0][tid + o]; red[1][tid] += red[1][tid + o]; }
+            __syncthreads();
+        }
+        if (tid < 2) kk[tid] = 1.0f / sqrtf((float)(red[tid][0] / (double)MH) + 1e-6f);
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            float k = kk[t];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                int c = tid + i * 256;
+                float h = xv[t][i] * k * __uint_as_float(pw[i] << 16);
+                hc[t][(c % NCH) * HP + c / NCH] = h;
+                if (y == 0 && (t == 0 || two)) hn_out[(size_t)(b0 + t) * MH + c] = h;
+            }
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const float *xr = in + (size_t)(two ? b0 + t : b0) * MH;
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                int c = (tid + 256 * i) * 4;
+                float4 f = *(const float4 *)(xr + c);
+                hc[t][((c + 0) % NCH) * HP + (c + 0) / NCH] = f.x; hc[t][((c + 1) % NCH) * HP + (c + 1) / NCH] = f.y;
+                hc[t][((c + 2) % NCH) * HP + (c + 2) / NCH] = f.z; hc[t][((c + 3) % NCH) * HP + (c + 3) / NCH] = f.w;
+            }
+        }
+    }
+    __syncthreads();
+    const float *h0p = hc[0] + j * HP, *h1p = hc[1] + j * HP;
+    float acc0 = 0.0f, acc1 = 0.0f;
+#pragma unroll
+    for (int half = 0; half < LEN / 128; half++) {
+        if (half > 0) {
+#pragma unroll
+            for (int qq = 0; qq < 16; qq++) wv[qq] = wp[(half * 16 + qq) * NCH];
+        }
+#pragma unroll
+        for (int qq = 0; qq < 16; qq++) {
+            int o = half * 128 + qq * 8;
+            float4 a0 = *(const float4 *)(h0p + o), a1 = *(const float4 *)(h0p + o + 4);
+            float4 c0 = *(const float4 *)(h1p + o), c1 = *(const float4 *)(h1p + o + 4);
+            uint32_t w4[4] = {(uint32_t)wv[qq].x, (uint32_t)wv[qq].y, (uint32_t)wv[qq].z, (uint32_t)wv[qq].w};
+            float hv0[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w}, hv1[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                float wf = __uint_as_float((u & 1) ? (w4[u >> 1] & 0xffff0000u) : (w4[u >> 1] << 16));
+                acc0 = __builtin_fmaf(wf, hv0[u], acc0);
+                acc1 = __builtin_fmaf(wf, hv1[u], acc1);
+            }
+        }
+    }
+    float r0 = hsum8_lanes<NCH>(acc0), r1 = hsum8_lanes<NCH>(acc1);
+    if (j == 0) {
+        if (bias) { r0 = r0 + be; r1 = r1 + be; }
+        rl[(size_t)b0 * MNE + e] = r0;
+        if (two) rl[(size_t)(b0 + 1) * MNE + e] = r1;
+    }
+    // the pair's softmax/top-8 and quantisation in the last of its NCH blocks to arrive (as k_router_chains)
+    __shared__ int last;
+    __shared__ __attribute__((aligned(16))) float E[2][MNE];
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(&tail.cnt[q], 1) == NCH - 1;
+    __syncthreads();
+    if (!last) return;
+    int wvi = tid >> 6, l = tid & 63, t = wvi & 1, b = b0 + t;
+    if (t == 1 && !two) return;   // whole wave
+    if (wvi < 2) {
+        int ek = topk_wave(rl + (size_t)b * MNE, E[t], l, tail.top + b * MTOPK, tail.tw + b * MTOPK);
+        if (tail.hist && l < MTOPK) atomicAdd(&tail.hist[(b >> 6) * MNE + ek], 1);
+    } else {
+        const float *hr = (NORM ? hn_out : in) + (size_t)b * MH;
+        quant_wave<MH>(hr, l, tail.qx + (size_t)b * MH, tail.qsx + b, tail.qsumx + b);
+        if (tid == 128) tail.cnt[q] = 0;   // every block of the pair has counted
+    }
+}
+
 // Large batches (batch order, NCH = 8) as a register-tiled GEMM that keeps maple.c's chains: one thread
 // owns one chain j for a TPT-token x 8-expert tile (independent FMA chains in registers), a block
 // covers 4 TPT tokens x 64 experts x 8 chains. Operands sit in LDS chain-major, hs[j][m][token] and

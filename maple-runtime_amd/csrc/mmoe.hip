@@ -238,6 +238,9 @@ static bool S_router_exact = false;
 #ifndef ROUTER_TK
 #define ROUTER_TK 1
 #endif
+#ifndef ROUTER_TPB
+#define ROUTER_TPB 2   // tokens per block of the chain router with the top-8 tail (below 512 tokens)
+#endif
 static bool S_router_tk = ROUTER_TK;   // batches below 512: top-8 and quantisation in the router launch   // batches of 512+: MFMA logits + exact refinement (else the exact chain GEMM)
 // exact_only: never the approximate large-batch router (callers that hand the logits themselves to the host)
 // tk (batches below 512 tokens): the router launch also runs each token's softmax/top-8 (per-chunk counts into
@@ -253,6 +256,15 @@ static int stage_router_launch(Work &w, int L, const float *d_hn, int nb, int or
         RouteTail rt{w.top, w.tw, w.qx, w.qsx, w.qsumx, hist, w.rcnt};
         w.routed = true;
         unsigned g8 = (unsigned)((nb + 7) / 8 * 8);
+        if (ROUTER_TPB == 2) {   // two tokens per block
+            unsigned p8 = (unsigned)(((nb + 1) / 2 + 7) / 8 * 8);
+            if (order == MMOE_ORDER_STEP) {
+                if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains2<16, true>, p8 * 16, 256, 0, w.norm_x, nb, lw.rc16, lw.bias, w.rl, w.norm_w, hn_w, rt); });
+                return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains2<16, false>, p8 * 16, 256, 0, d_hn, nb, lw.rc16, lw.bias, w.rl, (const uint16_t *)nullptr, (float *)nullptr, rt); });
+            }
+            if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains2<8, true>, p8 * 8, 256, 0, w.norm_x, nb, lw.rc8, lw.bias, w.rl, w.norm_w, hn_w, rt); });
+            return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains2<8, false>, p8 * 8, 256, 0, d_hn, nb, lw.rc8, lw.bias, w.rl, (const uint16_t *)nullptr, (float *)nullptr, rt); });
+        }
         if (order == MMOE_ORDER_STEP) {
             if (w.norm_x) return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16, true, true>, g8 * 16, 256, 0, w.norm_x, nb, lw.rc16, lw.bias, w.rl, w.norm_w, hn_w, rt); });
             return launch(MMOE_K_ROUTER, [&] { kl(k_router_chains<16, false, true>, g8 * 16, 256, 0, d_hn, nb, lw.rc16, lw.bias, w.rl, nullptr, nullptr, rt); });
