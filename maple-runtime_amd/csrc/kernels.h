@@ -572,21 +572,25 @@ __global__ void __launch_bounds__(256) k_router_gemm(const float *__restrict__ h
 }
 
 // Large batches, approximate logits on the bf16 MFMA + exact refinement (k_refine_topk).
-// Each fp32 input h is split into three bf16 parts by truncation: h1 = the top 8 significant bits of h,
-// h2 = the top 8 of h - h1, h3 = the top 8 of what is left. Both subtractions are exact and the three parts
-// hold all 24 significant bits, so h = h1 + h2 + h3 exactly (for |h| above 2^-110; the MoE input is RMS-normed).
-// The router is bf16 already, so every product w * h_i is exact in fp32: only the fp32 accumulation of the MFMA
-// makes the approximate logit A differ from maple.c's chain result L, bounded in k_refine_topk.
+// Each fp32 input h is split into bf16 parts by truncation: h1 = the top 8 significant bits of h, h2 = the top 8
+// of h - h1 (both subtractions exact), h3 = what is left, |h3| < 2^-7 |h - h1| < 2^-14 |h|. The MFMA takes h1 and
+// h2 (RM_PARTS = 2, the default: h3's share of a logit, below 2^-14 sum |w h|, goes into the refinement's bound)
+// or all three (RM_PARTS = 3: h = h1 + h2 + h3 exactly, for |h| above 2^-110). The router is bf16 already, so
+// every product w * h_i is exact in fp32: besides h3, only the fp32 accumulation of the MFMA makes the
+// approximate logit A differ from maple.c's chain result L, bounded in k_refine_topk.
 //
-// Partial logits on v_mfma_f32_32x32x16_bf16: P[q][b][e] = sum over columns [512 q, 512 q + 512) and the three
-// parts of w[e][c] * h_i[b][c], accumulated per chunk of 64 columns from zero (the 192 products of a chunk, in
-// 16-column steps, each step over the three parts) and the 8 chunk sums added in order, which keeps the rounding
+// Partial logits on v_mfma_f32_32x32x16_bf16: P[q][b][e] = sum over columns [512 q, 512 q + 512) and the
+// parts of w[e][c] * h_i[b][c], accumulated per chunk of 64 columns from zero (64 RM_PARTS products a chunk, in
+// 16-column steps, each step over the parts) and the 8 chunk sums added in order, which keeps the rounding
 // bound of k_refine_topk small. A block of WAVES waves takes 32 tokens x 32 WAVES EW experts x one column
 // quarter q (grid.z); wave w owns experts w * 32 EW .. +32 EW as EW fragments of 32 against the block's 32
 // tokens, so each input chunk is split into its parts once per block. Columns advance in chunks of 64: the
 // router chunk (bf16) and the input chunk (fp32) are read with coalesced 16-byte loads into registers two
-// chunks ahead, then stored to LDS (the input as its three bf16 parts; rows padded to 72 bf16).
+// chunks ahead, then stored to LDS (the input as its bf16 parts; rows padded to 72 bf16).
 #define RM_KC 64
+#ifndef RM_PARTS
+#define RM_PARTS 2   // bf16 parts of each input value on the MFMA (3: the third, below 2^-14 |h|, too)
+#endif
 #define RM_PF 2   // router chunks loaded ahead (registers); 4 and 8 measured slower
 #define RM_LR 72
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -616,7 +620,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_router_mfma(const uint16_t *__re
     // later, after every wave has passed the barrier of the chunk in between)
     constexpr int NB = WAVES == 8 ? 2 : 1;
     __shared__ __attribute__((aligned(16))) uint16_t ws_[NB][ER * RM_LR];
-    __shared__ __attribute__((aligned(16))) uint16_t hsl_[NB][3][32 * RM_LR];
+    __shared__ __attribute__((aligned(16))) uint16_t hsl_[NB][RM_PARTS][32 * RM_LR];
     int tid = threadIdx.x, wv = tid >> 6, l = tid & 63, r = l & 31, kg = l >> 5;
     int e0 = blockIdx.y * ER, t0 = blockIdx.x * 32, kq = blockIdx.z * (MH / 4);
     int wrow = tid >> 3, wpc = tid & 7, hrow = tid >> 4, hq = tid & 15;
@@ -647,7 +651,8 @@ __global__ void __launch_bounds__(WAVES * 64) k_router_mfma(const uint16_t *__re
             int o = (hrow + (NT / 16) * i) * RM_LR + hq * 4;
             uint2 p1, p2, p3;
             split3(rh[q][i], p1, p2, p3);
-            *(uint2 *)(&hsl[0][o]) = p1; *(uint2 *)(&hsl[1][o]) = p2; *(uint2 *)(&hsl[2][o]) = p3;
+            *(uint2 *)(&hsl[0][o]) = p1; *(uint2 *)(&hsl[1][o]) = p2;
+            if (RM_PARTS == 3) *(uint2 *)(&hsl[RM_PARTS - 1][o]) = p3;
         }
         __syncthreads();
         if (ck + RM_PF < NCK) RMW_LOAD(q, (ck + RM_PF) * RM_KC);
@@ -662,7 +667,7 @@ __global__ void __launch_bounds__(WAVES * 64) k_router_mfma(const uint16_t *__re
 #pragma unroll
             for (int f = 0; f < EW; f++) av[f] = *(const bf16x8 *)(&ws[(wv * 32 * EW + f * 32 + r) * RM_LR + kk + kg * 8]);
 #pragma unroll
-            for (int sp = 0; sp < 3; sp++) {
+            for (int sp = 0; sp < RM_PARTS; sp++) {
                 bf16x8 bv = *(const bf16x8 *)(&hsl[sp][r * RM_LR + kk + kg * 8]);
 #pragma unroll
                 for (int f = 0; f < EW; f++) cacc[f] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[f], bv, cacc[f], 0, 0, 0);
@@ -1033,17 +1038,22 @@ __global__ void __launch_bounds__(256) k_topk_quant(const float *__restrict__ rl
 // |A - L| <= RG_ERRK * sw = err_b bounds the gap between the MFMA logit A and maple.c's chain logit L, where sw
 // bounds sum_c |w_ec h_c| for every expert: the smaller of max|h_b| max_e sum_c |w_ec| (Hoelder) and
 // |h_b|_2 max_e |w_e|_2 (Cauchy-Schwarz, far smaller when a few coordinates of h dominate). Of the gap to
-// L: on the MFMA side a product of a column and an input part is exact and passes through at most
-// 192 roundings inside its chunk's accumulation (every one of the chunk's 3 x 64 products rounded on its own,
-// the worst case for the MFMA's internal sums), 8 for the chunk sums of its quarter, 3 for the quarter partials
-// and 1 for the bias; on the chain side through 256 FMAs and 3 hsum additions. Each rounding is at most 2^-24
-// times the running magnitude (at most sum |w h|): 463 x 2^-24 x sum |w h| in all; times 1.01 for the margin of
-// w1max's own float sum and the parts' sum of magnitudes, and 2 for safety. Every expert with A >= a8 - 2 err_b (a8 = the 8th largest A) is a candidate and gets its exact chain
+// L: on the MFMA side a product of a column and an input part is exact and passes through at most 64 RM_PARTS
+// roundings inside its chunk's accumulation (every product of the chunk rounded on its own, the worst case for the
+// MFMA's internal sums), 8 for the chunk sums of its quarter, 3 for the quarter partials and 1 for the bias; on
+// the chain side through 256 FMAs and 3 hsum additions. Each rounding is at most 2^-24 times the running
+// magnitude (at most sum |w h|): (64 RM_PARTS + 271) x 2^-24 x sum |w h|, plus 1024 x 2^-24 x sum |w h| for the
+// left-out part h3 when RM_PARTS = 2; times 1.01 for the parts' sum of magnitudes, and 2 for safety (which also
+// covers an accumulator that truncates: 2^-23 per operation). Every expert with A >= a8 - 2 err_b (a8 = the 8th largest A) is a candidate and gets its exact chain
 // logit in maple.c's batch order; no other expert can reach the top 8 of the exact logits, because the 8
 // experts with A >= a8 have L >= a8 - err_b while the rest have L < a8 - err_b. The softmax/top-8 then runs on
 // the row of exact (candidates) and approximate (the rest) logits, so the picks and their order are maple.c's;
 // p, and so tw, differ only through the softmax sum's approximate small terms.
+#if RM_PARTS == 3
 #define RG_ERRK (2.0f * 463.0f * 1.01f / 16777216.0f)
+#else
+#define RG_ERRK (2.0f * (399.0f + 1024.0f) * 1.01f / 16777216.0f)
+#endif
 #define RT_HP 260    // LDS floats per chain of the staged input (256 + 4 against bank conflicts)
 // One wave per token, 4 tokens per block (grid = (ceil(nb / 4), 2)); the blocks of grid row 1 quantise the
 // tokens instead (in the same wave they would raise the register count of the refinement). The input row sits in LDS chain-major
